@@ -1,0 +1,210 @@
+/*
+ * lfm_hip.h -- C ABI of the MI355X (gfx950) LFM2.5-8B-A1B Q6_K token loop.
+ *
+ * This is the drop-in boundary that replaces the reference's Vulkan engine
+ * (Amidwestnoob/lfm2-w9100-rust: engine/src/gpu_lfm.rs + gpu_lfm/resident_graph.rs
+ * over engine/src/ops.rs, engine/src/kernels*.rs and engine/src/vulkan*.rs).
+ * Callers that keep the reference's GGUF reader, tokenizer and CLI/JSONL code
+ * bind these symbols (cgo-style plain pointers and sizes; no C++ or torch types).
+ *
+ * Conventions
+ *   - Every call returns an int status (LFM_OK == 0); on failure a message is
+ *     available from lfm_last_error() (thread-local, valid until the next call
+ *     on the same thread).  No call aborts the process.
+ *   - An engine is single-threaded and non-reentrant, like the reference's
+ *     GpuEngine (engine/src/ops.rs:17-47 uses Cell/RefCell): one engine per
+ *     thread, calls serialized by the caller.  Every engine call returns after
+ *     its GPU work has completed.
+ *   - Host buffers stay owned by the caller; the library copies in and writes
+ *     results into caller buffers of stated capacity.
+ *   - Numerical contract (engine/src/gpu_lfm.rs:8-11): signed int8 Q6_K scales,
+ *     KV cache rounded to binary16 (stored as binary16), NEOX RoPE,
+ *     kv head = h * kv / heads, MoE top-k with a 6.103515625e-5 weight-sum clamp,
+ *     greedy argmax with ties to the lowest id and NaN never winning.
+ */
+#ifndef LFM_HIP_H
+#define LFM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+#define LFM_OK 0
+#define LFM_EINVAL 1    /* invalid argument or failed precondition (anyhow::ensure!) */
+#define LFM_ERANGE 2    /* context / token id / capacity out of range            */
+#define LFM_EDEVICE 3   /* HIP runtime or device failure                          */
+#define LFM_ESTATE 4    /* call not valid in the engine's current state           */
+#define LFM_EINTERNAL 5 /* library bug                                            */
+
+#define LFM_GGML_TYPE_F32 0u
+#define LFM_GGML_TYPE_Q6_K 14u
+#define LFM_MAX_LAYERS 64
+#define LFM_MAX_CTX 4096 /* engine/src/ops.rs:488-491 */
+#define LFM_MAX_TOKEN_BATCH 64 /* forward_token batch, resident_graph.rs:95-98 */
+
+/* Model hyper-parameters; mirrors Hyperparams (engine/src/lfm.rs:31-49) and the
+ * metadata keys read by load_hyperparams (engine/src/lfm.rs:102-145). */
+typedef struct lfm_hparams {
+    uint32_t dim;        /* lfm2moe.embedding_length (multiple of 256)          */
+    uint32_t heads;      /* lfm2moe.attention.head_count                        */
+    uint32_t head_dim;   /* 64                                                  */
+    uint32_t n_layers;   /* lfm2moe.block_count                                 */
+    uint32_t kv_heads[LFM_MAX_LAYERS]; /* lfm2moe.attention.head_count_kv[]: 0 = conv */
+    uint32_t vocab;      /* lfm2moe.vocab_size                                  */
+    float eps;           /* lfm2moe.attention.layer_norm_rms_epsilon            */
+    float rope_theta;    /* lfm2moe.rope.freq_base                              */
+    uint32_t eos;        /* tokenizer.ggml.eos_token_id                         */
+    uint32_t n_expert;   /* lfm2moe.expert_count (4..64)                        */
+    uint32_t n_used;     /* lfm2moe.expert_used_count (4)                       */
+    uint32_t expert_ff;  /* lfm2moe.expert_feed_forward_length (multiple of 256) */
+    uint32_t n_ff;       /* lfm2moe.feed_forward_length (multiple of 256)       */
+    uint32_t dense_lead; /* lfm2moe.leading_dense_block_count                   */
+    uint32_t conv_l_cache; /* lfm2moe.shortconv.l_cache (3)                     */
+} lfm_hparams;
+
+typedef struct lfm_engine lfm_engine;
+
+/* ---- library ------------------------------------------------------------- */
+const char *lfm_last_error(void);
+const char *lfm_version(void);
+/* Number of visible HIP devices (0 when none). */
+int lfm_device_count(int *count);
+
+/* ---- engine lifecycle ---------------------------------------------------- */
+/* GpuEngine::load (gpu_lfm.rs:51-115) is split into create / upload / finalize
+ * so that the caller's GGUF reader (model_file.rs:100-109) streams tensors in. */
+int lfm_engine_create(const lfm_hparams *hp, int device, lfm_engine **out);
+/* Copies one tensor (raw GGUF bytes, ne[0] fastest) to device memory.  Names
+ * and shapes are the reference's (gpu_lfm.rs:71-97, lfm.rs:330-669).  Q6_K
+ * tensors are re-laid out on upload; F32 tensors are copied as-is. */
+int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_t ggml_type,
+                             const uint64_t *ne, uint32_t n_dims, const void *host,
+                             size_t nbytes);
+/* Verifies every tensor is present, allocates the resident state and captures
+ * the decode graph.  Must precede any forward call. */
+int lfm_engine_finalize(lfm_engine *e);
+/* GpuEngine::set_ctx (gpu_lfm.rs:117): context capacity, 1..LFM_MAX_CTX.
+ * Must be called before lfm_engine_finalize (default 4096). */
+int lfm_engine_set_ctx(lfm_engine *e, uint32_t ctx);
+void lfm_engine_destroy(lfm_engine *e);
+int lfm_engine_hparams(const lfm_engine *e, lfm_hparams *out);
+
+/* ---- forward ------------------------------------------------------------- */
+/* GpuEngine::forward (gpu_lfm.rs:243): process ids[0..n) at positions
+ * start_pos.., return the last token's logits (vocab floats). */
+int lfm_forward_logits(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start_pos,
+                       float *logits, size_t logits_cap);
+/* GpuEngine::forward_token (resident_graph.rs:90-101): n in 1..64; greedy next
+ * id computed on the GPU; *max_logit receives the winning logit. */
+int lfm_forward_token(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start_pos,
+                      uint32_t *next, float *max_logit);
+/* The greedy loop of main.rs:182-189 / api_stream.rs:67-77 resident on the
+ * device: feed `first_token` at `start_pos`, then each argmax back in, for up
+ * to `steps` tokens; stops after emitting nothing once the argmax equals `eos`
+ * (eos >= vocab never stops).  out_tokens receives the argmax ids in order,
+ * *n_out their count (the eos id itself is not stored). */
+int lfm_decode_run(lfm_engine *e, uint32_t first_token, uint32_t start_pos, uint32_t steps,
+                   uint32_t eos, uint32_t *out_tokens, uint32_t *n_out);
+/* GpuEngine::reset_session (resident_graph.rs:105-115): zero conv state. */
+int lfm_reset_session(lfm_engine *e);
+/* snapshot_resident_cache (resident_graph.rs:572-602): same byte format
+ * (attention layers: K then V, head_dim*kv*valid f32 in [t][kh][d] order;
+ * conv layers: dim*2 f32 in [ch][slot] order). */
+int lfm_snapshot_bytes(const lfm_engine *e, uint32_t valid_tokens, size_t *nbytes);
+int lfm_snapshot_cache(lfm_engine *e, uint32_t valid_tokens, uint8_t *buf, size_t cap,
+                       size_t *written);
+/* restore_session (resident_graph.rs:119-158): exact-size input required. */
+int lfm_restore_session(lfm_engine *e, uint32_t valid_tokens, const uint8_t *buf, size_t len);
+/* snapshot_resident_logits (resident_graph.rs:561-568): last full logits. */
+int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap);
+/* gpu.dispatch_count(): kernels launched by this engine so far. */
+uint64_t lfm_dispatch_count(const lfm_engine *e);
+/* device_name (gpu_lfm.rs:126-128). */
+int lfm_device_name(const lfm_engine *e, char *buf, size_t cap);
+
+/* ---- layer-level entry points (parity tests) ------------------------------
+ * Run one layer's mixer half (RMSNorm -> conv or attention -> residual) or
+ * FFN half (RMSNorm -> dense SwiGLU or MoE -> residual) of the decode step on
+ * a host residual vector x[dim] in place, at position `pos`, with the same
+ * kernels the decode graph replays (lfm.rs:330-670 one token at a time).
+ * lfm_engine_last_route returns the ids/weights the last MoE kernel chose. */
+int lfm_engine_run_mixer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos);
+int lfm_engine_run_ffn(lfm_engine *e, uint32_t layer, float *x);
+int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *weights, uint32_t cap);
+
+/* ---- device buffers (op-level tests and measurement) --------------------- */
+int lfm_dev_alloc(size_t nbytes, void **ptr);
+int lfm_dev_free(void *ptr);
+int lfm_memcpy_htod(void *dst, const void *src, size_t nbytes);
+int lfm_memcpy_dtoh(void *dst, const void *src, size_t nbytes);
+int lfm_dev_synchronize(void);
+
+/* ---- Q6_K operator API (GpuOps::q6k_matmul, engine/src/ops.rs:340-374) ----
+ * Q6_K device layout: a tensor of `rows` rows of in_dim/256 superblocks is
+ * stored as four planes (ql 128 B, qh 64 B, scales 16 B, d 2 B per block, 210
+ * B per block in total, the same size as GGUF).  lfm_q6k_pack converts raw
+ * GGUF bytes (host) into that layout (host). */
+size_t lfm_q6k_nbytes(uint64_t rows, uint64_t in_dim);
+int lfm_q6k_pack(const void *raw, uint64_t rows, uint64_t in_dim, void *packed);
+int lfm_q6k_unpack(const void *packed, uint64_t rows, uint64_t in_dim, void *raw);
+/* Bit-exact dequantization of a packed device tensor to f32 (device). */
+int lfm_q6k_dequant(const void *packed_dev, uint64_t rows, uint64_t in_dim, float *out_dev,
+                    void *stream);
+/* y[r] = sum_k W[r,k] * x[k] on device buffers (q6k_matvec, q6k.rs:167-183). */
+int lfm_q6k_matvec(const void *packed_dev, uint64_t rows, uint64_t in_dim, const float *x_dev,
+                   float *y_dev, void *stream);
+/* Launch the matvec `iters` times, rotating over `ncopies` packed weight
+ * copies laid out back to back from packed_dev, and return the mean ms per
+ * launch measured with HIP events on the launch stream (rotation defeats the
+ * 256 MB Infinity Cache when ncopies * size exceeds it). */
+int lfm_q6k_matvec_time(const void *packed_dev, uint32_t ncopies, uint64_t rows, uint64_t in_dim,
+                        const float *x_dev, float *y_dev, uint32_t iters, float *ms_per_launch);
+
+/* ---- argmax (engine/src/kernels/persistent.rs:11-53 semantics) ------------ */
+int lfm_argmax(const float *v_dev, uint32_t n, uint32_t *index, float *value);
+
+/* ---- synthetic model (seeded; identical bytes on every host) -------------- */
+typedef struct lfm_tensor_desc {
+    char name[96];
+    uint32_t ggml_type;
+    uint32_t n_dims;
+    uint64_t ne[4];
+    uint32_t kind;   /* 0 = Q6_K weight, 1 = norm 1+N(0,s), 2 = N(0,s), 3 = zeros */
+    float sigma;
+} lfm_tensor_desc;
+typedef struct lfm_synth_opts {
+    uint64_t seed;
+    float d_sigma;      /* Q6_K super-block scale d ~ N(0, d_sigma) as binary16  */
+    float norm_sigma;   /* norm weights ~ 1 + N(0, norm_sigma)                    */
+    float router_sigma; /* ffn_gate_inp ~ N(0, router_sigma)                      */
+    float bias_sigma;   /* exp_probs_b ~ N(0, bias_sigma); 0 => zeros            */
+    float conv_sigma;   /* shortconv.conv ~ N(0, conv_sigma)                      */
+} lfm_synth_opts;
+void lfm_synth_default_opts(lfm_synth_opts *o);
+int lfm_model_tensor_count(const lfm_hparams *hp);
+int lfm_model_tensor_desc(const lfm_hparams *hp, const lfm_synth_opts *o, int index,
+                          lfm_tensor_desc *out);
+size_t lfm_tensor_nbytes(const lfm_tensor_desc *d);
+/* Fill `out` (lfm_tensor_nbytes bytes) with the tensor's seeded content. */
+int lfm_synth_tensor(const lfm_synth_opts *o, const lfm_tensor_desc *d, void *out, size_t cap,
+                     int threads);
+/* Uniform random Q6_K blocks / normal f32 values (seeded streams). */
+int lfm_synth_q6k_blocks(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
+                         uint8_t *out, int threads);
+int lfm_synth_normal_f32(uint64_t seed, const char *stream, uint64_t n, float mean,
+                         float sigma, float *out, int threads);
+/* Generate every tensor of the model and upload it (convenience for benches). */
+int lfm_engine_load_synthetic(lfm_engine *e, const lfm_synth_opts *o, int threads);
+
+/* ---- binary16 helpers (IEEE RNE) ------------------------------------------ */
+uint16_t lfm_f32_to_f16(float f);
+float lfm_f16_to_f32(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,1156 @@
+// engine.cpp -- host runtime of the MI355X LFM2 Q6_K token loop behind the C
+// ABI in include/lfm_hip.h.
+//
+// It replaces the reference's GpuEngine + resident graph + Vulkan runtime
+// (Amidwestnoob/lfm2-w9100-rust engine/src/gpu_lfm.rs:23-245,
+// engine/src/gpu_lfm/resident_graph.rs:4-602, engine/src/vulkan*.rs) with:
+//   * one HIP stream per engine (default priority), all work in stream order;
+//   * kernels from a gfx950 code object launched with hipModuleLaunchKernel;
+//   * two captured hipGraphs: the layer stack + prompt advance (prefill by
+//     decode steps) and the layer stack + head/argmax/feedback (decode step),
+//     both reading token and position from device memory, so a decode run is
+//     graph replays with no host round trip per token.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/lfm_hip.h"
+#include "kargs.h"
+
+// ------------------------------------------------------------------ errors
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPCHK(call)                                                                          \
+    do {                                                                                      \
+        hipError_t _e = (call);                                                               \
+        if (_e != hipSuccess)                                                                 \
+            return fail(LFM_EDEVICE, "%s failed: %s (%s:%d)", #call, hipGetErrorString(_e),   \
+                        __FILE__, __LINE__);                                                  \
+    } while (0)
+
+#define RC(call)                                                                              \
+    do {                                                                                      \
+        int _rc = (call);                                                                     \
+        if (_rc != LFM_OK)                                                                    \
+            return _rc;                                                                       \
+    } while (0)
+
+extern "C" const char *lfm_last_error(void) { return g_err.c_str(); }
+extern "C" const char *lfm_version(void) { return "lfm2-mi355x 0.1 (gfx950)"; }
+
+extern "C" int lfm_device_count(int *count)
+{
+    if (!count)
+        return fail(LFM_EINVAL, "count is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = e == hipSuccess ? n : 0;
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ kernels
+struct Kernels {
+    hipModule_t mod = nullptr;
+    hipFunction_t matvec, conv, qkv, attn, router, gateup, moe_down, head, advance, dequant,
+        argmax;
+};
+
+static std::mutex g_kmu;
+static std::unordered_map<int, Kernels *> g_kernels;
+
+static std::string code_object_path()
+{
+    const char *env = getenv("LFM_KERNELS");
+    if (env && *env)
+        return env;
+    Dl_info info;
+    if (dladdr((void *)&lfm_version, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t slash = p.rfind('/');
+        std::string dir = slash == std::string::npos ? "." : p.substr(0, slash);
+        return dir + "/lfm_kernels.hsaco";
+    }
+    return "lfm_kernels.hsaco";
+}
+
+// Loads the code object on the current device (once per device).
+static int get_kernels(Kernels **out)
+{
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_kmu);
+    auto it = g_kernels.find(dev);
+    if (it != g_kernels.end()) {
+        *out = it->second;
+        return LFM_OK;
+    }
+    Kernels *k = new Kernels();
+    std::string path = code_object_path();
+    hipError_t e = hipModuleLoad(&k->mod, path.c_str());
+    if (e != hipSuccess) {
+        delete k;
+        return fail(LFM_EDEVICE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    struct {
+        hipFunction_t *f;
+        const char *name;
+    } fns[] = {{&k->matvec, "k_q6_matvec"}, {&k->conv, "k_conv_inproj"}, {&k->qkv, "k_qkv"},
+               {&k->attn, "k_attn"},        {&k->router, "k_router"},    {&k->gateup, "k_gateup"},
+               {&k->moe_down, "k_moe_down"}, {&k->head, "k_head"},       {&k->advance, "k_advance"},
+               {&k->dequant, "k_q6_dequant"}, {&k->argmax, "k_argmax"}};
+    for (auto &f : fns) {
+        e = hipModuleGetFunction(f.f, k->mod, f.name);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(k->mod);
+            delete k;
+            return fail(LFM_EDEVICE, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
+        }
+    }
+    g_kernels[dev] = k;
+    *out = k;
+    return LFM_OK;
+}
+
+template <typename A>
+static int launch(hipFunction_t f, dim3 grid, uint32_t smem, hipStream_t s, const A &args)
+{
+    void *params[] = {(void *)&args};
+    HIPCHK(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, 256, 1, 1, smem, s, params, nullptr));
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ Q6_K layout
+extern "C" size_t lfm_q6k_nbytes(uint64_t rows, uint64_t in_dim) { return rows * (in_dim / 256) * 210; }
+
+// GGUF block_q6_K (ql[128] qh[64] scales[16] d[2]) -> four planes (kargs.h).
+static void pack_blocks(const uint8_t *raw, uint64_t nblk, uint8_t *out)
+{
+    uint8_t *ql = out, *qh = out + nblk * 128, *sc = out + nblk * 192, *dd = out + nblk * 208;
+    for (uint64_t b = 0; b < nblk; ++b) {
+        const uint8_t *r = raw + b * 210;
+        for (int c = 0; c < 8; ++c) {
+            const int h = c >> 2, l0 = (c & 3) * 8;
+            memcpy(ql + b * 128 + c * 16, r + h * 64 + l0, 8);
+            memcpy(ql + b * 128 + c * 16 + 8, r + h * 64 + 32 + l0, 8);
+        }
+        memcpy(qh + b * 64, r + 128, 64);
+        for (int p = 0; p < 4; ++p)
+            for (int s = 0; s < 4; ++s)
+                sc[b * 16 + p * 4 + s] = r[192 + (p >> 1) * 8 + (p & 1) + 2 * s];
+        dd[b * 2] = r[208];
+        dd[b * 2 + 1] = r[209];
+    }
+}
+
+static void unpack_blocks(const uint8_t *packed, uint64_t nblk, uint8_t *raw)
+{
+    const uint8_t *ql = packed, *qh = packed + nblk * 128, *sc = packed + nblk * 192,
+                  *dd = packed + nblk * 208;
+    for (uint64_t b = 0; b < nblk; ++b) {
+        uint8_t *r = raw + b * 210;
+        for (int c = 0; c < 8; ++c) {
+            const int h = c >> 2, l0 = (c & 3) * 8;
+            memcpy(r + h * 64 + l0, ql + b * 128 + c * 16, 8);
+            memcpy(r + h * 64 + 32 + l0, ql + b * 128 + c * 16 + 8, 8);
+        }
+        memcpy(r + 128, qh + b * 64, 64);
+        for (int p = 0; p < 4; ++p)
+            for (int s = 0; s < 4; ++s)
+                r[192 + (p >> 1) * 8 + (p & 1) + 2 * s] = sc[b * 16 + p * 4 + s];
+        r[208] = dd[b * 2];
+        r[209] = dd[b * 2 + 1];
+    }
+}
+
+extern "C" int lfm_q6k_pack(const void *raw, uint64_t rows, uint64_t in_dim, void *packed)
+{
+    if (!raw || !packed || in_dim == 0 || in_dim % 256)
+        return fail(LFM_EINVAL, "lfm_q6k_pack: in_dim must be a positive multiple of 256");
+    pack_blocks((const uint8_t *)raw, rows * (in_dim / 256), (uint8_t *)packed);
+    return LFM_OK;
+}
+
+extern "C" int lfm_q6k_unpack(const void *packed, uint64_t rows, uint64_t in_dim, void *raw)
+{
+    if (!raw || !packed || in_dim == 0 || in_dim % 256)
+        return fail(LFM_EINVAL, "lfm_q6k_unpack: in_dim must be a positive multiple of 256");
+    unpack_blocks((const uint8_t *)packed, rows * (in_dim / 256), (uint8_t *)raw);
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ device buffers
+extern "C" int lfm_dev_alloc(size_t nbytes, void **ptr)
+{
+    if (!ptr)
+        return fail(LFM_EINVAL, "ptr is null");
+    HIPCHK(hipMalloc(ptr, nbytes ? nbytes : 1));
+    return LFM_OK;
+}
+extern "C" int lfm_dev_free(void *ptr)
+{
+    HIPCHK(hipFree(ptr));
+    return LFM_OK;
+}
+extern "C" int lfm_memcpy_htod(void *dst, const void *src, size_t n)
+{
+    HIPCHK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+    return LFM_OK;
+}
+extern "C" int lfm_memcpy_dtoh(void *dst, const void *src, size_t n)
+{
+    HIPCHK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+    return LFM_OK;
+}
+extern "C" int lfm_dev_synchronize(void)
+{
+    HIPCHK(hipDeviceSynchronize());
+    return LFM_OK;
+}
+
+// Matvec launch geometry: ksplit waves per row (1, 2 or 4), nbw blocks per wave.
+static int matvec_geometry(uint32_t nb, uint32_t *ks, uint32_t *nbw)
+{
+    if (nb == 0 || nb > 32)
+        return fail(LFM_EINVAL, "Q6_K matvec supports 256..8192 inputs (got %u blocks)", nb);
+    uint32_t k = (nb + 7) / 8;
+    if (k == 3)
+        k = 4;
+    *ks = k;
+    *nbw = (nb + k - 1) / k;
+    return LFM_OK;
+}
+
+static uint32_t matvec_grid(uint32_t rows, uint32_t ks)
+{
+    const uint32_t rpi = 4 / ks;
+    const uint32_t groups = (rows + rpi - 1) / rpi;
+    return std::max(1u, std::min(groups, 65535u));
+}
+
+static Q6T q6view(const void *dev, uint64_t rows, uint64_t in_dim)
+{
+    Q6T t;
+    t.base = (const uint8_t *)dev;
+    t.rows = (uint32_t)rows;
+    t.nb = (uint32_t)(in_dim / 256);
+    return t;
+}
+
+static int check_q6_args(const void *packed, uint64_t rows, uint64_t in_dim)
+{
+    if (!packed || rows == 0 || rows > 0xFFFFFFFFull || in_dim == 0 || in_dim % 256)
+        return fail(LFM_EINVAL, "Q6_K tensor: rows must be 1..2^32-1, in_dim a multiple of 256");
+    return LFM_OK;
+}
+
+extern "C" int lfm_q6k_dequant(const void *packed, uint64_t rows, uint64_t in_dim, float *out,
+                               void *stream)
+{
+    RC(check_q6_args(packed, rows, in_dim));
+    Kernels *K;
+    RC(get_kernels(&K));
+    DequantArgs a;
+    a.w = q6view(packed, rows, in_dim);
+    a.out = out;
+    a.in_dim = (uint32_t)in_dim;
+    const uint64_t units = rows * (in_dim / 256) * 8;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((units + 255) / 256, 65535);
+    RC(launch(K->dequant, dim3(grid), 0, (hipStream_t)stream, a));
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    return LFM_OK;
+}
+
+static int matvec_args(const void *packed, uint64_t rows, uint64_t in_dim, const float *x, float *y,
+                       MatvecArgs *a, uint32_t *grid)
+{
+    RC(check_q6_args(packed, rows, in_dim));
+    memset(a, 0, sizeof(*a));
+    a->w = q6view(packed, rows, in_dim);
+    a->src.x = x;
+    a->y = y;
+    a->in_dim = (uint32_t)in_dim;
+    a->mode = 0;
+    RC(matvec_geometry(a->w.nb, &a->ksplit, &a->nbw));
+    *grid = matvec_grid(a->w.rows, a->ksplit);
+    return LFM_OK;
+}
+
+extern "C" int lfm_q6k_matvec(const void *packed, uint64_t rows, uint64_t in_dim, const float *x,
+                              float *y, void *stream)
+{
+    MatvecArgs a;
+    uint32_t grid;
+    RC(matvec_args(packed, rows, in_dim, x, y, &a, &grid));
+    Kernels *K;
+    RC(get_kernels(&K));
+    RC(launch(K->matvec, dim3(grid), (a.in_dim + 16) * 4, (hipStream_t)stream, a));
+    HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+    return LFM_OK;
+}
+
+extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_t rows,
+                                   uint64_t in_dim, const float *x, float *y, uint32_t iters,
+                                   float *ms)
+{
+    if (ncopies == 0 || iters == 0 || !ms)
+        return fail(LFM_EINVAL, "ncopies, iters must be positive and ms non-null");
+    MatvecArgs a;
+    uint32_t grid;
+    RC(matvec_args(packed, rows, in_dim, x, y, &a, &grid));
+    Kernels *K;
+    RC(get_kernels(&K));
+    hipStream_t s;
+    HIPCHK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    const size_t sz = lfm_q6k_nbytes(rows, in_dim);
+    const uint32_t smem = (a.in_dim + 16) * 4;
+    for (uint32_t i = 0; i < std::min(iters, ncopies); ++i) { // warm the code path
+        a.w.base = (const uint8_t *)packed + (size_t)(i % ncopies) * sz;
+        RC(launch(K->matvec, dim3(grid), smem, s, a));
+    }
+    HIPCHK(hipEventRecord(e0, s));
+    for (uint32_t i = 0; i < iters; ++i) {
+        a.w.base = (const uint8_t *)packed + (size_t)(i % ncopies) * sz;
+        RC(launch(K->matvec, dim3(grid), smem, s, a));
+    }
+    HIPCHK(hipEventRecord(e1, s));
+    HIPCHK(hipEventSynchronize(e1));
+    float total = 0.f;
+    HIPCHK(hipEventElapsedTime(&total, e0, e1));
+    *ms = total / (float)iters;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(s);
+    return LFM_OK;
+}
+
+// Stand-alone argmax uses a small private state block per device.
+extern "C" int lfm_argmax(const float *v, uint32_t n, uint32_t *index, float *value)
+{
+    if (!v || n == 0 || !index)
+        return fail(LFM_EINVAL, "lfm_argmax: empty input");
+    Kernels *K;
+    RC(get_kernels(&K));
+    const uint32_t grid = std::min<uint32_t>((n + 255) / 256, 1024);
+    DevState *st = nullptr;
+    float *partial = nullptr;
+    HIPCHK(hipMalloc(&st, sizeof(DevState)));
+    HIPCHK(hipMalloc(&partial, grid * 2 * sizeof(float)));
+    DevState h;
+    memset(&h, 0, sizeof(h));
+    HIPCHK(hipMemcpy(st, &h, sizeof(h), hipMemcpyHostToDevice));
+    ArgmaxArgs a{v, partial, n, st};
+    int rc = launch(K->argmax, dim3(grid), 0, nullptr, a);
+    if (rc == LFM_OK) {
+        HIPCHK(hipDeviceSynchronize());
+        HIPCHK(hipMemcpy(&h, st, sizeof(h), hipMemcpyDeviceToHost));
+        *index = h.last_token;
+        if (value)
+            *value = h.last_value;
+    }
+    (void)hipFree(st);
+    (void)hipFree(partial);
+    return rc;
+}
+
+// ------------------------------------------------------------------ engine
+struct DevTensor {
+    uint32_t type = 0;
+    uint32_t nd = 0;
+    uint64_t ne[4] = {1, 1, 1, 1};
+    void *dev = nullptr;
+    size_t nbytes = 0;
+    Q6T q6{};
+};
+
+struct lfm_engine {
+    lfm_hparams hp{};
+    int device = 0;
+    uint32_t ctx = LFM_MAX_CTX;
+    bool finalized = false;
+    hipStream_t stream = nullptr;
+    Kernels *K = nullptr;
+    std::unordered_map<std::string, DevTensor> tensors;
+    std::string devname;
+
+    DevState *st = nullptr;
+    uint32_t *ids = nullptr, *out_tokens = nullptr, *sel = nullptr;
+    float *x = nullptr, *y = nullptr, *qkv = nullptr, *sw = nullptr, *rlogits = nullptr,
+          *logits = nullptr, *hpart = nullptr, *apart = nullptr;
+    std::vector<uint16_t *> kc, vc;
+    std::vector<float *> conv;
+    uint32_t head_grid = 1, nchunk = 1;
+    float tscale = 1.f;
+
+    hipGraphExec_t g_layers = nullptr, g_decode = nullptr;
+    uint64_t nodes_layers = 0, nodes_decode = 0;
+    uint64_t dispatches = 0;
+};
+
+static int engine_dev(lfm_engine *e)
+{
+    if (!e)
+        return fail(LFM_EINVAL, "engine is null");
+    HIPCHK(hipSetDevice(e->device));
+    return LFM_OK;
+}
+
+static int validate_hparams(const lfm_hparams *hp)
+{
+    if (!hp)
+        return fail(LFM_EINVAL, "hparams is null");
+    if (hp->n_layers == 0 || hp->n_layers > LFM_MAX_LAYERS)
+        return fail(LFM_EINVAL, "n_layers must be 1..%d", LFM_MAX_LAYERS);
+    if (hp->dim == 0 || hp->dim % 256 || hp->dim > 2048)
+        return fail(LFM_EINVAL, "dim must be a multiple of 256 up to 2048 (got %u)", hp->dim);
+    if (hp->head_dim != 64 || hp->heads * hp->head_dim != hp->dim)
+        return fail(LFM_EINVAL, "head_dim must be 64 and heads*head_dim == dim");
+    for (uint32_t l = 0; l < hp->n_layers; ++l) {
+        const uint32_t kv = hp->kv_heads[l];
+        if (kv && (kv > 8 || hp->heads % kv || hp->heads / kv > 4))
+            return fail(LFM_EINVAL, "layer %u: kv heads must divide heads, <= 8, heads/kv <= 4", l);
+    }
+    if (hp->vocab == 0)
+        return fail(LFM_EINVAL, "vocab must be positive");
+    if (hp->n_used == 0 || hp->n_used > 4 || hp->n_expert < hp->n_used || hp->n_expert > 64)
+        return fail(LFM_EINVAL, "experts: need 1 <= n_used <= 4 and n_used <= n_expert <= 64");
+    if (hp->expert_ff == 0 || hp->expert_ff % 256 || hp->expert_ff > 2048)
+        return fail(LFM_EINVAL, "expert_ff must be a multiple of 256 up to 2048");
+    if (hp->dense_lead > 0 && (hp->n_ff == 0 || hp->n_ff % 256 || hp->n_ff > 8192))
+        return fail(LFM_EINVAL, "n_ff must be a multiple of 256 up to 8192");
+    if (hp->conv_l_cache != 3)
+        return fail(LFM_EINVAL, "shortconv l_cache must be 3");
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_create(const lfm_hparams *hp, int device, lfm_engine **out)
+{
+    if (!out)
+        return fail(LFM_EINVAL, "out is null");
+    *out = nullptr;
+    RC(validate_hparams(hp));
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(LFM_EDEVICE, "no HIP device available");
+    if (device < 0 || device >= n)
+        return fail(LFM_EINVAL, "device %d out of range (%d devices)", device, n);
+    HIPCHK(hipSetDevice(device));
+    lfm_engine *e = new lfm_engine();
+    e->hp = *hp;
+    e->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess)
+        e->devname = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    int rc = get_kernels(&e->K);
+    if (rc == LFM_OK && hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+        rc = fail(LFM_EDEVICE, "hipStreamCreateWithFlags failed");
+    if (rc != LFM_OK) {
+        delete e;
+        return rc;
+    }
+    *out = e;
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_set_ctx(lfm_engine *e, uint32_t ctx)
+{
+    if (!e)
+        return fail(LFM_EINVAL, "engine is null");
+    if (e->finalized)
+        return fail(LFM_ESTATE, "set_ctx must precede lfm_engine_finalize");
+    if (ctx == 0 || ctx > LFM_MAX_CTX)
+        return fail(LFM_ERANGE, "ctx must be 1..%d", LFM_MAX_CTX);
+    e->ctx = ctx;
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_hparams(const lfm_engine *e, lfm_hparams *out)
+{
+    if (!e || !out)
+        return fail(LFM_EINVAL, "null argument");
+    *out = e->hp;
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_t type,
+                                        const uint64_t *ne, uint32_t nd, const void *host,
+                                        size_t nbytes)
+{
+    RC(engine_dev(e));
+    if (e->finalized)
+        return fail(LFM_ESTATE, "tensors must be uploaded before lfm_engine_finalize");
+    if (!name || !ne || !host || nd == 0 || nd > 4)
+        return fail(LFM_EINVAL, "upload_tensor: bad arguments");
+    DevTensor t;
+    t.type = type;
+    t.nd = nd;
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < nd; ++i) {
+        t.ne[i] = ne[i];
+        n *= ne[i];
+    }
+    size_t want;
+    if (type == LFM_GGML_TYPE_Q6_K) {
+        if (ne[0] % 256)
+            return fail(LFM_EINVAL, "%s: Q6_K row length %llu is not a multiple of 256", name,
+                        (unsigned long long)ne[0]);
+        want = (size_t)(n / 256 * 210);
+    } else if (type == LFM_GGML_TYPE_F32) {
+        want = (size_t)(n * 4);
+    } else {
+        return fail(LFM_EINVAL, "%s: unsupported ggml type %u (F32 and Q6_K only)", name, type);
+    }
+    if (nbytes != want)
+        return fail(LFM_EINVAL, "%s: %zu bytes given, %zu expected", name, nbytes, want);
+    auto old = e->tensors.find(name);
+    if (old != e->tensors.end()) {
+        (void)hipFree(old->second.dev);
+        e->tensors.erase(old);
+    }
+    HIPCHK(hipMalloc(&t.dev, want));
+    t.nbytes = want;
+    if (type == LFM_GGML_TYPE_Q6_K) {
+        std::vector<uint8_t> packed(want);
+        pack_blocks((const uint8_t *)host, n / 256, packed.data());
+        HIPCHK(hipMemcpy(t.dev, packed.data(), want, hipMemcpyHostToDevice));
+        t.q6 = q6view(t.dev, n / ne[0], ne[0]);
+    } else {
+        HIPCHK(hipMemcpy(t.dev, host, want, hipMemcpyHostToDevice));
+    }
+    e->tensors[name] = t;
+    return LFM_OK;
+}
+
+static DevTensor *tensor(lfm_engine *e, const char *fmt, uint32_t l = 0)
+{
+    char nm[128];
+    snprintf(nm, sizeof(nm), fmt, l);
+    auto it = e->tensors.find(nm);
+    return it == e->tensors.end() ? nullptr : &it->second;
+}
+static const float *f32(lfm_engine *e, const char *fmt, uint32_t l = 0)
+{
+    return (const float *)tensor(e, fmt, l)->dev;
+}
+static Q6T q6(lfm_engine *e, const char *fmt, uint32_t l = 0) { return tensor(e, fmt, l)->q6; }
+
+// ------------------------------------------------------------------ step plan
+static XSrc xsrc(const float *x, const float *norm, float eps)
+{
+    XSrc s;
+    memset(&s, 0, sizeof(s));
+    s.x = x;
+    s.norm_w = norm;
+    s.eps = eps;
+    return s;
+}
+
+static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
+{
+    const lfm_hparams &hp = e->hp;
+    const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
+    const uint32_t smem = (dim + 16) * 4;
+    XSrc src = xsrc(e->x, f32(e, "blk.%u.attn_norm.weight", l), hp.eps);
+    if (embed) {
+        src.embed = 1;
+        src.emb = q6(e, "token_embd.weight");
+        src.x_out = e->x;
+    }
+    if (kv == 0) {
+        ConvInprojArgs a;
+        a.w = q6(e, "blk.%u.shortconv.in_proj.weight", l);
+        a.src = src;
+        a.conv_w = f32(e, "blk.%u.shortconv.conv.weight", l);
+        a.state = e->conv[l];
+        a.y = e->y;
+        a.dim = dim;
+        a.st = e->st;
+        RC(launch(e->K->conv, dim3(std::max(1u, dim / 4)), smem, e->stream, a));
+        MatvecArgs m;
+        memset(&m, 0, sizeof(m));
+        m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
+        m.src = xsrc(e->y, nullptr, 0.f);
+        m.y = e->x;
+        m.in_dim = dim;
+        m.mode = 1;
+        RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
+        m.st = e->st;
+        RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), smem, e->stream, m));
+        e->dispatches += 2;
+        return LFM_OK;
+    }
+    const uint32_t hdkv = 64 * kv;
+    QkvArgs q;
+    q.wq = q6(e, "blk.%u.attn_q.weight", l);
+    q.wk = q6(e, "blk.%u.attn_k.weight", l);
+    q.wv = q6(e, "blk.%u.attn_v.weight", l);
+    q.src = src;
+    q.qkv = e->qkv;
+    q.dim = dim;
+    q.hdkv = hdkv;
+    q.st = e->st;
+    RC(launch(e->K->qkv, dim3(std::max(1u, (dim + 2 * hdkv + 3) / 4)), smem, e->stream, q));
+    AttnArgs at;
+    at.qkv = e->qkv;
+    at.q_norm = f32(e, "blk.%u.attn_q_norm.weight", l);
+    at.k_norm = f32(e, "blk.%u.attn_k_norm.weight", l);
+    at.eps = hp.eps;
+    at.tscale = e->tscale;
+    at.scale = 1.0f / sqrtf((float)hp.head_dim);
+    at.kcache = e->kc[l];
+    at.vcache = e->vc[l];
+    at.part = e->apart;
+    at.out = e->y;
+    at.ctx = e->ctx;
+    at.heads = hp.heads;
+    at.kv = kv;
+    at.nchunk = e->nchunk;
+    at.st = e->st;
+    RC(launch(e->K->attn, dim3(e->nchunk, kv), 0, e->stream, at));
+    MatvecArgs m;
+    memset(&m, 0, sizeof(m));
+    m.w = q6(e, "blk.%u.attn_output.weight", l);
+    m.src = xsrc(e->y, nullptr, 0.f);
+    m.y = e->x;
+    m.in_dim = dim;
+    m.mode = 1;
+    RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
+    m.st = e->st;
+    RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), smem, e->stream, m));
+    e->dispatches += 3;
+    return LFM_OK;
+}
+
+static int enq_ffn(lfm_engine *e, uint32_t l)
+{
+    const lfm_hparams &hp = e->hp;
+    const uint32_t dim = hp.dim;
+    const uint32_t smem = (dim + 16) * 4;
+    XSrc src = xsrc(e->x, f32(e, "blk.%u.ffn_norm.weight", l), hp.eps);
+    if (l < hp.dense_lead) {
+        GateUpArgs g;
+        g.wg = q6(e, "blk.%u.ffn_gate.weight", l);
+        g.wu = q6(e, "blk.%u.ffn_up.weight", l);
+        g.src = src;
+        g.sel = nullptr;
+        g.sw = e->sw;
+        g.ff = hp.n_ff;
+        g.n_used = 1;
+        g.st = e->st;
+        RC(launch(e->K->gateup, dim3(std::max(1u, hp.n_ff / 4)), smem, e->stream, g));
+        MatvecArgs m;
+        memset(&m, 0, sizeof(m));
+        m.w = q6(e, "blk.%u.ffn_down.weight", l);
+        m.src = xsrc(e->sw, nullptr, 0.f);
+        m.y = e->x;
+        m.in_dim = hp.n_ff;
+        m.mode = 1;
+        RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
+        m.st = e->st;
+        RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), (hp.n_ff + 16) * 4, e->stream,
+                  m));
+        e->dispatches += 2;
+        return LFM_OK;
+    }
+    RouterArgs r;
+    r.src = src;
+    r.w = f32(e, "blk.%u.ffn_gate_inp.weight", l);
+    r.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
+    r.logits = e->rlogits;
+    r.sel = e->sel;
+    r.dim = dim;
+    r.n_expert = hp.n_expert;
+    r.n_used = hp.n_used;
+    r.st = e->st;
+    RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), smem, e->stream, r));
+    GateUpArgs g;
+    g.wg = q6(e, "blk.%u.ffn_gate_exps.weight", l);
+    g.wu = q6(e, "blk.%u.ffn_up_exps.weight", l);
+    g.src = src;
+    g.sel = e->sel;
+    g.sw = e->sw;
+    g.ff = hp.expert_ff;
+    g.n_used = hp.n_used;
+    g.st = e->st;
+    RC(launch(e->K->gateup, dim3(std::max(1u, hp.n_used * hp.expert_ff / 4)), smem, e->stream, g));
+    MoeDownArgs d;
+    d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
+    d.sw = e->sw;
+    d.sel = e->sel;
+    d.x = e->x;
+    d.dim = dim;
+    d.ff = hp.expert_ff;
+    d.n_used = hp.n_used;
+    d.st = e->st;
+    RC(launch(e->K->moe_down, dim3(std::max(1u, dim / 2)), 0, e->stream, d));
+    e->dispatches += 3;
+    return LFM_OK;
+}
+
+static int enq_head(lfm_engine *e, uint32_t advance)
+{
+    HeadArgs h;
+    h.emb = q6(e, "token_embd.weight");
+    h.src = xsrc(e->x, f32(e, "token_embd_norm.weight"), e->hp.eps);
+    h.logits = e->logits;
+    h.partial = e->hpart;
+    h.out_tokens = e->out_tokens;
+    h.vocab = e->hp.vocab;
+    h.advance = advance;
+    h.st = e->st;
+    RC(launch(e->K->head, dim3(e->head_grid), (e->hp.dim + 16) * 4, e->stream, h));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+static int enq_advance(lfm_engine *e)
+{
+    AdvanceArgs a{e->ids, e->st};
+    RC(launch(e->K->advance, dim3(1), 0, e->stream, a));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+static int enq_layers(lfm_engine *e)
+{
+    for (uint32_t l = 0; l < e->hp.n_layers; ++l) {
+        RC(enq_mixer(e, l, l == 0));
+        RC(enq_ffn(e, l));
+    }
+    return LFM_OK;
+}
+
+static int capture(lfm_engine *e, bool decode, hipGraphExec_t *exec, uint64_t *nodes)
+{
+    const uint64_t before = e->dispatches;
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enq_layers(e);
+    if (rc == LFM_OK)
+        rc = decode ? enq_head(e, 1) : enq_advance(e);
+    hipError_t ce = hipStreamEndCapture(e->stream, &g);
+    *nodes = e->dispatches - before;
+    e->dispatches = before;
+    if (rc != LFM_OK) {
+        if (g)
+            (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (ce != hipSuccess)
+        return fail(LFM_EDEVICE, "hipStreamEndCapture: %s", hipGetErrorString(ce));
+    hipError_t ie = hipGraphInstantiate(exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess)
+        return fail(LFM_EDEVICE, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_finalize(lfm_engine *e)
+{
+    RC(engine_dev(e));
+    if (e->finalized)
+        return fail(LFM_ESTATE, "engine already finalized");
+    const lfm_hparams &hp = e->hp;
+    // every tensor of the model must be present with the reference's shape
+    const int count = lfm_model_tensor_count(&hp);
+    for (int i = 0; i < count; ++i) {
+        lfm_tensor_desc d;
+        RC(lfm_model_tensor_desc(&hp, nullptr, i, &d));
+        auto it = e->tensors.find(d.name);
+        if (it == e->tensors.end())
+            return fail(LFM_EINVAL, "missing tensor %s", d.name);
+        const DevTensor &t = it->second;
+        bool ok = t.type == d.ggml_type && t.nd == d.n_dims;
+        for (uint32_t k = 0; ok && k < d.n_dims; ++k)
+            ok = t.ne[k] == d.ne[k];
+        if (!ok)
+            return fail(LFM_EINVAL, "tensor %s has the wrong type or shape", d.name);
+    }
+    const uint32_t dim = hp.dim;
+    uint32_t max_hdkv = 0;
+    for (uint32_t l = 0; l < hp.n_layers; ++l)
+        max_hdkv = std::max(max_hdkv, 64 * hp.kv_heads[l]);
+    e->nchunk = (e->ctx + 127) / 128;
+    e->head_grid = std::max(1u, std::min(1024u, (hp.vocab + 63) / 64));
+    e->tscale = powf(hp.rope_theta, -2.0f / (float)hp.head_dim);
+    const size_t swn = std::max<size_t>((size_t)hp.n_ff, (size_t)hp.n_used * hp.expert_ff);
+    HIPCHK(hipMalloc(&e->st, sizeof(DevState)));
+    HIPCHK(hipMemset(e->st, 0, sizeof(DevState)));
+    HIPCHK(hipMalloc(&e->ids, e->ctx * 4));
+    HIPCHK(hipMalloc(&e->out_tokens, e->ctx * 4));
+    HIPCHK(hipMalloc(&e->sel, 16 * 4));
+    HIPCHK(hipMemset(e->sel, 0, 16 * 4));
+    HIPCHK(hipMalloc(&e->x, dim * 4));
+    HIPCHK(hipMalloc(&e->y, dim * 4));
+    HIPCHK(hipMalloc(&e->qkv, (dim + 2 * max_hdkv) * 4));
+    HIPCHK(hipMalloc(&e->sw, swn * 4));
+    HIPCHK(hipMalloc(&e->rlogits, 64 * 4));
+    HIPCHK(hipMalloc(&e->logits, (size_t)hp.vocab * 4));
+    HIPCHK(hipMemset(e->logits, 0, (size_t)hp.vocab * 4));
+    HIPCHK(hipMalloc(&e->hpart, e->head_grid * 2 * 4));
+    HIPCHK(hipMalloc(&e->apart, (size_t)8 * e->nchunk * 4 * 66 * 4));
+    e->kc.assign(hp.n_layers, nullptr);
+    e->vc.assign(hp.n_layers, nullptr);
+    e->conv.assign(hp.n_layers, nullptr);
+    for (uint32_t l = 0; l < hp.n_layers; ++l) {
+        if (hp.kv_heads[l]) {
+            const size_t n = (size_t)hp.kv_heads[l] * e->ctx * 64 * 2;
+            HIPCHK(hipMalloc(&e->kc[l], n));
+            HIPCHK(hipMalloc(&e->vc[l], n));
+            HIPCHK(hipMemset(e->kc[l], 0, n));
+            HIPCHK(hipMemset(e->vc[l], 0, n));
+        } else {
+            HIPCHK(hipMalloc(&e->conv[l], (size_t)dim * 2 * 4));
+            HIPCHK(hipMemset(e->conv[l], 0, (size_t)dim * 2 * 4));
+        }
+    }
+    HIPCHK(hipDeviceSynchronize());
+    RC(capture(e, false, &e->g_layers, &e->nodes_layers));
+    RC(capture(e, true, &e->g_decode, &e->nodes_decode));
+    e->finalized = true;
+    return LFM_OK;
+}
+
+extern "C" void lfm_engine_destroy(lfm_engine *e)
+{
+    if (!e)
+        return;
+    (void)hipSetDevice(e->device);
+    if (e->stream)
+        (void)hipStreamSynchronize(e->stream);
+    if (e->g_layers)
+        (void)hipGraphExecDestroy(e->g_layers);
+    if (e->g_decode)
+        (void)hipGraphExecDestroy(e->g_decode);
+    for (auto &kv : e->tensors)
+        (void)hipFree(kv.second.dev);
+    void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
+                    e->rlogits, e->logits, e->hpart, e->apart};
+    for (void *p : bufs)
+        if (p)
+            (void)hipFree(p);
+    for (auto p : e->kc)
+        if (p)
+            (void)hipFree(p);
+    for (auto p : e->vc)
+        if (p)
+            (void)hipFree(p);
+    for (auto p : e->conv)
+        if (p)
+            (void)hipFree(p);
+    if (e->stream)
+        (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+// ------------------------------------------------------------------ forward
+static int need_final(lfm_engine *e)
+{
+    RC(engine_dev(e));
+    if (!e->finalized)
+        return fail(LFM_ESTATE, "engine is not finalized");
+    return LFM_OK;
+}
+
+// Writes the host-controlled head of DevState (counters are left alone).
+static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, uint32_t eos)
+{
+    DevState h;
+    memset(&h, 0, sizeof(h));
+    h.tok = tok;
+    h.pos = pos;
+    h.halt = 0;
+    h.step = 0;
+    h.eos = eos;
+    h.cursor = 0;
+    h.n_ids = n_ids;
+    HIPCHK(hipMemcpyAsync(e->st, &h, offsetof(DevState, counters), hipMemcpyHostToDevice, e->stream));
+    return LFM_OK;
+}
+
+static int read_state(lfm_engine *e, DevState *h)
+{
+    HIPCHK(hipMemcpyAsync(h, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(hipStreamSynchronize(e->stream));
+    return LFM_OK;
+}
+
+static int check_ids(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start)
+{
+    if (!ids || n == 0)
+        return fail(LFM_EINVAL, "token list must not be empty");
+    if ((uint64_t)start + n > e->ctx)
+        return fail(LFM_ERANGE, "forward context range: start %u + n %u > ctx %u", start, n, e->ctx);
+    for (uint32_t j = 0; j < n; ++j)
+        if (ids[j] >= e->hp.vocab)
+            return fail(LFM_ERANGE, "token out of range: %u >= vocab %u", ids[j], e->hp.vocab);
+    return LFM_OK;
+}
+
+// Layers for every id (graph replays), then the head without feedback.
+static int run_prompt(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start)
+{
+    RC(check_ids(e, ids, n, start));
+    HIPCHK(hipMemcpyAsync(e->ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+    RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu));
+    for (uint32_t j = 0; j < n; ++j) {
+        HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
+        e->dispatches += e->nodes_layers;
+    }
+    RC(enq_head(e, 0));
+    return LFM_OK;
+}
+
+extern "C" int lfm_forward_logits(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start,
+                                  float *logits, size_t cap)
+{
+    RC(need_final(e));
+    if (!logits || cap < e->hp.vocab)
+        return fail(LFM_ERANGE, "logits buffer holds %zu < vocab %u floats", cap, e->hp.vocab);
+    RC(run_prompt(e, ids, n, start));
+    HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->hp.vocab * 4, hipMemcpyDeviceToHost,
+                          e->stream));
+    HIPCHK(hipStreamSynchronize(e->stream));
+    return LFM_OK;
+}
+
+extern "C" int lfm_forward_token(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start,
+                                 uint32_t *next, float *max_logit)
+{
+    RC(need_final(e));
+    if (n == 0 || n > LFM_MAX_TOKEN_BATCH)
+        return fail(LFM_EINVAL, "token batch must be 1..%d", LFM_MAX_TOKEN_BATCH);
+    if (!next)
+        return fail(LFM_EINVAL, "next is null");
+    RC(run_prompt(e, ids, n, start));
+    DevState h;
+    RC(read_state(e, &h));
+    *next = h.last_token;
+    if (max_logit)
+        *max_logit = h.last_value;
+    return LFM_OK;
+}
+
+extern "C" int lfm_decode_run(lfm_engine *e, uint32_t first, uint32_t start, uint32_t steps,
+                              uint32_t eos, uint32_t *out_tokens, uint32_t *n_out)
+{
+    RC(need_final(e));
+    if (!out_tokens || !n_out)
+        return fail(LFM_EINVAL, "output pointers are null");
+    *n_out = 0;
+    if (steps == 0)
+        return LFM_OK;
+    if ((uint64_t)start + steps > e->ctx)
+        return fail(LFM_ERANGE, "decode range: start %u + steps %u > ctx %u", start, steps, e->ctx);
+    if (first >= e->hp.vocab)
+        return fail(LFM_ERANGE, "token out of range: %u >= vocab %u", first, e->hp.vocab);
+    RC(set_state(e, first, start, 0, eos));
+    for (uint32_t s = 0; s < steps; ++s) {
+        HIPCHK(hipGraphLaunch(e->g_decode, e->stream));
+        e->dispatches += e->nodes_decode;
+    }
+    DevState h;
+    RC(read_state(e, &h));
+    const uint32_t n = std::min(h.step, steps);
+    HIPCHK(hipMemcpy(out_tokens, e->out_tokens, (size_t)n * 4, hipMemcpyDeviceToHost));
+    *n_out = n;
+    return LFM_OK;
+}
+
+extern "C" int lfm_reset_session(lfm_engine *e)
+{
+    RC(need_final(e));
+    for (uint32_t l = 0; l < e->hp.n_layers; ++l)
+        if (e->conv[l])
+            HIPCHK(hipMemsetAsync(e->conv[l], 0, (size_t)e->hp.dim * 2 * 4, e->stream));
+    HIPCHK(hipStreamSynchronize(e->stream));
+    return LFM_OK;
+}
+
+extern "C" int lfm_snapshot_bytes(const lfm_engine *e, uint32_t valid, size_t *nbytes)
+{
+    if (!e || !nbytes)
+        return fail(LFM_EINVAL, "null argument");
+    if (valid > e->ctx)
+        return fail(LFM_ERANGE, "snapshot range: %u > ctx %u", valid, e->ctx);
+    size_t total = 0;
+    for (uint32_t l = 0; l < e->hp.n_layers; ++l)
+        total += e->hp.kv_heads[l] ? 2 * (size_t)64 * e->hp.kv_heads[l] * valid * 4
+                                   : (size_t)e->hp.dim * 2 * 4;
+    *nbytes = total;
+    return LFM_OK;
+}
+
+extern "C" int lfm_snapshot_cache(lfm_engine *e, uint32_t valid, uint8_t *buf, size_t cap,
+                                  size_t *written)
+{
+    RC(need_final(e));
+    size_t need;
+    RC(lfm_snapshot_bytes(e, valid, &need));
+    if (!buf || cap < need)
+        return fail(LFM_ERANGE, "snapshot buffer holds %zu < %zu bytes", cap, need);
+    HIPCHK(hipStreamSynchronize(e->stream));
+    float *out = (float *)buf;
+    size_t o = 0;
+    std::vector<uint16_t> kh;
+    for (uint32_t l = 0; l < e->hp.n_layers; ++l) {
+        const uint32_t kv = e->hp.kv_heads[l];
+        if (kv) {
+            kh.resize((size_t)kv * e->ctx * 64);
+            for (int which = 0; which < 2; ++which) {
+                HIPCHK(hipMemcpy(kh.data(), which ? e->vc[l] : e->kc[l], kh.size() * 2,
+                                 hipMemcpyDeviceToHost));
+                for (uint32_t t = 0; t < valid; ++t)
+                    for (uint32_t h = 0; h < kv; ++h)
+                        for (uint32_t d = 0; d < 64; ++d)
+                            out[o++] = lfm_f16_to_f32(kh[((size_t)h * e->ctx + t) * 64 + d]);
+            }
+        } else {
+            HIPCHK(hipMemcpy(out + o, e->conv[l], (size_t)e->hp.dim * 2 * 4, hipMemcpyDeviceToHost));
+            o += (size_t)e->hp.dim * 2;
+        }
+    }
+    if (written)
+        *written = need;
+    return LFM_OK;
+}
+
+extern "C" int lfm_restore_session(lfm_engine *e, uint32_t valid, const uint8_t *buf, size_t len)
+{
+    RC(need_final(e));
+    size_t need;
+    RC(lfm_snapshot_bytes(e, valid, &need));
+    if (!buf && len)
+        return fail(LFM_EINVAL, "snapshot buffer is null");
+    if (len < need)
+        return fail(LFM_EINVAL, "truncated snapshot: %zu < %zu bytes", len, need);
+    if (len > need)
+        return fail(LFM_EINVAL, "extra snapshot data: %zu > %zu bytes", len, need);
+    HIPCHK(hipStreamSynchronize(e->stream));
+    const float *in = (const float *)buf;
+    size_t o = 0;
+    std::vector<uint16_t> kh;
+    for (uint32_t l = 0; l < e->hp.n_layers; ++l) {
+        const uint32_t kv = e->hp.kv_heads[l];
+        if (kv) {
+            kh.resize((size_t)kv * e->ctx * 64);
+            for (int which = 0; which < 2; ++which) {
+                uint16_t *dst = which ? e->vc[l] : e->kc[l];
+                HIPCHK(hipMemcpy(kh.data(), dst, kh.size() * 2, hipMemcpyDeviceToHost));
+                for (uint32_t t = 0; t < valid; ++t)
+                    for (uint32_t h = 0; h < kv; ++h)
+                        for (uint32_t d = 0; d < 64; ++d)
+                            kh[((size_t)h * e->ctx + t) * 64 + d] = lfm_f32_to_f16(in[o++]);
+                HIPCHK(hipMemcpy(dst, kh.data(), kh.size() * 2, hipMemcpyHostToDevice));
+            }
+        } else {
+            HIPCHK(hipMemcpy(e->conv[l], in + o, (size_t)e->hp.dim * 2 * 4, hipMemcpyHostToDevice));
+            o += (size_t)e->hp.dim * 2;
+        }
+    }
+    return LFM_OK;
+}
+
+extern "C" int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap)
+{
+    RC(need_final(e));
+    if (!out || cap < e->hp.vocab)
+        return fail(LFM_ERANGE, "logits buffer holds %zu < vocab %u floats", cap, e->hp.vocab);
+    HIPCHK(hipStreamSynchronize(e->stream));
+    HIPCHK(hipMemcpy(out, e->logits, (size_t)e->hp.vocab * 4, hipMemcpyDeviceToHost));
+    return LFM_OK;
+}
+
+extern "C" uint64_t lfm_dispatch_count(const lfm_engine *e) { return e ? e->dispatches : 0; }
+
+extern "C" int lfm_device_name(const lfm_engine *e, char *buf, size_t cap)
+{
+    if (!e || !buf || cap == 0)
+        return fail(LFM_EINVAL, "null argument");
+    snprintf(buf, cap, "%s", e->devname.c_str());
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ layer entry points
+static int run_layer_part(lfm_engine *e, uint32_t layer, float *x, uint32_t pos, bool mixer)
+{
+    RC(need_final(e));
+    if (!x)
+        return fail(LFM_EINVAL, "x is null");
+    if (layer >= e->hp.n_layers)
+        return fail(LFM_ERANGE, "layer %u >= %u", layer, e->hp.n_layers);
+    if (pos >= e->ctx)
+        return fail(LFM_ERANGE, "position %u >= ctx %u", pos, e->ctx);
+    HIPCHK(hipMemcpyAsync(e->x, x, (size_t)e->hp.dim * 4, hipMemcpyHostToDevice, e->stream));
+    RC(set_state(e, 0, pos, 0, 0xFFFFFFFFu));
+    RC(mixer ? enq_mixer(e, layer, false) : enq_ffn(e, layer));
+    HIPCHK(hipMemcpyAsync(x, e->x, (size_t)e->hp.dim * 4, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(hipStreamSynchronize(e->stream));
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_run_mixer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos)
+{
+    return run_layer_part(e, layer, x, pos, true);
+}
+
+extern "C" int lfm_engine_run_ffn(lfm_engine *e, uint32_t layer, float *x)
+{
+    return run_layer_part(e, layer, x, 0, false);
+}
+
+extern "C" int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *w, uint32_t cap)
+{
+    RC(need_final(e));
+    if (!ids || !w || cap < e->hp.n_used)
+        return fail(LFM_ERANGE, "route buffers hold %u < %u entries", cap, e->hp.n_used);
+    uint32_t h[16];
+    HIPCHK(hipStreamSynchronize(e->stream));
+    HIPCHK(hipMemcpy(h, e->sel, sizeof(h), hipMemcpyDeviceToHost));
+    for (uint32_t r = 0; r < e->hp.n_used; ++r) {
+        ids[r] = h[r];
+        memcpy(&w[r], &h[8 + r], 4);
+    }
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ synthetic model
+extern "C" int lfm_engine_load_synthetic(lfm_engine *e, const lfm_synth_opts *o, int threads)
+{
+    RC(engine_dev(e));
+    const int count = lfm_model_tensor_count(&e->hp);
+    if (count < 0)
+        return fail(LFM_EINVAL, "bad hparams");
+    std::vector<uint8_t> buf;
+    for (int i = 0; i < count; ++i) {
+        lfm_tensor_desc d;
+        RC(lfm_model_tensor_desc(&e->hp, o, i, &d));
+        const size_t nb = lfm_tensor_nbytes(&d);
+        buf.resize(nb);
+        RC(lfm_synth_tensor(o, &d, buf.data(), nb, threads));
+        RC(lfm_engine_upload_tensor(e, d.name, d.ggml_type, d.ne, d.n_dims, buf.data(), nb));
+    }
+    return LFM_OK;
+}

@@ -1,0 +1,454 @@
+"""Python mirror of the reference engine interface over the C ABI (include/lfm_hip.h).
+
+The reference's callers use ``GpuEngine`` (Amidwestnoob/lfm2-w9100-rust
+engine/src/gpu_lfm.rs:23-245, engine/src/gpu_lfm/resident_graph.rs:89-602) and
+``GpuOps`` (engine/src/ops.rs).  This module keeps those names, argument
+meanings and error behaviour (precondition failures raise ``LfmError`` where the
+reference returns ``anyhow`` errors) on top of ``liblfm_hip.so``, whose HIP
+kernels do all the work.  There is no CPU fallback: if the library or its gfx950
+code object is missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Iterable, List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblfm_hip.so")
+CODE_OBJECT_PATH = os.path.join(_HERE, "lfm_kernels.hsaco")
+
+LFM_OK, LFM_EINVAL, LFM_ERANGE, LFM_EDEVICE, LFM_ESTATE, LFM_EINTERNAL = range(6)
+GGML_TYPE_F32 = 0
+GGML_TYPE_Q6_K = 14
+MAX_LAYERS = 64
+MAX_CTX = 4096
+QK_K = 256
+Q6_K_BYTES = 210
+
+
+class LfmError(RuntimeError):
+    """A non-zero status from the C ABI; ``code`` is one of the LFM_E* values."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class Hparams(C.Structure):
+    """``lfm_hparams``; mirrors Hyperparams (engine/src/lfm.rs:31-49)."""
+
+    _fields_ = [
+        ("dim", C.c_uint32), ("heads", C.c_uint32), ("head_dim", C.c_uint32),
+        ("n_layers", C.c_uint32), ("kv_heads", C.c_uint32 * MAX_LAYERS),
+        ("vocab", C.c_uint32), ("eps", C.c_float), ("rope_theta", C.c_float),
+        ("eos", C.c_uint32), ("n_expert", C.c_uint32), ("n_used", C.c_uint32),
+        ("expert_ff", C.c_uint32), ("n_ff", C.c_uint32), ("dense_lead", C.c_uint32),
+        ("conv_l_cache", C.c_uint32),
+    ]
+
+    def kv_list(self) -> List[int]:
+        return [int(self.kv_heads[i]) for i in range(self.n_layers)]
+
+
+class TensorDesc(C.Structure):
+    _fields_ = [
+        ("name", C.c_char * 96), ("ggml_type", C.c_uint32), ("n_dims", C.c_uint32),
+        ("ne", C.c_uint64 * 4), ("kind", C.c_uint32), ("sigma", C.c_float),
+    ]
+
+    @property
+    def shape(self):
+        return tuple(int(self.ne[i]) for i in range(self.n_dims))
+
+
+class SynthOpts(C.Structure):
+    _fields_ = [
+        ("seed", C.c_uint64), ("d_sigma", C.c_float), ("norm_sigma", C.c_float),
+        ("router_sigma", C.c_float), ("bias_sigma", C.c_float), ("conv_sigma", C.c_float),
+    ]
+
+
+# Attention layers of the synthetic LFM2.5-8B-A1B-shaped model (18 conv + 6 GQA).
+LFM2_ATTENTION_LAYERS = (2, 6, 10, 14, 18, 21)
+
+
+def make_hparams(dim=2048, heads=32, n_layers=24, attention_layers=LFM2_ATTENTION_LAYERS,
+                 kv=8, vocab=65536, eps=1e-5, rope_theta=1e6, eos=124900, n_expert=32,
+                 n_used=4, expert_ff=1792, n_ff=7168, dense_lead=2) -> Hparams:
+    hp = Hparams()
+    hp.dim, hp.heads, hp.head_dim, hp.n_layers = dim, heads, 64, n_layers
+    for l in range(n_layers):
+        hp.kv_heads[l] = kv if l in attention_layers else 0
+    hp.vocab, hp.eps, hp.rope_theta, hp.eos = vocab, eps, rope_theta, eos
+    hp.n_expert, hp.n_used, hp.expert_ff, hp.n_ff = n_expert, n_used, expert_ff, n_ff
+    hp.dense_lead, hp.conv_l_cache = dense_lead, 3
+    return hp
+
+
+_lib = None
+
+
+def lib():
+    """Load liblfm_hip.so (raises if it or the gfx950 code object is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH) or not os.path.exists(CODE_OBJECT_PATH):
+        raise LfmError(LFM_EDEVICE, f"native library not built: {LIB_PATH} / {CODE_OBJECT_PATH}"
+                       " (run __graft_entry__.build())")
+    L = C.CDLL(LIB_PATH)
+    P, u32, u64, i32, f32, sz = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_size_t
+    pu32, pf32, pu8 = C.POINTER(C.c_uint32), C.POINTER(C.c_float), C.POINTER(C.c_uint8)
+    sig = {
+        "lfm_last_error": (C.c_char_p, []), "lfm_version": (C.c_char_p, []),
+        "lfm_device_count": (i32, [C.POINTER(i32)]),
+        "lfm_engine_create": (i32, [C.POINTER(Hparams), i32, C.POINTER(P)]),
+        "lfm_engine_upload_tensor": (i32, [P, C.c_char_p, u32, C.POINTER(u64), u32, P, sz]),
+        "lfm_engine_finalize": (i32, [P]), "lfm_engine_set_ctx": (i32, [P, u32]),
+        "lfm_engine_destroy": (None, [P]), "lfm_engine_hparams": (i32, [P, C.POINTER(Hparams)]),
+        "lfm_forward_logits": (i32, [P, pu32, u32, u32, pf32, sz]),
+        "lfm_forward_token": (i32, [P, pu32, u32, u32, pu32, pf32]),
+        "lfm_decode_run": (i32, [P, u32, u32, u32, u32, pu32, pu32]),
+        "lfm_reset_session": (i32, [P]),
+        "lfm_snapshot_bytes": (i32, [P, u32, C.POINTER(sz)]),
+        "lfm_snapshot_cache": (i32, [P, u32, pu8, sz, C.POINTER(sz)]),
+        "lfm_restore_session": (i32, [P, u32, pu8, sz]),
+        "lfm_snapshot_logits": (i32, [P, pf32, sz]),
+        "lfm_dispatch_count": (u64, [P]), "lfm_device_name": (i32, [P, C.c_char_p, sz]),
+        "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
+        "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
+        "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
+        "lfm_dev_alloc": (i32, [sz, C.POINTER(P)]), "lfm_dev_free": (i32, [P]),
+        "lfm_memcpy_htod": (i32, [P, P, sz]), "lfm_memcpy_dtoh": (i32, [P, P, sz]),
+        "lfm_dev_synchronize": (i32, []),
+        "lfm_q6k_nbytes": (sz, [u64, u64]), "lfm_q6k_pack": (i32, [P, u64, u64, P]),
+        "lfm_q6k_unpack": (i32, [P, u64, u64, P]),
+        "lfm_q6k_dequant": (i32, [P, u64, u64, P, P]),
+        "lfm_q6k_matvec": (i32, [P, u64, u64, P, P, P]),
+        "lfm_q6k_matvec_time": (i32, [P, u32, u64, u64, P, P, u32, pf32]),
+        "lfm_argmax": (i32, [P, u32, pu32, pf32]),
+        "lfm_synth_default_opts": (None, [C.POINTER(SynthOpts)]),
+        "lfm_model_tensor_count": (i32, [C.POINTER(Hparams)]),
+        "lfm_model_tensor_desc": (i32, [C.POINTER(Hparams), C.POINTER(SynthOpts), i32,
+                                        C.POINTER(TensorDesc)]),
+        "lfm_tensor_nbytes": (sz, [C.POINTER(TensorDesc)]),
+        "lfm_synth_tensor": (i32, [C.POINTER(SynthOpts), C.POINTER(TensorDesc), P, sz, i32]),
+        "lfm_synth_q6k_blocks": (i32, [u64, C.c_char_p, u64, f32, P, i32]),
+        "lfm_synth_normal_f32": (i32, [u64, C.c_char_p, u64, f32, f32, P, i32]),
+        "lfm_engine_load_synthetic": (i32, [P, C.POINTER(SynthOpts), i32]),
+        "lfm_f32_to_f16": (C.c_uint16, [f32]), "lfm_f16_to_f32": (f32, [C.c_uint16]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != LFM_OK:
+        raise LfmError(rc, lib().lfm_last_error().decode(errors="replace"))
+
+
+def _u32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+def _f32p(a: np.ndarray):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    _check(lib().lfm_device_count(C.byref(n)))
+    return n.value
+
+
+# ------------------------------------------------------------------ synthetic model
+def synth_opts(seed: int = 0x9E3779B97F4A7C15, bias_sigma: float = 0.0, **kw) -> SynthOpts:
+    o = SynthOpts()
+    lib().lfm_synth_default_opts(C.byref(o))
+    o.seed = seed
+    o.bias_sigma = bias_sigma
+    for k, v in kw.items():
+        setattr(o, k, v)
+    return o
+
+
+def model_tensor_descs(hp: Hparams, opts: Optional[SynthOpts] = None) -> List[TensorDesc]:
+    n = lib().lfm_model_tensor_count(C.byref(hp))
+    if n < 0:
+        raise LfmError(LFM_EINVAL, "bad hparams")
+    out = []
+    for i in range(n):
+        d = TensorDesc()
+        _check(lib().lfm_model_tensor_desc(C.byref(hp), C.byref(opts) if opts else None, i, C.byref(d)))
+        out.append(d)
+    return out
+
+
+def synth_tensor(desc: TensorDesc, opts: Optional[SynthOpts] = None, threads: int = 8) -> np.ndarray:
+    """Seeded tensor content: uint8 raw GGUF bytes (Q6_K) or float32 values."""
+    nb = lib().lfm_tensor_nbytes(C.byref(desc))
+    buf = np.empty(nb, dtype=np.uint8)
+    _check(lib().lfm_synth_tensor(C.byref(opts) if opts else None, C.byref(desc),
+                                  buf.ctypes.data, nb, threads))
+    return buf if desc.ggml_type == GGML_TYPE_Q6_K else buf.view(np.float32)
+
+
+def synth_q6k_blocks(seed: int, stream: str, nblocks: int, d_sigma: float = 1e-3,
+                     threads: int = 8) -> np.ndarray:
+    out = np.empty(nblocks * Q6_K_BYTES, dtype=np.uint8)
+    _check(lib().lfm_synth_q6k_blocks(seed, stream.encode(), nblocks, d_sigma, out.ctypes.data,
+                                      threads))
+    return out
+
+
+def synth_normal(seed: int, stream: str, n: int, mean: float = 0.0, sigma: float = 1.0,
+                 threads: int = 8) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().lfm_synth_normal_f32(seed, stream.encode(), n, mean, sigma, out.ctypes.data,
+                                      threads))
+    return out
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().lfm_f32_to_f16(x))
+
+
+# ------------------------------------------------------------------ device buffers
+class DeviceBuffer:
+    """Device memory owned by the library's HIP runtime (hipMalloc)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(lib().lfm_dev_alloc(self.nbytes, C.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        _check(lib().lfm_memcpy_htod(b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0):
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        _check(lib().lfm_memcpy_htod(self.ptr + offset, a.ctypes.data, a.nbytes))
+
+    def download(self, dtype, count: Optional[int] = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        _check(lib().lfm_memcpy_dtoh(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            _check(lib().lfm_dev_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ Q6_K operator API
+def q6k_nbytes(rows: int, in_dim: int) -> int:
+    return rows * (in_dim // QK_K) * Q6_K_BYTES
+
+
+def q6k_pack(raw: np.ndarray, rows: int, in_dim: int) -> np.ndarray:
+    """Raw GGUF Q6_K bytes -> the device plane layout (host to host)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    if raw.nbytes != q6k_nbytes(rows, in_dim):
+        raise LfmError(LFM_EINVAL, "raw size does not match rows x in_dim")
+    out = np.empty_like(raw)
+    _check(lib().lfm_q6k_pack(raw.ctypes.data, rows, in_dim, out.ctypes.data))
+    return out
+
+
+def q6k_unpack(packed: np.ndarray, rows: int, in_dim: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty_like(packed)
+    _check(lib().lfm_q6k_unpack(packed.ctypes.data, rows, in_dim, out.ctypes.data))
+    return out
+
+
+class Q6Weight:
+    """A packed Q6_K tensor resident on the device (rows x in_dim)."""
+
+    def __init__(self, raw: np.ndarray, rows: int, in_dim: int):
+        self.rows, self.in_dim = rows, in_dim
+        self.buf = DeviceBuffer.from_array(q6k_pack(raw, rows, in_dim))
+
+    def dequant(self) -> np.ndarray:
+        out = DeviceBuffer(self.rows * self.in_dim * 4)
+        _check(lib().lfm_q6k_dequant(self.buf.ptr, self.rows, self.in_dim, out.ptr, None))
+        return out.download(np.float32).reshape(self.rows, self.in_dim)
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        """GpuOps::q6k_matmul for one column (engine/src/ops.rs:340-374)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.shape != (self.in_dim,):
+            raise LfmError(LFM_EINVAL, "x has the wrong length")
+        xb = DeviceBuffer.from_array(x)
+        yb = DeviceBuffer(self.rows * 4)
+        _check(lib().lfm_q6k_matvec(self.buf.ptr, self.rows, self.in_dim, xb.ptr, yb.ptr, None))
+        return yb.download(np.float32)
+
+
+def q6k_matvec_time(weights: DeviceBuffer, ncopies: int, rows: int, in_dim: int,
+                    x: DeviceBuffer, y: DeviceBuffer, iters: int) -> float:
+    ms = C.c_float(0)
+    _check(lib().lfm_q6k_matvec_time(weights.ptr, ncopies, rows, in_dim, x.ptr, y.ptr, iters,
+                                     C.byref(ms)))
+    return ms.value
+
+
+def argmax(v: np.ndarray):
+    """GPU greedy argmax (ties to the lowest id, NaN never wins) -> (index, value)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    b = DeviceBuffer.from_array(v)
+    idx, val = C.c_uint32(0), C.c_float(0)
+    _check(lib().lfm_argmax(b.ptr, v.size, C.byref(idx), C.byref(val)))
+    return idx.value, val.value
+
+
+# ------------------------------------------------------------------ engine
+class GpuEngine:
+    """The reference's GpuEngine (engine/src/gpu_lfm.rs:23-245) on MI355X."""
+
+    def __init__(self, hp: Hparams, device: int = 0, ctx: int = MAX_CTX):
+        self._e = C.c_void_p()
+        _check(lib().lfm_engine_create(C.byref(hp), device, C.byref(self._e)))
+        self.hp = hp
+        self.ctx = ctx
+        _check(lib().lfm_engine_set_ctx(self._e, ctx))
+        self._finalized = False
+
+    # GpuEngine::load (gpu_lfm.rs:51-115), tensors supplied by the caller
+    @classmethod
+    def load(cls, hp: Hparams, tensors: Iterable, device: int = 0, ctx: int = MAX_CTX) -> "GpuEngine":
+        e = cls(hp, device, ctx)
+        for name, ggml_type, shape, data in tensors:
+            e.upload_tensor(name, ggml_type, shape, data)
+        e.finalize()
+        return e
+
+    @classmethod
+    def load_synthetic(cls, hp: Hparams, opts: Optional[SynthOpts] = None, device: int = 0,
+                       ctx: int = MAX_CTX, threads: int = 16) -> "GpuEngine":
+        e = cls(hp, device, ctx)
+        o = opts if opts is not None else synth_opts()
+        _check(lib().lfm_engine_load_synthetic(e._e, C.byref(o), threads))
+        e.finalize()
+        return e
+
+    def upload_tensor(self, name: str, ggml_type: int, shape: Sequence[int], data: np.ndarray):
+        data = np.ascontiguousarray(data)
+        ne = (C.c_uint64 * 4)(*([int(s) for s in shape] + [1] * (4 - len(shape))))
+        _check(lib().lfm_engine_upload_tensor(self._e, name.encode(), ggml_type, ne, len(shape),
+                                              data.ctypes.data, data.nbytes))
+
+    def finalize(self):
+        _check(lib().lfm_engine_finalize(self._e))
+        self._finalized = True
+
+    def set_ctx(self, ctx: int):
+        _check(lib().lfm_engine_set_ctx(self._e, ctx))
+        self.ctx = ctx
+
+    def forward(self, ids: Sequence[int], start_pos: int) -> np.ndarray:
+        ids_a = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.hp.vocab, dtype=np.float32)
+        _check(lib().lfm_forward_logits(self._e, _u32p(ids_a), ids_a.size, start_pos, _f32p(out),
+                                        out.size))
+        return out
+
+    def forward_token(self, ids: Sequence[int], position: int) -> int:
+        ids_a = np.ascontiguousarray(ids, dtype=np.uint32)
+        nxt, val = C.c_uint32(0), C.c_float(0)
+        _check(lib().lfm_forward_token(self._e, _u32p(ids_a), ids_a.size, position, C.byref(nxt),
+                                       C.byref(val)))
+        self.last_max_logit = val.value
+        return nxt.value
+
+    def decode_run(self, first_token: int, start_pos: int, steps: int, eos: Optional[int] = None) -> List[int]:
+        out = np.empty(max(steps, 1), dtype=np.uint32)
+        n = C.c_uint32(0)
+        e = self.hp.eos if eos is None else eos
+        _check(lib().lfm_decode_run(self._e, first_token, start_pos, steps, e, _u32p(out), C.byref(n)))
+        return [int(t) for t in out[: n.value]]
+
+    def reset_session(self):
+        _check(lib().lfm_reset_session(self._e))
+
+    def snapshot_bytes(self, valid_tokens: int) -> int:
+        n = C.c_size_t(0)
+        _check(lib().lfm_snapshot_bytes(self._e, valid_tokens, C.byref(n)))
+        return n.value
+
+    def snapshot_resident_cache(self, valid_tokens: int) -> bytes:
+        n = self.snapshot_bytes(valid_tokens)
+        buf = np.empty(n, dtype=np.uint8)
+        w = C.c_size_t(0)
+        _check(lib().lfm_snapshot_cache(self._e, valid_tokens,
+                                        buf.ctypes.data_as(C.POINTER(C.c_uint8)), n, C.byref(w)))
+        return buf.tobytes()
+
+    def restore_session(self, valid_tokens: int, data: bytes):
+        a = np.frombuffer(data, dtype=np.uint8)
+        _check(lib().lfm_restore_session(self._e, valid_tokens,
+                                         a.ctypes.data_as(C.POINTER(C.c_uint8)), a.size))
+
+    def snapshot_resident_logits(self) -> np.ndarray:
+        out = np.empty(self.hp.vocab, dtype=np.float32)
+        _check(lib().lfm_snapshot_logits(self._e, _f32p(out), out.size))
+        return out
+
+    def dispatch_count(self) -> int:
+        return int(lib().lfm_dispatch_count(self._e))
+
+    @property
+    def device_name(self) -> str:
+        buf = C.create_string_buffer(256)
+        _check(lib().lfm_device_name(self._e, buf, 256))
+        return buf.value.decode()
+
+    # layer-level entry points (one decode-step half on a host residual vector)
+    def run_mixer(self, layer: int, x: np.ndarray, pos: int) -> np.ndarray:
+        xa = np.array(x, dtype=np.float32, copy=True)
+        _check(lib().lfm_engine_run_mixer(self._e, layer, _f32p(xa), pos))
+        return xa
+
+    def run_ffn(self, layer: int, x: np.ndarray) -> np.ndarray:
+        xa = np.array(x, dtype=np.float32, copy=True)
+        _check(lib().lfm_engine_run_ffn(self._e, layer, _f32p(xa)))
+        return xa
+
+    def last_route(self):
+        ids = np.zeros(8, dtype=np.uint32)
+        w = np.zeros(8, dtype=np.float32)
+        _check(lib().lfm_engine_last_route(self._e, _u32p(ids), _f32p(w), 8))
+        return [int(i) for i in ids[: self.hp.n_used]], w[: self.hp.n_used].copy()
+
+    def close(self):
+        if self._e:
+            lib().lfm_engine_destroy(self._e)
+            self._e = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

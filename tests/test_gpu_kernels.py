@@ -1,0 +1,91 @@
+"""GPU parity of the Q6_K kernels and argmax against the oracle (C ABI calls).
+
+Bars: Q6_K unpack bit-exact; matvec relative L2 <= 1e-5 against the f64
+q6k_matvec oracle (engine/src/q6k.rs:167-183, relative-L2 convention of
+bin/q6_check.rs:120-136); argmax index bit-exact (main.rs:112-141 semantics).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def blocks(n, seed, d_sigma=1e-3):
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(n, 210), dtype=np.uint8)
+    raw[:, 192:208] = (rng.integers(-32, 32, size=(n, 16))).astype(np.int8).view(np.uint8)
+    d = (rng.standard_normal(n) * d_sigma).astype(np.float16)
+    raw[:, 208:210] = d.view(np.uint8).reshape(n, 2)
+    return raw
+
+
+def test_dequant_bit_exact_cfg0_shape(gpu, oracle):
+    rows, in_dim = 6144, 2048
+    raw = gpu.synth_q6k_blocks(0x9E3779B97F4A7C15, "cfg0.weight", rows * in_dim // 256)
+    w = gpu.Q6Weight(raw, rows, in_dim)
+    got = w.dequant()
+    exp = oracle.dequant_rows(raw, rows, in_dim)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_dequant_bit_exact_edge_blocks(gpu, oracle):
+    raw = blocks(64, 11)
+    raw[0, 192:208] = 0                          # zero scales -> signed zeros
+    raw[1, :128] = 0; raw[1, 128:192] = 0xAA     # q - 32 == 0 everywhere
+    raw[2, 208:210] = np.array([3e-7], np.float16).view(np.uint8)   # subnormal d
+    raw[3, 208:210] = np.array([-0.0], np.float16).view(np.uint8)
+    raw[4, 192:208] = np.array([-128, 127] * 8, np.int8).view(np.uint8)
+    from test_oracle_q6k import xorshift_blocks
+    mirror = xorshift_blocks(64)
+    for r in (raw, mirror):
+        w = gpu.Q6Weight(r.reshape(-1), 64, 256)
+        got = w.dequant()
+        exp = oracle.dequant_rows(r.reshape(-1), 64, 256)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+
+
+def test_matvec_cfg0(gpu, oracle):
+    """cfg0: W 6144x2048 Q6_K, x ~ N(0,1) f32, rel-L2 <= 1e-5 vs the f64 oracle."""
+    rows, in_dim = 6144, 2048
+    raw = gpu.synth_q6k_blocks(0x9E3779B97F4A7C15, "cfg0.weight", rows * in_dim // 256)
+    x = gpu.synth_normal(0x9E3779B97F4A7C15, "cfg0.x", in_dim)
+    y = gpu.Q6Weight(raw, rows, in_dim).matvec(x)
+    ref = oracle.q6k_matvec(raw, in_dim, rows, x)
+    err = rel_l2(y, ref)
+    print(f"cfg0 rel-L2 {err:.3e}")
+    assert err <= 1e-5
+
+
+@pytest.mark.parametrize("rows,in_dim", [(1, 256), (3, 512), (513, 1792), (2048, 7168), (64, 8192),
+                                         (1000, 2048), (7, 768)])
+def test_matvec_shapes(gpu, oracle, rows, in_dim):
+    raw = blocks(rows * in_dim // 256, rows + in_dim).reshape(-1)
+    x = np.random.default_rng(rows).standard_normal(in_dim).astype(np.float32)
+    y = gpu.Q6Weight(raw, rows, in_dim).matvec(x)
+    ref = oracle.q6k_matvec(raw, in_dim, rows, x)
+    assert rel_l2(y, ref) <= 1e-5
+
+
+def test_argmax_cases(gpu, oracle):
+    from test_oracle_argmax_route import lcg_bits
+    seed = 17
+    for n in (1, 2, 7, 8, 9, 63, 64, 65, 255, 256, 257, 513, 4097):
+        xs, seed = lcg_bits(n, seed)
+        xs = xs.copy()
+        assert gpu.argmax(xs)[0] == oracle.argmax(xs)
+        for v in [np.nan, -np.inf, np.inf, 0.0, -0.0, 1.0]:
+            xs.fill(v)
+            assert gpu.argmax(xs)[0] == oracle.argmax(xs)
+        if n > 8:
+            xs[7] = 2.0
+            xs[8] = 2.0
+            assert gpu.argmax(xs)[0] == 7
+    for n in (63, 513, 128003):
+        xs = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+        xs[0] = np.nan
+        xs[-1] = 100.0
+        assert gpu.argmax(xs)[0] == n - 1
+        xs[n // 2] = 100.0
+        assert gpu.argmax(xs)[0] == n // 2
