@@ -111,6 +111,9 @@ def main():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--synthetic-state", action="store_true",
+                    help="skip the prefill: restore a seeded binary16 KV / conv state for the "
+                         "prompt positions instead (isolates decode kernels for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the batch-1 decode path is not sharded across GPUs "
@@ -128,12 +131,19 @@ def main():
     prompt = [int(v) for v in np.random.default_rng(SEED & 0xFFFFFFFF).integers(0, hp.vocab, n_prompt)]
 
     t = time.perf_counter()
-    pos, first = 0, None
-    for c in range(0, n_prompt, 64):  # api_stream.rs:58-63 chunked prefill
-        first = eng.forward_token(prompt[c:c + 64], pos)
-        pos += len(prompt[c:c + 64])
+    if args.synthetic_state:
+        nbytes = eng.snapshot_bytes(n_prompt)
+        state = lfm_hip.synth_normal(SEED, "bench.state", nbytes // 4, threads=16)
+        eng.restore_session(n_prompt, state.astype(np.float16).astype(np.float32).tobytes())
+        first = prompt[-1]
+    else:
+        pos, first = 0, None
+        for c in range(0, n_prompt, 64):  # api_stream.rs:58-63 chunked prefill
+            first = eng.forward_token(prompt[c:c + 64], pos)
+            pos += len(prompt[c:c + 64])
     prefill_s = time.perf_counter() - t
-    log(f"[bench] prefill {n_prompt} tokens: {prefill_s * 1e3:.1f} ms")
+    log(f"[bench] {'state restore' if args.synthetic_state else 'prefill'} {n_prompt} tokens: "
+        f"{prefill_s * 1e3:.1f} ms")
     snap = eng.snapshot_resident_cache(n_prompt)
 
     if args.warmup > 0:
@@ -183,8 +193,8 @@ def main():
         "roofline": roof, "cpu_baseline": cpu,
         "decode_hbm_gbs": round(decode_gbs, 1),
         "decode_bytes_per_token": int(wbytes + kvbytes),
-        "prefill_ms": round(prefill_s * 1e3, 1),
-        "prefill_tok_s": round(n_prompt / prefill_s, 1),
+        "prefill_ms": None if args.synthetic_state else round(prefill_s * 1e3, 1),
+        "prefill_tok_s": None if args.synthetic_state else round(n_prompt / prefill_s, 1),
         **extra,
     }
     print(json.dumps(line), flush=True)

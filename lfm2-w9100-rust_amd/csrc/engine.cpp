@@ -71,8 +71,8 @@ extern "C" int lfm_device_count(int *count)
 // ------------------------------------------------------------------ kernels
 struct Kernels {
     hipModule_t mod = nullptr;
-    hipFunction_t matvec, conv, qkv, attn, router, gateup, moe_down, head, advance, dequant,
-        argmax;
+    hipFunction_t matvec, matvec_ks, conv, qkv, attn, attn_merge, router, gateup, moe_down, head,
+        argmax, argmax_final, advance, dequant;
 };
 
 static std::mutex g_kmu;
@@ -114,10 +114,13 @@ static int get_kernels(Kernels **out)
     struct {
         hipFunction_t *f;
         const char *name;
-    } fns[] = {{&k->matvec, "k_q6_matvec"}, {&k->conv, "k_conv_inproj"}, {&k->qkv, "k_qkv"},
-               {&k->attn, "k_attn"},        {&k->router, "k_router"},    {&k->gateup, "k_gateup"},
-               {&k->moe_down, "k_moe_down"}, {&k->head, "k_head"},       {&k->advance, "k_advance"},
-               {&k->dequant, "k_q6_dequant"}, {&k->argmax, "k_argmax"}};
+    } fns[] = {{&k->matvec, "k_q6_matvec"},     {&k->matvec_ks, "k_q6_matvec_ks"},
+               {&k->conv, "k_conv_inproj"},     {&k->qkv, "k_qkv"},
+               {&k->attn, "k_attn"},            {&k->attn_merge, "k_attn_merge"},
+               {&k->router, "k_router"},        {&k->gateup, "k_gateup"},
+               {&k->moe_down, "k_moe_down"},    {&k->head, "k_head"},
+               {&k->argmax, "k_argmax"},        {&k->argmax_final, "k_argmax_final"},
+               {&k->advance, "k_advance"},      {&k->dequant, "k_q6_dequant"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -247,6 +250,23 @@ static uint32_t matvec_grid(uint32_t rows, uint32_t ks)
     return std::max(1u, std::min(groups, 65535u));
 }
 
+// Workgroups (4 waves) for `items` work items at about `per_wave` items per wave.
+static uint32_t wave_grid(uint32_t items, uint32_t per_wave, uint32_t cap = 4096)
+{
+    const uint32_t waves = (items + per_wave - 1) / per_wave;
+    return std::max(1u, std::min((waves + 3) / 4, cap));
+}
+
+// Launches y = W x (mode 0) or y += W x (mode 1): the one-wave-per-row kernel for
+// rows of up to 8 blocks, the split-row kernel for longer rows.
+static int launch_matvec(Kernels *K, MatvecArgs &m, hipStream_t s)
+{
+    if (m.w.nb <= 8)
+        return launch(K->matvec, dim3(wave_grid(m.w.rows, 2)), 0, s, m);
+    RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
+    return launch(K->matvec_ks, dim3(matvec_grid(m.w.rows, m.ksplit)), (m.in_dim + 16) * 4, s, m);
+}
+
 static Q6T q6view(const void *dev, uint64_t rows, uint64_t in_dim)
 {
     Q6T t;
@@ -303,7 +323,7 @@ extern "C" int lfm_q6k_matvec(const void *packed, uint64_t rows, uint64_t in_dim
     RC(matvec_args(packed, rows, in_dim, x, y, &a, &grid));
     Kernels *K;
     RC(get_kernels(&K));
-    RC(launch(K->matvec, dim3(grid), (a.in_dim + 16) * 4, (hipStream_t)stream, a));
+    RC(launch_matvec(K, a, (hipStream_t)stream));
     HIPCHK(hipStreamSynchronize((hipStream_t)stream));
     return LFM_OK;
 }
@@ -325,15 +345,14 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
     const size_t sz = lfm_q6k_nbytes(rows, in_dim);
-    const uint32_t smem = (a.in_dim + 16) * 4;
     for (uint32_t i = 0; i < std::min(iters, ncopies); ++i) { // warm the code path
         a.w.base = (const uint8_t *)packed + (size_t)(i % ncopies) * sz;
-        RC(launch(K->matvec, dim3(grid), smem, s, a));
+        RC(launch_matvec(K, a, s));
     }
     HIPCHK(hipEventRecord(e0, s));
     for (uint32_t i = 0; i < iters; ++i) {
         a.w.base = (const uint8_t *)packed + (size_t)(i % ncopies) * sz;
-        RC(launch(K->matvec, dim3(grid), smem, s, a));
+        RC(launch_matvec(K, a, s));
     }
     HIPCHK(hipEventRecord(e1, s));
     HIPCHK(hipEventSynchronize(e1));
@@ -362,7 +381,10 @@ extern "C" int lfm_argmax(const float *v, uint32_t n, uint32_t *index, float *va
     memset(&h, 0, sizeof(h));
     HIPCHK(hipMemcpy(st, &h, sizeof(h), hipMemcpyHostToDevice));
     ArgmaxArgs a{v, partial, n, st};
+    FinalArgs f{partial, grid, nullptr, 0, st};
     int rc = launch(K->argmax, dim3(grid), 0, nullptr, a);
+    if (rc == LFM_OK)
+        rc = launch(K->argmax_final, dim3(1), 0, nullptr, f);
     if (rc == LFM_OK) {
         HIPCHK(hipDeviceSynchronize());
         HIPCHK(hipMemcpy(&h, st, sizeof(h), hipMemcpyDeviceToHost));
@@ -460,9 +482,11 @@ extern "C" int lfm_engine_create(const lfm_hparams *hp, int device, lfm_engine *
     lfm_engine *e = new lfm_engine();
     e->hp = *hp;
     e->device = device;
+    char name[256] = {0};
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) == hipSuccess)
-        e->devname = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+    if (hipDeviceGetName(name, sizeof(name) - 1, device) == hipSuccess &&
+        hipGetDeviceProperties(&prop, device) == hipSuccess)
+        e->devname = std::string(name) + " (" + prop.gcnArchName + ")";
     int rc = get_kernels(&e->K);
     if (rc == LFM_OK && hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
         rc = fail(LFM_EDEVICE, "hipStreamCreateWithFlags failed");
@@ -571,13 +595,19 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
-    const uint32_t smem = (dim + 16) * 4;
     XSrc src = xsrc(e->x, f32(e, "blk.%u.attn_norm.weight", l), hp.eps);
     if (embed) {
         src.embed = 1;
         src.emb = q6(e, "token_embd.weight");
         src.x_out = e->x;
     }
+    MatvecArgs m;
+    memset(&m, 0, sizeof(m));
+    m.src = xsrc(e->y, nullptr, 0.f);
+    m.y = e->x;
+    m.in_dim = dim;
+    m.mode = 1;
+    m.st = e->st;
     if (kv == 0) {
         ConvInprojArgs a;
         a.w = q6(e, "blk.%u.shortconv.in_proj.weight", l);
@@ -587,17 +617,9 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
         a.y = e->y;
         a.dim = dim;
         a.st = e->st;
-        RC(launch(e->K->conv, dim3(std::max(1u, dim / 4)), smem, e->stream, a));
-        MatvecArgs m;
-        memset(&m, 0, sizeof(m));
+        RC(launch(e->K->conv, dim3(wave_grid(dim, 2)), 0, e->stream, a));
         m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
-        m.src = xsrc(e->y, nullptr, 0.f);
-        m.y = e->x;
-        m.in_dim = dim;
-        m.mode = 1;
-        RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
-        m.st = e->st;
-        RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), smem, e->stream, m));
+        RC(launch_matvec(e->K, m, e->stream));
         e->dispatches += 2;
         return LFM_OK;
     }
@@ -611,7 +633,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     q.dim = dim;
     q.hdkv = hdkv;
     q.st = e->st;
-    RC(launch(e->K->qkv, dim3(std::max(1u, (dim + 2 * hdkv + 3) / 4)), smem, e->stream, q));
+    RC(launch(e->K->qkv, dim3(wave_grid(dim + 2 * hdkv, 2)), 0, e->stream, q));
     AttnArgs at;
     at.qkv = e->qkv;
     at.q_norm = f32(e, "blk.%u.attn_q_norm.weight", l);
@@ -622,24 +644,17 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     at.kcache = e->kc[l];
     at.vcache = e->vc[l];
     at.part = e->apart;
-    at.out = e->y;
     at.ctx = e->ctx;
     at.heads = hp.heads;
     at.kv = kv;
     at.nchunk = e->nchunk;
     at.st = e->st;
     RC(launch(e->K->attn, dim3(e->nchunk, kv), 0, e->stream, at));
-    MatvecArgs m;
-    memset(&m, 0, sizeof(m));
+    AttnMergeArgs mg{e->apart, e->y, hp.heads, kv, e->nchunk, e->st};
+    RC(launch(e->K->attn_merge, dim3(kv), 0, e->stream, mg));
     m.w = q6(e, "blk.%u.attn_output.weight", l);
-    m.src = xsrc(e->y, nullptr, 0.f);
-    m.y = e->x;
-    m.in_dim = dim;
-    m.mode = 1;
-    RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
-    m.st = e->st;
-    RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), smem, e->stream, m));
-    e->dispatches += 3;
+    RC(launch_matvec(e->K, m, e->stream));
+    e->dispatches += 4;
     return LFM_OK;
 }
 
@@ -647,19 +662,17 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim;
-    const uint32_t smem = (dim + 16) * 4;
     XSrc src = xsrc(e->x, f32(e, "blk.%u.ffn_norm.weight", l), hp.eps);
+    GateUpArgs g;
+    memset(&g, 0, sizeof(g));
+    g.src = src;
+    g.sw = e->sw;
+    g.st = e->st;
     if (l < hp.dense_lead) {
-        GateUpArgs g;
         g.wg = q6(e, "blk.%u.ffn_gate.weight", l);
         g.wu = q6(e, "blk.%u.ffn_up.weight", l);
-        g.src = src;
-        g.sel = nullptr;
-        g.sw = e->sw;
         g.ff = hp.n_ff;
-        g.n_used = 1;
-        g.st = e->st;
-        RC(launch(e->K->gateup, dim3(std::max(1u, hp.n_ff / 4)), smem, e->stream, g));
+        RC(launch(e->K->gateup, dim3(wave_grid(hp.n_ff, 2)), 0, e->stream, g));
         MatvecArgs m;
         memset(&m, 0, sizeof(m));
         m.w = q6(e, "blk.%u.ffn_down.weight", l);
@@ -667,44 +680,40 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
         m.y = e->x;
         m.in_dim = hp.n_ff;
         m.mode = 1;
-        RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
         m.st = e->st;
-        RC(launch(e->K->matvec, dim3(matvec_grid(m.w.rows, m.ksplit)), (hp.n_ff + 16) * 4, e->stream,
-                  m));
+        RC(launch_matvec(e->K, m, e->stream));
         e->dispatches += 2;
         return LFM_OK;
     }
     RouterArgs r;
     r.src = src;
     r.w = f32(e, "blk.%u.ffn_gate_inp.weight", l);
-    r.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
     r.logits = e->rlogits;
-    r.sel = e->sel;
     r.dim = dim;
     r.n_expert = hp.n_expert;
-    r.n_used = hp.n_used;
     r.st = e->st;
-    RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), smem, e->stream, r));
-    GateUpArgs g;
+    RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), 0, e->stream, r));
+    Route route;
+    route.logits = e->rlogits;
+    route.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
+    route.n_expert = hp.n_expert;
+    route.n_used = hp.n_used;
+    route.sel_out = e->sel;
     g.wg = q6(e, "blk.%u.ffn_gate_exps.weight", l);
     g.wu = q6(e, "blk.%u.ffn_up_exps.weight", l);
-    g.src = src;
-    g.sel = e->sel;
-    g.sw = e->sw;
+    g.route = route;
     g.ff = hp.expert_ff;
-    g.n_used = hp.n_used;
-    g.st = e->st;
-    RC(launch(e->K->gateup, dim3(std::max(1u, hp.n_used * hp.expert_ff / 4)), smem, e->stream, g));
+    RC(launch(e->K->gateup, dim3(wave_grid(hp.n_used * hp.expert_ff, 2)), 0, e->stream, g));
     MoeDownArgs d;
     d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
     d.sw = e->sw;
-    d.sel = e->sel;
+    d.route = route;
+    d.route.sel_out = nullptr;
     d.x = e->x;
     d.dim = dim;
     d.ff = hp.expert_ff;
-    d.n_used = hp.n_used;
     d.st = e->st;
-    RC(launch(e->K->moe_down, dim3(std::max(1u, dim / 2)), 0, e->stream, d));
+    RC(launch(e->K->moe_down, dim3(std::max(1u, std::min((dim + 7) / 8, 4096u))), 0, e->stream, d));
     e->dispatches += 3;
     return LFM_OK;
 }
@@ -716,12 +725,12 @@ static int enq_head(lfm_engine *e, uint32_t advance)
     h.src = xsrc(e->x, f32(e, "token_embd_norm.weight"), e->hp.eps);
     h.logits = e->logits;
     h.partial = e->hpart;
-    h.out_tokens = e->out_tokens;
     h.vocab = e->hp.vocab;
-    h.advance = advance;
     h.st = e->st;
-    RC(launch(e->K->head, dim3(e->head_grid), (e->hp.dim + 16) * 4, e->stream, h));
-    e->dispatches += 1;
+    RC(launch(e->K->head, dim3(e->head_grid), 0, e->stream, h));
+    FinalArgs f{e->hpart, e->head_grid, e->out_tokens, advance, e->st};
+    RC(launch(e->K->argmax_final, dim3(1), 0, e->stream, f));
+    e->dispatches += 2;
     return LFM_OK;
 }
 
@@ -793,7 +802,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     for (uint32_t l = 0; l < hp.n_layers; ++l)
         max_hdkv = std::max(max_hdkv, 64 * hp.kv_heads[l]);
     e->nchunk = (e->ctx + 127) / 128;
-    e->head_grid = std::max(1u, std::min(1024u, (hp.vocab + 63) / 64));
+    e->head_grid = wave_grid(hp.vocab, 16, 1024);
     e->tscale = powf(hp.rope_theta, -2.0f / (float)hp.head_dim);
     const size_t swn = std::max<size_t>((size_t)hp.n_ff, (size_t)hp.n_used * hp.expert_ff);
     HIPCHK(hipMalloc(&e->st, sizeof(DevState)));
@@ -874,7 +883,7 @@ static int need_final(lfm_engine *e)
     return LFM_OK;
 }
 
-// Writes the host-controlled head of DevState (counters are left alone).
+// Writes the device-resident decode state.
 static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, uint32_t eos)
 {
     DevState h;
@@ -886,7 +895,7 @@ static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, 
     h.eos = eos;
     h.cursor = 0;
     h.n_ids = n_ids;
-    HIPCHK(hipMemcpyAsync(e->st, &h, offsetof(DevState, counters), hipMemcpyHostToDevice, e->stream));
+    HIPCHK(hipMemcpyAsync(e->st, &h, sizeof(DevState), hipMemcpyHostToDevice, e->stream));
     return LFM_OK;
 }
 

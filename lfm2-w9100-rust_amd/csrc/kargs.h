@@ -30,14 +30,8 @@ struct DevState {
     uint32_t n_ids;     // prompt length in ids
     uint32_t last_token;
     float last_value;
-    uint32_t pad[7];
-    uint32_t counters[64]; // last-workgroup counters (each kernel resets its own)
+    uint32_t pad[7];    // 64 bytes
 };
-
-#define LFM_CNT_ROUTER 0
-#define LFM_CNT_HEAD 1
-#define LFM_CNT_ARGMAX 2
-#define LFM_CNT_ATTN 8 // 8 .. 8+kv-1
 
 // Where a kernel's input vector comes from.
 struct XSrc {
@@ -55,8 +49,8 @@ struct MatvecArgs {      // y = W x  (mode 0)  or  y += W x  (mode 1)
     float *y;
     uint32_t in_dim;
     uint32_t mode;
-    uint32_t ksplit;     // waves per row (1, 2 or 4)
-    uint32_t nbw;        // blocks per wave
+    uint32_t ksplit;     // k_q6_matvec_ks: waves per row (1, 2 or 4)
+    uint32_t nbw;        // k_q6_matvec_ks: blocks per wave
     DevState *st;        // nullable
 };
 
@@ -83,48 +77,74 @@ struct AttnArgs {
     const float *q_norm, *k_norm;
     float eps, tscale, scale;
     uint16_t *kcache, *vcache; // [kv][ctx][64] binary16
-    float *part;               // [kv][nchunk][G][66]
-    float *out;                // [heads*64]
+    float *part;               // [kv][nchunk][4][66]: max, sum, o[64]
     uint32_t ctx, heads, kv, nchunk;
     DevState *st;
 };
 
+struct AttnMergeArgs {
+    const float *part;
+    float *out;                // [heads*64]
+    uint32_t heads, kv, nchunk;
+    DevState *st;
+};
+
+// Router logits of the MoE layer; the top-k itself is taken by every consumer
+// wave from these logits (identical result everywhere, no cross-workgroup sync).
 struct RouterArgs {
     XSrc src;
     const float *w;      // [n_expert][dim] f32
-    const float *bias;   // [n_expert]
-    float *logits;       // [n_expert] scratch
-    uint32_t *sel;       // ids[8] then weights[8] (as float bits)
-    uint32_t dim, n_expert, n_used;
+    float *logits;       // [n_expert]
+    uint32_t dim, n_expert;
     DevState *st;
+};
+
+struct Route {
+    const float *logits; // nullptr = dense layer
+    const float *bias;
+    uint32_t n_expert, n_used;
+    uint32_t *sel_out;   // written by one wave: ids[8] then weights[8] (float bits)
 };
 
 struct GateUpArgs {      // sw = silu(Wg h) * (Wu h), dense or routed
     Q6T wg, wu;
     XSrc src;
-    const uint32_t *sel; // nullptr = dense
+    Route route;
     float *sw;           // [n_used][ff] or [ff]
-    uint32_t ff, n_used;
+    uint32_t ff;
     DevState *st;
 };
 
 struct MoeDownArgs {     // x[k] += sum_r w_r * (Wd[e_r] sw_r)[k]
     Q6T wd;              // rows n_expert*dim
     const float *sw;     // [n_used][ff]
-    const uint32_t *sel;
+    Route route;
     float *x;
-    uint32_t dim, ff, n_used;
+    uint32_t dim, ff;
     DevState *st;
 };
 
-struct HeadArgs {        // logits = E rmsnorm(x), fused greedy argmax
+struct HeadArgs {        // logits = E rmsnorm(x), per-workgroup greedy argmax partials
     Q6T emb;
     XSrc src;
     float *logits;       // [vocab]
     float *partial;      // [grid][2]
-    uint32_t *out_tokens;
     uint32_t vocab;
-    uint32_t advance;    // 1: decode step (store token, feed it back, pos++)
+    DevState *st;
+};
+
+struct ArgmaxArgs {      // per-workgroup argmax partials of a plain vector
+    const float *v;
+    float *partial;
+    uint32_t n;
+    DevState *st;
+};
+
+struct FinalArgs {       // reduce partials; decode step: store, feed back, advance
+    const float *partial;
+    uint32_t n_partial;
+    uint32_t *out_tokens;
+    uint32_t advance;
     DevState *st;
 };
 
@@ -137,11 +157,4 @@ struct DequantArgs {
     Q6T w;
     float *out;
     uint32_t in_dim;
-};
-
-struct ArgmaxArgs {
-    const float *v;
-    float *partial;
-    uint32_t n;
-    DevState *st;
 };

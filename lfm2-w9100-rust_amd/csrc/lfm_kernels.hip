@@ -177,102 +177,303 @@ __device__ __forceinline__ uint32_t lane_pos(uint32_t b, uint32_t c, int s, int 
     return b * 256 + (c >> 2) * 128 + s * 32 + (c & 3) * 8 + i;
 }
 
-// ------------------------------------------------------------ input staging
-// Copies (or, for the first kernel of a step, dequantizes the embedding row of
-// DevState::tok into) LDS and applies RMSNorm in place:
-// x * (1 / sqrt(sum x^2 / n + eps)) * w  (lfm.rs:231-244).
-// Every workgroup computes the same sum in the same order.
-__device__ void stage_x(const XSrc &src, float *xs, uint32_t n, const DevState *st, float *red)
+// ------------------------------------------------------------ input vector
+// A wave holds the input vector in registers: lane (b, c) owns the 32 values
+// at lane_pos(b, c, s, i), i.e. exactly the positions its Q6_K chunk multiplies.
+// RMSNorm x * (1 / sqrt(sum x^2 / n + eps)) * w (lfm.rs:231-244) is a wave
+// reduction, identical in every wave.  For the first kernel of a step the
+// vector is the dequantized embedding row DevState::tok (lfm.rs:310-320); wave
+// 0 of workgroup 0 also stores it as the residual.
+__device__ __forceinline__ void wave_x(const XSrc &src, uint32_t nb, const DevState *st, LaneX &X,
+                                       bool writer)
 {
-    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63, b = lane >> 3, c = lane & 7;
+    const bool active = b < nb;
+    const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+        v[i] = 0.f;
     if (src.embed) {
-        const uint32_t tok = st->tok;
-        for (uint32_t u = tid; u < n / 32; u += WG_THREADS) {
-            const uint32_t b = u >> 3, c = u & 7;
-            float v[32];
-            lane_dequant(load_lane(src.emb, tok, b, c), v);
+        if (active) {
+            lane_dequant(load_lane(src.emb, st->tok, b, c), v);
+            if (writer && src.x_out)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+                for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    xs[lane_pos(b, c, s, i)] = v[s * 8 + i];
+                    for (int i = 0; i < 8; ++i)
+                        src.x_out[base + s * 32 + i] = v[s * 8 + i];
         }
-        __syncthreads();
-        if (blockIdx.x == 0 && blockIdx.y == 0 && src.x_out)
-            for (uint32_t i = tid; i < n; i += WG_THREADS)
-                src.x_out[i] = xs[i];
-    } else {
-        for (uint32_t i = tid * 4; i < n; i += WG_THREADS * 4)
-            *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(src.x + i);
-        __syncthreads();
+    } else if (active) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4 a = *reinterpret_cast<const float4 *>(src.x + base + s * 32);
+            const float4 bb = *reinterpret_cast<const float4 *>(src.x + base + s * 32 + 4);
+            v[s * 8 + 0] = a.x, v[s * 8 + 1] = a.y, v[s * 8 + 2] = a.z, v[s * 8 + 3] = a.w;
+            v[s * 8 + 4] = bb.x, v[s * 8 + 5] = bb.y, v[s * 8 + 6] = bb.z, v[s * 8 + 7] = bb.w;
+        }
     }
     if (src.norm_w) {
         float ss = 0.f;
-        for (uint32_t i = tid; i < n; i += WG_THREADS)
-            ss += xs[i] * xs[i];
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            ss += v[i] * v[i];
         ss = wave_sum(ss);
-        if ((tid & 63) == 0)
-            red[tid >> 6] = ss;
-        __syncthreads();
-        const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-        const float inv = 1.0f / sqrtf(tot / (float)n + src.eps);
-        __syncthreads();
-        for (uint32_t i = tid; i < n; i += WG_THREADS)
-            xs[i] = xs[i] * inv * src.norm_w[i];
-        __syncthreads();
+        const float inv = 1.0f / sqrtf(ss / (float)(nb * 256) + src.eps);
+        if (active) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const float4 a = *reinterpret_cast<const float4 *>(src.norm_w + base + s * 32);
+                const float4 bb = *reinterpret_cast<const float4 *>(src.norm_w + base + s * 32 + 4);
+                const float w8[8] = {a.x, a.y, a.z, a.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    v[s * 8 + i] = v[s * 8 + i] * inv * w8[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            X.v[s * 8 + i] = v[s * 8 + i];
+            t += v[s * 8 + i];
+        }
+        X.s32[s] = 32.f * t;
     }
 }
 
+// Sums two per-lane partials across the wave (results in every lane).
+__device__ __forceinline__ void wave_sum2(float &a, float &b)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off, 64);
+        b += __shfl_xor(b, off, 64);
+    }
+}
+
+__device__ __forceinline__ void wave_sum3(float &a, float &b, float &c)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off, 64);
+        b += __shfl_xor(b, off, 64);
+        c += __shfl_xor(c, off, 64);
+    }
+}
+
+// MoE routing of one token (lfm.rs:613-637, resident.rs:58-99), computed by a
+// whole wave from the router logits: sigmoid probabilities, score = p + bias,
+// n_used rounds of (max score, then lowest id among equals), weights
+// p / max(sum in rank order, 2^-14).  The results are wave-uniform and kept in
+// scalar registers (no small arrays: dynamically indexed ones end up in memory).
+struct Routed {
+    uint32_t id0, id1, id2, id3;
+    float w0, w1, w2, w3;
+    __device__ __forceinline__ uint32_t id(uint32_t k) const
+    {
+        return k == 0 ? id0 : k == 1 ? id1 : k == 2 ? id2 : id3;
+    }
+    __device__ __forceinline__ float w(uint32_t k) const
+    {
+        return k == 0 ? w0 : k == 1 ? w1 : k == 2 ? w2 : w3;
+    }
+};
+
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+__device__ __forceinline__ float uniform_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+__device__ __forceinline__ Routed wave_route(const Route &r)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    float prob = 0.f, score = -INFINITY;
+    if (lane < r.n_expert) {
+        const float lg = r.logits[lane];
+        prob = 1.0f / (1.0f + expf(-lg));
+        score = prob + r.bias[lane];
+    }
+    uint32_t id[4];
+    float p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        id[k] = 0;
+        p[k] = 0.f;
+        if ((uint32_t)k < r.n_used) {
+            const float best = wave_max(score);
+            const uint32_t cand = (lane < r.n_expert && score == best) ? lane : 0xFFFFFFFFu;
+            uint32_t e = wave_min_u32(cand);
+            if (e >= r.n_expert) // only with NaN logits: fall back to a valid expert
+                e = 0;
+            id[k] = uniform_u32(e);
+            p[k] = uniform_f32(__shfl(prob, (int)e, 64));
+            if (lane == e)
+                score = -INFINITY;
+        }
+    }
+    float wsum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if ((uint32_t)k < r.n_used)
+            wsum = wsum + p[k];
+    if (wsum < 6.103515625e-5f)
+        wsum = 6.103515625e-5f;
+    Routed o;
+    o.id0 = id[0], o.id1 = id[1], o.id2 = id[2], o.id3 = id[3];
+    o.w0 = p[0] / wsum, o.w1 = p[1] / wsum, o.w2 = p[2] / wsum, o.w3 = p[3] / wsum;
+    return o;
+}
+
+// Double-buffered streaming of one wave's work items.  The wave's items are
+// it = first + k*W (k = 0, 1, ...) below `total`; each item is NR Q6_K rows.
+// Two groups of G items are in flight: group A is reduced while group B's loads
+// are outstanding, then A is refilled, so the wave keeps up to 2*G items of
+// weights in flight without copying registers between iterations (a copy
+// would force a wait for the loads just issued).  `prologue` runs after the
+// first loads are issued (it builds the input vector meanwhile).
+template <int NR> struct Item {
+    Lane l[NR];
+};
+
+template <int NR, int G, typename LoadF, typename PrologueF, typename UseF>
+__device__ __forceinline__ void stream_items(uint32_t first, uint32_t W, uint32_t total, LoadF load,
+                                             PrologueF prologue, UseF use)
+{
+    Item<NR> A[G], B[G];
+    const uint32_t nitems = first < total ? (total - first + W - 1) / W : 0;
+    const uint32_t ngroups = (nitems + G - 1) / G;
+    auto fill = [&](Item<NR> *buf, uint32_t g) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const uint32_t k = g * G + j;
+            if (k < nitems)
+                load(first + k * W, buf[j]);
+        }
+    };
+    if (ngroups > 0)
+        fill(A, 0);
+    if (ngroups > 1)
+        fill(B, 1);
+    prologue();
+    for (uint32_t g = 0; g < ngroups; g += 2) {
+        use(A, g * G, nitems);
+        if (g + 2 < ngroups)
+            fill(A, g + 2);
+        if (g + 1 < ngroups) {
+            use(B, (g + 1) * G, nitems);
+            if (g + 3 < ngroups)
+                fill(B, g + 3);
+        }
+    }
+}
+
+// Wave sum of N per-lane values at once (results in every lane).
+template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            v[i] += __shfl_xor(v[i], off, 64);
+}
+
 // ------------------------------------------------------------------ kernels
-// Generic Q6_K matvec: y = W x or y += W x, x optionally RMS-normed.  ksplit
-// waves share a row (nbw blocks each, combined in LDS in wave order).
+// Q6_K matvec y = W x (mode 0) or y += W x (mode 1), rows of up to 8 blocks:
+// one wave per row, rows streamed two at a time with two more in flight.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec(const MatvecArgs a)
+{
+    if (a.st && a.st->halt)
+        return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t b = lane >> 3, c = lane & 7;
+    const bool active = b < a.w.nb;
+    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    LaneX X;
+    stream_items<1, 2>(
+        first, W, a.w.rows,
+        [&](uint32_t r, Item<1> &it) {
+            if (active)
+                it.l[0] = load_lane(a.w, r, b, c);
+        },
+        [&]() { wave_x(a.src, a.w.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
+        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
+            float p[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
+            wave_sum_n<2>(p);
+            if (lane == 0)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    if (k0 + j < n) {
+                        const uint32_t r = first + (k0 + j) * W;
+                        a.y[r] = a.mode ? a.y[r] + p[j] : p[j];
+                    }
+        });
+}
+
+// Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
+// `ksplit` waves share a row (nbw blocks each); x staged in LDS; partials
+// combined in wave order.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const MatvecArgs a)
 {
     if (a.st && a.st->halt)
         return;
     extern __shared__ float smem[];
     float *xs = smem;
     float *red = smem + a.in_dim;
-    stage_x(a.src, xs, a.in_dim, a.st, red);
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t ks = a.ksplit, rpi = 4 / ks;
     const uint32_t slot = wave / ks, kp = wave % ks;
     const uint32_t bslot = lane >> 3, c = lane & 7;
     const uint32_t b = kp * a.nbw + bslot;
     const bool active = bslot < a.nbw && b < a.w.nb;
+    const uint32_t rows = a.w.rows;
+    const uint32_t ngroups = (rows + rpi - 1) / rpi;
+    uint32_t g = blockIdx.x;
+    Lane cur;
+    if (active && g < ngroups && g * rpi + slot < rows)
+        cur = load_lane(a.w, g * rpi + slot, b, c);
+    for (uint32_t i = tid * 4; i < a.in_dim; i += WG_THREADS * 4)
+        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.src.x + i);
+    __syncthreads();
     LaneX X;
     if (active)
         load_lanex(X, xs, b, c);
     else
         zero_lanex(X);
-    const uint32_t rows = a.w.rows;
-    const uint32_t ngroups = (rows + rpi - 1) / rpi;
-    for (uint32_t g = blockIdx.x; g < ngroups; g += gridDim.x) {
+    for (; g < ngroups; g += gridDim.x) {
         const uint32_t row = g * rpi + slot;
-        float p = 0.f;
-        if (active && row < rows)
-            p = lane_dot(load_lane(a.w, row, b, c), X);
+        const uint32_t gn = g + gridDim.x, rown = gn * rpi + slot;
+        Lane nxt;
+        if (active && gn < ngroups && rown < rows)
+            nxt = load_lane(a.w, rown, b, c);
+        float p = (active && row < rows) ? lane_dot(cur, X) : 0.f;
         p = wave_sum(p);
-        if (ks == 1) {
-            if (lane == 0 && row < rows)
-                a.y[row] = a.mode ? a.y[row] + p : p;
-        } else {
-            if (lane == 0)
-                red[8 + wave] = p;
-            __syncthreads();
-            if (kp == 0 && lane == 0 && row < rows) {
-                float s = 0.f;
-                for (uint32_t k = 0; k < ks; ++k)
-                    s += red[8 + slot * ks + k];
-                a.y[row] = a.mode ? a.y[row] + s : s;
-            }
-            __syncthreads();
+        if (lane == 0)
+            red[wave] = p;
+        __syncthreads();
+        if (kp == 0 && lane == 0 && row < rows) {
+            float s = 0.f;
+            for (uint32_t k = 0; k < ks; ++k)
+                s += red[slot * ks + k];
+            a.y[row] = a.mode ? a.y[row] + s : s;
         }
+        __syncthreads();
+        cur = nxt;
     }
 }
 
-// Short-conv block, decode (lfm.rs:450-533 for n = 1): one wave per channel
-// computes the in_proj rows B[ch], C[ch], X[ch], then
+// Short-conv block, decode (lfm.rs:450-533 for n = 1): the wave of channel ch
+// computes in_proj rows B[ch], C[ch], X[ch] of the normed input, then
 //   bx = B*X; co = ((0 + s0*w0) + s1*w1) + bx*w2; y = C*co; state = (s1, bx)
 // in the reference's operation order with no contraction.
 __device__ __forceinline__ void conv_step(float B, float C, float Xv, const float *w3, float *s2,
@@ -294,70 +495,74 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_inproj(const Con
 {
     if (a.st->halt)
         return;
-    extern __shared__ float smem[];
-    float *xs = smem;
-    float *red = smem + a.dim;
-    stage_x(a.src, xs, a.dim, a.st, red);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
+    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave, dim = a.dim;
     LaneX X;
-    if (active)
-        load_lanex(X, xs, b, c);
-    else
-        zero_lanex(X);
-    const uint32_t dim = a.dim;
-    for (uint32_t ch = blockIdx.x * 4 + wave; ch < dim; ch += gridDim.x * 4) {
-        float pb = 0.f, pc = 0.f, px = 0.f;
-        if (active) {
-            const Lane wb = load_lane(a.w, ch, b, c);
-            const Lane wc = load_lane(a.w, dim + ch, b, c);
-            const Lane wx = load_lane(a.w, 2 * dim + ch, b, c);
-            pb = lane_dot(wb, X);
-            pc = lane_dot(wc, X);
-            px = lane_dot(wx, X);
-        }
-        pb = wave_sum(pb);
-        pc = wave_sum(pc);
-        px = wave_sum(px);
-        if (lane == 0)
-            conv_step(pb, pc, px, a.conv_w + ch * 3, a.state + ch * 2, a.y + ch);
-    }
+    stream_items<3, 1>(
+        first, W, dim,
+        [&](uint32_t ch, Item<3> &it) {
+            if (active) {
+                it.l[0] = load_lane(a.w, ch, b, c);
+                it.l[1] = load_lane(a.w, dim + ch, b, c);
+                it.l[2] = load_lane(a.w, 2 * dim + ch, b, c);
+            }
+        },
+        [&]() { wave_x(a.src, a.w.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
+        [&](Item<3> *buf, uint32_t k0, uint32_t n) {
+            float p[3] = {0.f, 0.f, 0.f};
+            if (active && k0 < n)
+#pragma unroll
+                for (int j = 0; j < 3; ++j)
+                    p[j] = lane_dot(buf[0].l[j], X);
+            wave_sum_n<3>(p);
+            if (lane == 0 && k0 < n) {
+                const uint32_t ch = first + k0 * W;
+                conv_step(p[0], p[1], p[2], a.conv_w + ch * 3, a.state + ch * 2, a.y + ch);
+            }
+        });
 }
 
-// Attention projections q (dim rows), k and v (hdkv rows each) of the normed
-// input, written raw to qkv[0..dim+2*hdkv).
+// Attention projections: rows of q (dim), k and v (hdkv each) of the normed
+// input, written raw to qkv[0 .. dim + 2*hdkv).
+__device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t b, uint32_t c)
+{
+    if (r < a.dim)
+        return load_lane(a.wq, r, b, c);
+    if (r < a.dim + a.hdkv)
+        return load_lane(a.wk, r - a.dim, b, c);
+    return load_lane(a.wv, r - a.dim - a.hdkv, b, c);
+}
+
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_qkv(const QkvArgs a)
 {
     if (a.st->halt)
         return;
-    extern __shared__ float smem[];
-    float *xs = smem;
-    float *red = smem + a.dim;
-    stage_x(a.src, xs, a.dim, a.st, red);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wq.nb;
+    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
     LaneX X;
-    if (active)
-        load_lanex(X, xs, b, c);
-    else
-        zero_lanex(X);
-    const uint32_t total = a.dim + 2 * a.hdkv;
-    for (uint32_t r = blockIdx.x * 4 + wave; r < total; r += gridDim.x * 4) {
-        float p = 0.f;
-        if (active) {
-            if (r < a.dim)
-                p = lane_dot(load_lane(a.wq, r, b, c), X);
-            else if (r < a.dim + a.hdkv)
-                p = lane_dot(load_lane(a.wk, r - a.dim, b, c), X);
-            else
-                p = lane_dot(load_lane(a.wv, r - a.dim - a.hdkv, b, c), X);
-        }
-        p = wave_sum(p);
-        if (lane == 0)
-            a.qkv[r] = p;
-    }
+    stream_items<1, 2>(
+        first, W, a.dim + 2 * a.hdkv,
+        [&](uint32_t r, Item<1> &it) {
+            if (active)
+                it.l[0] = qkv_lane(a, r, b, c);
+        },
+        [&]() { wave_x(a.src, a.wq.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
+        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
+            float p[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
+            wave_sum_n<2>(p);
+            if (lane == 0)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    if (k0 + j < n)
+                        a.qkv[first + (k0 + j) * W] = p[j];
+        });
 }
 
 // Per-head RMSNorm then NEOX RoPE of one 64-wide head held one value per lane
@@ -391,11 +596,11 @@ __device__ __forceinline__ float head_norm_rope(float v, const float *w, float e
     return d < 32 ? v * cs - other * sn : other * sn + v * cs;
 }
 
-// Split-K decode attention over the binary16 KV cache, one workgroup per
-// (position chunk of 128, kv head); the G = heads/kv query heads of a kv head
-// share the K/V reads.  The workgroup holding the current position also
-// normalizes, rotates, rounds and stores the new K/V row.  Partials
-// (max, sum, o[64]) are merged by the last workgroup of each kv head.
+// Split-K decode attention over the binary16 KV cache (lfm.rs:395-437): one
+// workgroup per (chunk of 128 positions, kv head); the G = heads/kv query heads
+// of a kv head share the K/V reads.  The workgroup holding the current position
+// normalizes, rotates, rounds (RNE) and stores the new K/V row.  Each workgroup
+// writes (max, sum, o[64]) per head; k_attn_merge combines the chunks.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a)
 {
     if (a.st->halt)
@@ -418,8 +623,29 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     __shared__ __attribute__((aligned(16))) uint16_t Vs[ATT_CH * 64];
     __shared__ float sc[4][ATT_CH];
     __shared__ float stat[4][2];
-    __shared__ uint32_t s_last;
 
+    // K/V rows of this chunk -> LDS (16 B per thread per pass), issued first.
+    const uint16_t *kg = a.kcache + ((size_t)kh * a.ctx + t0) * 64;
+    const uint16_t *vg = a.vcache + ((size_t)kh * a.ctx + t0) * 64;
+    {
+        constexpr int PASSES = ATT_CH * 8 / WG_THREADS; // 16-B pieces per thread
+        uint4 kr[PASSES], vr[PASSES];
+#pragma unroll
+        for (int i = 0; i < PASSES; ++i) { // rows past the chunk re-read row 0 (unused)
+            const uint32_t u = tid + i * WG_THREADS, seg = u & 7;
+            const uint32_t t = (u >> 3) < nt ? (u >> 3) : 0;
+            kr[i] = *reinterpret_cast<const uint4 *>(kg + t * 64 + seg * 8);
+            vr[i] = *reinterpret_cast<const uint4 *>(vg + t * 64 + seg * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < PASSES; ++i) {
+            const uint32_t u = tid + i * WG_THREADS, t = u >> 3, seg = u & 7;
+            if (t < nt && t0 + t != p) {
+                *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) = kr[i];
+                *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) = vr[i];
+            }
+        }
+    }
     if (wave < G) {
         const float v = a.qkv[(kh * G + wave) * 64 + lane];
         qr[wave][lane] = head_norm_rope(v, a.q_norm, a.eps, a.tscale, p, lane);
@@ -433,18 +659,6 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
         a.vcache[((size_t)kh * a.ctx + p) * 64 + lane] = vb;
         knew[lane] = half_bits_to_float(kb);
         vnew[lane] = half_bits_to_float(vb);
-    }
-    // K/V rows of this chunk -> LDS (16 B per thread per pass).
-    const uint16_t *kg = a.kcache + ((size_t)kh * a.ctx + t0) * 64;
-    const uint16_t *vg = a.vcache + ((size_t)kh * a.ctx + t0) * 64;
-    for (uint32_t u = tid; u < nt * 8; u += WG_THREADS) {
-        const uint32_t t = u >> 3, seg = u & 7;
-        if (t0 + t != p) {
-            *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) =
-                *reinterpret_cast<const uint4 *>(kg + t * 64 + seg * 8);
-            *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) =
-                *reinterpret_cast<const uint4 *>(vg + t * 64 + seg * 8);
-        }
     }
     __syncthreads();
     // scores: thread -> position t, heads 2*hp and 2*hp+1
@@ -492,159 +706,145 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     }
     __syncthreads();
     const uint32_t hh = tid >> 6, d = tid & 63;
-    float *part = a.part + (((size_t)kh * a.nchunk + chunk) * 4 + hh) * 66;
     if (hh < G) {
         float acc = 0.f;
         for (uint32_t t = 0; t < nt; ++t) {
             const float vv = (t0 + t == p) ? vnew[d] : half_bits_to_float(Vs[t * 64 + d]);
             acc += sc[hh][t] * vv;
         }
+        float *part = a.part + (((size_t)kh * a.nchunk + chunk) * 4 + hh) * 66;
         part[2 + d] = acc;
         if (d == 0) {
             part[0] = stat[hh][0];
             part[1] = stat[hh][1];
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.st->counters[LFM_CNT_ATTN + kh], 1u);
-        s_last = (prev == nact - 1);
-    }
-    __syncthreads();
-    if (!s_last)
-        return;
-    __threadfence();
-    if (hh < G) {
-        const float *pb = a.part + ((size_t)kh * a.nchunk * 4 + hh) * 66;
-        float M = -INFINITY;
-        for (uint32_t cc = 0; cc < nact; ++cc)
-            M = fmaxf(M, __builtin_nontemporal_load(pb + (size_t)cc * 4 * 66));
-        float acc = 0.f, L = 0.f;
-        for (uint32_t cc = 0; cc < nact; ++cc) {
-            const float *pc = pb + (size_t)cc * 4 * 66;
-            const float f = expf(__builtin_nontemporal_load(pc) - M);
-            L += f * __builtin_nontemporal_load(pc + 1);
-            acc += f * __builtin_nontemporal_load(pc + 2 + d);
-        }
-        a.out[(kh * G + hh) * 64 + d] = acc / L;
-    }
-    if (tid == 0)
-        a.st->counters[LFM_CNT_ATTN + kh] = 0;
 }
 
-// MoE router (lfm.rs:599-637): logits = W_r h (f32), then the last workgroup
-// takes sigmoid probabilities, score = p + bias, the top n_used by score with
-// ties to the lower id (max score, then min id), weights p / max(sum, 2^-14).
+// Combines the chunk partials of each head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge(const AttnMergeArgs a)
+{
+    if (a.st->halt)
+        return;
+    const uint32_t kh = blockIdx.x, hh = threadIdx.x >> 6, d = threadIdx.x & 63;
+    const uint32_t G = a.heads / a.kv;
+    if (hh >= G)
+        return;
+    const uint32_t nact = a.st->pos / ATT_CH + 1;
+    const float *pb = a.part + ((size_t)kh * a.nchunk * 4 + hh) * 66;
+    float M = -INFINITY, acc = 0.f, L = 0.f;
+    for (uint32_t c0 = 0; c0 < nact; c0 += 8) { // 8 chunks' loads in flight
+        float m[8], l[8], o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float *pc = pb + (size_t)(c0 + j) * 4 * 66;
+            const bool ok = c0 + j < nact;
+            m[j] = ok ? pc[0] : -INFINITY;
+            l[j] = ok ? pc[1] : 0.f;
+            o[j] = ok ? pc[2 + d] : 0.f;
+        }
+        float mn = M;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            mn = fmaxf(mn, m[j]);
+        const float r = expf(M - mn); // rescale the running sums (M = -inf first: 0)
+        acc *= r;
+        L *= r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float f = expf(m[j] - mn);
+            L += f * l[j];
+            acc += f * o[j];
+        }
+        M = mn;
+    }
+    a.out[(kh * G + hh) * 64 + d] = acc / L;
+}
+
+// MoE router logits W_r h (f32 weights [n_expert][dim], lfm.rs:599-607): one
+// wave per expert row.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router(const RouterArgs a)
 {
     if (a.st->halt)
         return;
-    extern __shared__ float smem[];
-    float *xs = smem;
-    float *red = smem + a.dim;
-    __shared__ uint32_t s_last;
-    stage_x(a.src, xs, a.dim, a.st, red);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t b = lane >> 3, c = lane & 7, nb = a.dim / 256;
     const uint32_t e = blockIdx.x * 4 + wave;
-    if (e < a.n_expert) {
-        const float *w = a.w + (size_t)e * a.dim;
-        float acc = 0.f;
-        for (uint32_t k = lane * 4; k < a.dim; k += 256) {
-            const float4 wv = *reinterpret_cast<const float4 *>(w + k);
-            acc += wv.x * xs[k] + wv.y * xs[k + 1] + wv.z * xs[k + 2] + wv.w * xs[k + 3];
-        }
-        acc = wave_sum(acc);
-        if (lane == 0)
-            a.logits[e] = acc;
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.st->counters[LFM_CNT_ROUTER], 1u);
-        s_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!s_last)
+    if (e >= a.n_expert)
         return;
-    __threadfence();
-    if (wave == 0) {
-        float prob = 0.f, score = -INFINITY;
-        if (lane < a.n_expert) {
-            const float lg = __builtin_nontemporal_load(a.logits + lane);
-            prob = 1.0f / (1.0f + expf(-lg));
-            score = prob + a.bias[lane];
-        }
-        float psel[8];
-        uint32_t ids[8];
-        for (uint32_t r = 0; r < a.n_used; ++r) {
-            const float best = wave_max(score);
-            const uint32_t cand = (lane < a.n_expert && score == best) ? lane : 0xFFFFFFFFu;
-            const uint32_t id = wave_min_u32(cand);
-            ids[r] = id;
-            psel[r] = __shfl(prob, (int)id, 64);
-            if (lane == id)
-                score = -INFINITY;
-        }
-        if (lane == 0) {
-            float wsum = 0.f;
-            for (uint32_t r = 0; r < a.n_used; ++r)
-                wsum = wsum + psel[r];
-            if (wsum < 6.103515625e-5f)
-                wsum = 6.103515625e-5f;
-            for (uint32_t r = 0; r < a.n_used; ++r) {
-                a.sel[r] = ids[r];
-                a.sel[8 + r] = __float_as_uint(psel[r] / wsum);
-            }
-            a.st->counters[LFM_CNT_ROUTER] = 0;
+    float wv[32];
+    const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
+    const float *w = a.w + (size_t)e * a.dim;
+    if (b < nb) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4 x0 = *reinterpret_cast<const float4 *>(w + base + s * 32);
+            const float4 x1 = *reinterpret_cast<const float4 *>(w + base + s * 32 + 4);
+            wv[s * 8 + 0] = x0.x, wv[s * 8 + 1] = x0.y, wv[s * 8 + 2] = x0.z, wv[s * 8 + 3] = x0.w;
+            wv[s * 8 + 4] = x1.x, wv[s * 8 + 5] = x1.y, wv[s * 8 + 6] = x1.z, wv[s * 8 + 7] = x1.w;
         }
     }
+    LaneX X;
+    wave_x(a.src, nb, a.st, X, false);
+    float acc = 0.f;
+    if (b < nb)
+#pragma unroll
+        for (int i = 0; i < 32; ++i)
+            acc += wv[i] * X.v[i];
+    acc = wave_sum(acc);
+    if (lane == 0)
+        a.logits[e] = acc;
 }
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
-// Routed: work item (rank, row) reads expert sel[rank]'s rows.
+// Routed: work item (rank, row) reads expert ids[rank]'s rows.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gateup(const GateUpArgs a)
 {
     if (a.st->halt)
         return;
-    extern __shared__ float smem[];
-    const uint32_t in_dim = a.wg.nb * 256;
-    float *xs = smem;
-    float *red = smem + in_dim;
-    stage_x(a.src, xs, in_dim, a.st, red);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wg.nb;
-    LaneX X;
-    if (active)
-        load_lanex(X, xs, b, c);
-    else
-        zero_lanex(X);
-    const uint32_t nrank = a.sel ? a.n_used : 1;
-    const uint32_t total = nrank * a.ff;
-    for (uint32_t item = blockIdx.x * 4 + wave; item < total; item += gridDim.x * 4) {
-        const uint32_t rank = item / a.ff, r = item - rank * a.ff;
-        uint32_t row = a.sel ? a.sel[rank] * a.ff + r : r;
-        if (row >= a.wg.rows) // an id outside the table (NaN router scores) reads expert 0
-            row = r;
-        float g = 0.f, u = 0.f;
-        if (active) {
-            const Lane lg = load_lane(a.wg, row, b, c);
-            const Lane lu = load_lane(a.wu, row, b, c);
-            g = lane_dot(lg, X);
-            u = lane_dot(lu, X);
+    const bool routed = a.route.logits != nullptr;
+    Routed rt = {0, 0, 0, 0, 0.f, 0.f, 0.f, 0.f};
+    uint32_t nrank = 1;
+    if (routed) {
+        rt = wave_route(a.route);
+        nrank = a.route.n_used;
+        if (blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
+            a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
+            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
         }
-        g = wave_sum(g);
-        u = wave_sum(u);
-        if (lane == 0)
-            a.sw[item] = g / (1.0f + expf(-g)) * u;
     }
+    const uint32_t ff = a.ff, W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    LaneX X;
+    stream_items<2, 1>(
+        first, W, nrank * ff,
+        [&](uint32_t it, Item<2> &buf) {
+            const uint32_t rank = it / ff, r = it - rank * ff;
+            const uint32_t row = routed ? rt.id(rank) * ff + r : r;
+            if (active) {
+                buf.l[0] = load_lane(a.wg, row, b, c);
+                buf.l[1] = load_lane(a.wu, row, b, c);
+            }
+        },
+        [&]() { wave_x(a.src, a.wg.nb, a.st, X, false); },
+        [&](Item<2> *buf, uint32_t k0, uint32_t n) {
+            float p[2] = {0.f, 0.f};
+            if (active && k0 < n) {
+                p[0] = lane_dot(buf[0].l[0], X);
+                p[1] = lane_dot(buf[0].l[1], X);
+            }
+            wave_sum_n<2>(p);
+            if (lane == 0 && k0 < n)
+                a.sw[first + k0 * W] = p[0] / (1.0f + expf(-p[0])) * p[1];
+        });
 }
 
 // Routed down projections and combine (lfm.rs:660-668, resident.rs:101-117):
-// wave r computes d_r = (Wd[e_r] sw_r)[k]; then
+// wave r computes d_r = (Wd[e_r] sw_r)[k] for 4 rows; then per row
 // x[k] += ((((0 + d_0 w_0) + d_1 w_1) + d_2 w_2) + d_3 w_3)  (no contraction).
-__device__ __forceinline__ float combine4(const float *dv, const float *wv, uint32_t n, float x)
+__device__ __forceinline__ float combine(const float *dv, const float *wv, uint32_t n, float x)
 {
 #pragma clang fp contract(off)
     float s = 0.0f;
@@ -653,51 +853,53 @@ __device__ __forceinline__ float combine4(const float *dv, const float *wv, uint
     return x + s;
 }
 
+#define DOWN_ROWS 8 // output rows per workgroup pass (each wave: its expert's 8 rows)
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_moe_down(const MoeDownArgs a)
 {
     if (a.st->halt)
         return;
-    __shared__ float red[2][4];
-    __shared__ float wsel[4];
+    __shared__ float red[DOWN_ROWS][4];
+    __shared__ float wsh[4];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t b = lane >> 3, c = lane & 7;
-    const bool active = b < a.wd.nb && wave < a.n_used;
-    uint32_t e = a.sel[wave < a.n_used ? wave : 0];
-    if ((size_t)e * a.dim + a.dim > a.wd.rows) // id outside the table (NaN scores): expert 0
-        e = 0;
+    const Routed rt = wave_route(a.route);
+    const uint32_t n_used = a.route.n_used;
+    const bool active = b < a.wd.nb && wave < n_used;
+    const uint32_t e = rt.id(wave);
     if (tid < 4)
-        wsel[tid] = tid < a.n_used ? __uint_as_float(a.sel[8 + tid]) : 0.f;
-    LaneX X;
-    if (active)
-        load_lanex(X, a.sw + (size_t)wave * a.ff, b, c);
-    else
-        zero_lanex(X);
+        wsh[tid] = rt.w(tid);
     const uint32_t dim = a.dim;
-    for (uint32_t k0 = blockIdx.x * 2; k0 < dim; k0 += gridDim.x * 2) {
-        float p0 = 0.f, p1 = 0.f;
-        if (active) {
-            const Lane l0 = load_lane(a.wd, e * dim + k0, b, c);
-            const bool two = k0 + 1 < dim;
-            const Lane l1 = load_lane(a.wd, e * dim + (two ? k0 + 1 : k0), b, c);
-            p0 = lane_dot(l0, X);
-            p1 = lane_dot(l1, X);
-        }
-        p0 = wave_sum(p0);
-        p1 = wave_sum(p1);
-        if (lane == 0) {
-            red[0][wave] = p0;
-            red[1][wave] = p1;
-        }
+    for (uint32_t k0 = blockIdx.x * DOWN_ROWS; k0 < dim; k0 += gridDim.x * DOWN_ROWS) {
+        Lane l[DOWN_ROWS];
+        if (active)
+#pragma unroll
+            for (int i = 0; i < DOWN_ROWS; ++i)
+                if (k0 + i < dim)
+                    l[i] = load_lane(a.wd, e * dim + k0 + i, b, c);
+        LaneX X;
+        if (active)
+            load_lanex(X, a.sw + (size_t)wave * a.ff, b, c);
+        else
+            zero_lanex(X);
+        float p[DOWN_ROWS];
+#pragma unroll
+        for (int i = 0; i < DOWN_ROWS; ++i)
+            p[i] = (active && k0 + i < dim) ? lane_dot(l[i], X) : 0.f;
+        wave_sum_n<DOWN_ROWS>(p);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < DOWN_ROWS; ++i)
+                red[i][wave] = p[i];
         __syncthreads();
-        if (tid < 2 && k0 + tid < dim)
-            a.x[k0 + tid] = combine4(red[tid], wsel, a.n_used, a.x[k0 + tid]);
+        if (tid < DOWN_ROWS && k0 + tid < dim)
+            a.x[k0 + tid] = combine(red[tid], wsh, n_used, a.x[k0 + tid]);
         __syncthreads();
     }
 }
 
-// (value, index) reduction for greedy argmax (main.rs:112-141): the larger
-// value wins; equal values keep the lower index; -inf is "no candidate" and
-// NaN never wins; with no candidate the result index is 0.
+// (value, index) merge for greedy argmax (main.rs:112-141): the larger value
+// wins; equal values keep the lower index; -inf is "no candidate" and NaN
+// never wins; with no candidate the index is 0.
 __device__ __forceinline__ void amax_merge(float &bv, uint32_t &bi, float v, uint32_t i)
 {
     if (v > bv || (v == bv && v > -INFINITY && i < bi)) {
@@ -716,105 +918,108 @@ __device__ __forceinline__ void amax_wave(float &bv, uint32_t &bi)
     }
 }
 
-// Final reduction of per-workgroup partials by the last workgroup.
-__device__ void amax_final(const float *partial, uint32_t n, float &bv, uint32_t &bi,
-                           float (*redv)[4], uint32_t (*redi)[4])
+// Workgroup-level merge of per-wave (value, index); result in thread 0.
+__device__ __forceinline__ void amax_block(float &bv, uint32_t &bi)
 {
+    __shared__ float rv[4];
+    __shared__ uint32_t ri[4];
     const uint32_t tid = threadIdx.x;
-    bv = -INFINITY;
-    bi = 0;
-    for (uint32_t i = tid; i < n; i += WG_THREADS)
-        amax_merge(bv, bi, __builtin_nontemporal_load(partial + 2 * i),
-                   __float_as_uint(__builtin_nontemporal_load(partial + 2 * i + 1)));
     amax_wave(bv, bi);
     if ((tid & 63) == 0) {
-        (*redv)[tid >> 6] = bv;
-        (*redi)[tid >> 6] = bi;
+        rv[tid >> 6] = bv;
+        ri[tid >> 6] = bi;
     }
     __syncthreads();
-    bv = (*redv)[0];
-    bi = (*redi)[0];
-    for (int w = 1; w < 4; ++w)
-        amax_merge(bv, bi, (*redv)[w], (*redi)[w]);
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            amax_merge(bv, bi, rv[w], ri[w]);
+    }
 }
 
-// Final RMSNorm + tied Q6_K head (lfm.rs:676-693) with the greedy argmax fused;
-// the last workgroup stores the winner and, in a decode step, feeds it back
-// (stops the loop at eos, main.rs:182-189).
+// Final RMSNorm + tied Q6_K head (lfm.rs:676-693): one wave per row, rows
+// streamed two at a time with two more in flight; each workgroup leaves its
+// argmax (value, index) partial for k_argmax_final.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_head(const HeadArgs a)
 {
     if (a.st->halt)
         return;
-    extern __shared__ float smem[];
-    const uint32_t dim = a.emb.nb * 256;
-    float *xs = smem;
-    float *red = smem + dim;
-    __shared__ float redv[4];
-    __shared__ uint32_t redi[4];
-    __shared__ uint32_t s_last;
-    stage_x(a.src, xs, dim, a.st, red);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.emb.nb;
+    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
     LaneX X;
-    if (active)
-        load_lanex(X, xs, b, c);
-    else
-        zero_lanex(X);
     float bv = -INFINITY;
     uint32_t bi = 0;
-    for (uint32_t r = blockIdx.x * 4 + wave; r < a.vocab; r += gridDim.x * 4) {
-        float v = active ? lane_dot(load_lane(a.emb, r, b, c), X) : 0.f;
-        v = wave_sum(v);
-        if (lane == 0 && a.logits)
-            a.logits[r] = v;
-        amax_merge(bv, bi, v, r);
+    stream_items<1, 2>(
+        first, W, a.vocab,
+        [&](uint32_t r, Item<1> &it) {
+            if (active)
+                it.l[0] = load_lane(a.emb, r, b, c);
+        },
+        [&]() { wave_x(a.src, a.emb.nb, a.st, X, false); },
+        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
+            float p[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
+            wave_sum_n<2>(p);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (k0 + j < n) {
+                    const uint32_t r = first + (k0 + j) * W;
+                    if (lane == 0)
+                        a.logits[r] = p[j];
+                    amax_merge(bv, bi, p[j], r);
+                }
+        });
+    amax_block(bv, bi);
+    if (threadIdx.x == 0) {
+        a.partial[2 * blockIdx.x] = bv;
+        a.partial[2 * blockIdx.x + 1] = __uint_as_float(bi);
     }
-    if (lane == 0) {
-        redv[wave] = bv;
-        redi[wave] = bi;
+}
+
+// Per-workgroup argmax partials of a plain vector.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax(const ArgmaxArgs a)
+{
+    float bv = -INFINITY;
+    uint32_t bi = 0;
+    for (uint32_t i = blockIdx.x * WG_THREADS + threadIdx.x; i < a.n; i += gridDim.x * WG_THREADS)
+        amax_merge(bv, bi, a.v[i], i);
+    amax_block(bv, bi);
+    if (threadIdx.x == 0) {
+        a.partial[2 * blockIdx.x] = bv;
+        a.partial[2 * blockIdx.x + 1] = __uint_as_float(bi);
     }
-    __syncthreads();
-    if (tid == 0) {
-        float v = redv[0];
-        uint32_t i = redi[0];
-        for (int w = 1; w < 4; ++w)
-            amax_merge(v, i, redv[w], redi[w]);
-        a.partial[2 * blockIdx.x] = v;
-        a.partial[2 * blockIdx.x + 1] = __uint_as_float(i);
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.st->counters[LFM_CNT_HEAD], 1u);
-        s_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!s_last)
+}
+
+// Reduces the partials; in a decode step stores the token and feeds it back
+// (stops the loop at eos, main.rs:182-189).
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax_final(const FinalArgs a)
+{
+    if (a.st->halt)
         return;
-    __threadfence();
-    __shared__ float fredv[4];
-    __shared__ uint32_t fredi[4];
-    float fv;
-    uint32_t fi;
-    amax_final(a.partial, gridDim.x, fv, fi, &fredv, &fredi);
-    if (tid == 0) {
-        if (!(fv > -INFINITY))
-            fi = 0;
+    float bv = -INFINITY;
+    uint32_t bi = 0;
+    for (uint32_t i = threadIdx.x; i < a.n_partial; i += WG_THREADS)
+        amax_merge(bv, bi, a.partial[2 * i], __float_as_uint(a.partial[2 * i + 1]));
+    amax_block(bv, bi);
+    if (threadIdx.x == 0) {
+        if (!(bv > -INFINITY))
+            bi = 0;
         DevState *st = a.st;
-        st->last_token = fi;
-        st->last_value = fv;
+        st->last_token = bi;
+        st->last_value = bv;
         if (a.advance) {
-            if (fi == st->eos) {
+            if (bi == st->eos) {
                 st->halt = 1;
             } else {
-                a.out_tokens[st->step] = fi;
+                a.out_tokens[st->step] = bi;
                 st->step = st->step + 1;
-                st->tok = fi;
+                st->tok = bi;
                 st->pos = st->pos + 1;
             }
         }
-        st->counters[LFM_CNT_HEAD] = 0;
     }
 }
 
@@ -848,54 +1053,5 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_dequant(const Dequ
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 o[lane_pos(b, c, s, i)] = v[s * 8 + i];
-    }
-}
-
-// Stand-alone greedy argmax of a device vector.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax(const ArgmaxArgs a)
-{
-    __shared__ float redv[4];
-    __shared__ uint32_t redi[4];
-    __shared__ uint32_t s_last;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    float bv = -INFINITY;
-    uint32_t bi = 0;
-    for (uint32_t i = blockIdx.x * WG_THREADS + tid; i < a.n; i += gridDim.x * WG_THREADS)
-        amax_merge(bv, bi, a.v[i], i);
-    amax_wave(bv, bi);
-    if (lane == 0) {
-        redv[wave] = bv;
-        redi[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float v = redv[0];
-        uint32_t i = redi[0];
-        for (int w = 1; w < 4; ++w)
-            amax_merge(v, i, redv[w], redi[w]);
-        a.partial[2 * blockIdx.x] = v;
-        a.partial[2 * blockIdx.x + 1] = __uint_as_float(i);
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.st->counters[LFM_CNT_ARGMAX], 1u);
-        s_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!s_last)
-        return;
-    __threadfence();
-    __shared__ float fredv[4];
-    __shared__ uint32_t fredi[4];
-    float fv;
-    uint32_t fi;
-    amax_final(a.partial, gridDim.x, fv, fi, &fredv, &fredi);
-    if (tid == 0) {
-        if (!(fv > -INFINITY))
-            fi = 0;
-        a.st->last_token = fi;
-        a.st->last_value = fv;
-        a.st->counters[LFM_CNT_ARGMAX] = 0;
     }
 }
