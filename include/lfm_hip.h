@@ -136,6 +136,12 @@ int lfm_engine_run_mixer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos);
 int lfm_engine_run_ffn(lfm_engine *e, uint32_t layer, float *x);
 int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *weights, uint32_t cap);
 
+/* Mean duration of the routed MoE gate/up kernel (the largest share of a decode
+ * step), timed with HIP events over one graph of `reps` rounds across every MoE
+ * layer's routed experts; *bytes_per_launch = its algorithmic HBM bytes. */
+int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *us_per_launch,
+                               uint64_t *bytes_per_launch);
+
 /* ---- device buffers (op-level tests and measurement) --------------------- */
 int lfm_dev_alloc(size_t nbytes, void **ptr);
 int lfm_dev_free(void *ptr);

@@ -424,7 +424,9 @@ struct lfm_engine {
     std::vector<uint16_t *> kc, vc;
     std::vector<float *> conv;
     uint32_t head_grid = 1, nchunk = 1;
-    float tscale = 1.f;
+    float *rope = nullptr; // [ctx][32] (cos, sin)
+    DevState *host_st = nullptr;    // pinned staging for state copies
+    uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
     hipGraphExec_t g_layers = nullptr, g_decode = nullptr;
     uint64_t nodes_layers = 0, nodes_decode = 0;
@@ -617,7 +619,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
         a.y = e->y;
         a.dim = dim;
         a.st = e->st;
-        RC(launch(e->K->conv, dim3(wave_grid(dim, 2)), 0, e->stream, a));
+        RC(launch(e->K->conv, dim3(wave_grid(dim, 1)), 0, e->stream, a));
         m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
         RC(launch_matvec(e->K, m, e->stream));
         e->dispatches += 2;
@@ -639,7 +641,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     at.q_norm = f32(e, "blk.%u.attn_q_norm.weight", l);
     at.k_norm = f32(e, "blk.%u.attn_k_norm.weight", l);
     at.eps = hp.eps;
-    at.tscale = e->tscale;
+    at.rope = e->rope;
     at.scale = 1.0f / sqrtf((float)hp.head_dim);
     at.kcache = e->kc[l];
     at.vcache = e->vc[l];
@@ -656,6 +658,25 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     RC(launch_matvec(e->K, m, e->stream));
     e->dispatches += 4;
     return LFM_OK;
+}
+
+static GateUpArgs moe_gateup_args(lfm_engine *e, uint32_t l)
+{
+    const lfm_hparams &hp = e->hp;
+    GateUpArgs g;
+    memset(&g, 0, sizeof(g));
+    g.src = xsrc(e->x, f32(e, "blk.%u.ffn_norm.weight", l), hp.eps);
+    g.sw = e->sw;
+    g.st = e->st;
+    g.route.logits = e->rlogits;
+    g.route.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
+    g.route.n_expert = hp.n_expert;
+    g.route.n_used = hp.n_used;
+    g.route.sel_out = e->sel;
+    g.wg = q6(e, "blk.%u.ffn_gate_exps.weight", l);
+    g.wu = q6(e, "blk.%u.ffn_up_exps.weight", l);
+    g.ff = hp.expert_ff;
+    return g;
 }
 
 static int enq_ffn(lfm_engine *e, uint32_t l)
@@ -693,16 +714,8 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
     r.n_expert = hp.n_expert;
     r.st = e->st;
     RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), 0, e->stream, r));
-    Route route;
-    route.logits = e->rlogits;
-    route.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
-    route.n_expert = hp.n_expert;
-    route.n_used = hp.n_used;
-    route.sel_out = e->sel;
-    g.wg = q6(e, "blk.%u.ffn_gate_exps.weight", l);
-    g.wu = q6(e, "blk.%u.ffn_up_exps.weight", l);
-    g.route = route;
-    g.ff = hp.expert_ff;
+    g = moe_gateup_args(e, l);
+    const Route route = g.route;
     RC(launch(e->K->gateup, dim3(wave_grid(hp.n_used * hp.expert_ff, 2)), 0, e->stream, g));
     MoeDownArgs d;
     d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
@@ -803,8 +816,34 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         max_hdkv = std::max(max_hdkv, 64 * hp.kv_heads[l]);
     e->nchunk = (e->ctx + 127) / 128;
     e->head_grid = wave_grid(hp.vocab, 16, 1024);
-    e->tscale = powf(hp.rope_theta, -2.0f / (float)hp.head_dim);
+    {
+        // NEOX RoPE angles as lfm.rs:251-256 computes them: tscale = theta^(-2/hd)
+        // (powf), theta_p = pos * tscale^p with f32 square-and-multiply powi, then
+        // sinf / cosf; tabulated once for every position of the context.
+        const float tscale = powf(hp.rope_theta, -2.0f / (float)hp.head_dim);
+        std::vector<float> tab((size_t)e->ctx * 64);
+        for (uint32_t p = 0; p < 32; ++p) {
+            float r = 1.0f, a = tscale;
+            for (int b = (int)p;;) {
+                if (b & 1)
+                    r *= a;
+                b /= 2;
+                if (b == 0)
+                    break;
+                a *= a;
+            }
+            for (uint32_t pos = 0; pos < e->ctx; ++pos) {
+                const float th = (float)pos * r;
+                tab[(size_t)pos * 64 + 2 * p] = cosf(th);
+                tab[(size_t)pos * 64 + 2 * p + 1] = sinf(th);
+            }
+        }
+        HIPCHK(hipMalloc(&e->rope, tab.size() * 4));
+        HIPCHK(hipMemcpy(e->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice));
+    }
     const size_t swn = std::max<size_t>((size_t)hp.n_ff, (size_t)hp.n_used * hp.expert_ff);
+    HIPCHK(hipHostMalloc((void **)&e->host_st, sizeof(DevState), hipHostMallocDefault));
+    HIPCHK(hipHostMalloc((void **)&e->host_ids, (size_t)e->ctx * 4, hipHostMallocDefault));
     HIPCHK(hipMalloc(&e->st, sizeof(DevState)));
     HIPCHK(hipMemset(e->st, 0, sizeof(DevState)));
     HIPCHK(hipMalloc(&e->ids, e->ctx * 4));
@@ -856,10 +895,14 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (auto &kv : e->tensors)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
-                    e->rlogits, e->logits, e->hpart, e->apart};
+                    e->rlogits, e->logits, e->hpart, e->apart, e->rope};
     for (void *p : bufs)
         if (p)
             (void)hipFree(p);
+    if (e->host_st)
+        (void)hipHostFree(e->host_st);
+    if (e->host_ids)
+        (void)hipHostFree(e->host_ids);
     for (auto p : e->kc)
         if (p)
             (void)hipFree(p);
@@ -886,7 +929,8 @@ static int need_final(lfm_engine *e)
 // Writes the device-resident decode state.
 static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, uint32_t eos)
 {
-    DevState h;
+    HIPCHK(hipStreamSynchronize(e->stream)); // the pinned staging block is reused
+    DevState &h = *e->host_st;
     memset(&h, 0, sizeof(h));
     h.tok = tok;
     h.pos = pos;
@@ -901,8 +945,9 @@ static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, 
 
 static int read_state(lfm_engine *e, DevState *h)
 {
-    HIPCHK(hipMemcpyAsync(h, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(hipMemcpyAsync(e->host_st, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
     HIPCHK(hipStreamSynchronize(e->stream));
+    *h = *e->host_st;
     return LFM_OK;
 }
 
@@ -922,8 +967,9 @@ static int check_ids(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t st
 static int run_prompt(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start)
 {
     RC(check_ids(e, ids, n, start));
-    HIPCHK(hipMemcpyAsync(e->ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
-    RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu));
+    RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu)); // also waits for prior use of host_ids
+    memcpy(e->host_ids, ids, (size_t)n * 4);
+    HIPCHK(hipMemcpyAsync(e->ids, e->host_ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
     for (uint32_t j = 0; j < n; ++j) {
         HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
         e->dispatches += e->nodes_layers;
@@ -1099,6 +1145,65 @@ extern "C" int lfm_device_name(const lfm_engine *e, char *buf, size_t cap)
     if (!e || !buf || cap == 0)
         return fail(LFM_EINVAL, "null argument");
     snprintf(buf, cap, "%s", e->devname.c_str());
+    return LFM_OK;
+}
+
+// ------------------------------------------------------------------ kernel timing
+// Average duration of the routed gate/up kernel (the largest share of a decode
+// step): one graph of `reps` rounds over every MoE layer's weights (their 4
+// routed experts, > 256 MB in total, so the Infinity Cache cannot hold them),
+// timed with HIP events on the engine stream.  Routing uses the router logits
+// of the last decode step.
+extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *us_per_launch,
+                                          uint64_t *bytes_per_launch)
+{
+    RC(need_final(e));
+    const lfm_hparams &hp = e->hp;
+    if (!us_per_launch || !bytes_per_launch || reps == 0)
+        return fail(LFM_EINVAL, "bad arguments");
+    uint32_t nmoe = 0;
+    for (uint32_t l = hp.dense_lead; l < hp.n_layers; ++l)
+        ++nmoe;
+    if (nmoe == 0)
+        return fail(LFM_ESTATE, "model has no MoE layer");
+    RC(set_state(e, 0, 0, 0, 0xFFFFFFFFu));
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    int rc = LFM_OK;
+    for (uint32_t r = 0; r < reps && rc == LFM_OK; ++r)
+        for (uint32_t l = hp.dense_lead; l < hp.n_layers && rc == LFM_OK; ++l) {
+            GateUpArgs a = moe_gateup_args(e, l);
+            rc = launch(e->K->gateup, dim3(wave_grid(hp.n_used * hp.expert_ff, 2)), 0, e->stream, a);
+        }
+    hipError_t ce = hipStreamEndCapture(e->stream, &g);
+    if (rc != LFM_OK || ce != hipSuccess) {
+        if (g)
+            (void)hipGraphDestroy(g);
+        return rc != LFM_OK ? rc : fail(LFM_EDEVICE, "capture: %s", hipGetErrorString(ce));
+    }
+    hipError_t ie = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ie != hipSuccess)
+        return fail(LFM_EDEVICE, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+    hipEvent_t e0, e1;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    HIPCHK(hipGraphLaunch(ge, e->stream)); // warm
+    HIPCHK(hipEventRecord(e0, e->stream));
+    HIPCHK(hipGraphLaunch(ge, e->stream));
+    HIPCHK(hipEventRecord(e1, e->stream));
+    HIPCHK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipGraphExecDestroy(ge);
+    e->dispatches += 2ull * reps * nmoe;
+    *us_per_launch = ms * 1e3f / (float)(reps * nmoe);
+    const uint64_t wbytes = 2ull * hp.n_used * hp.expert_ff * (hp.dim / 256) * 210;
+    *bytes_per_launch = wbytes + 2ull * hp.dim * 4 + 2ull * hp.n_expert * 4 +
+                        (uint64_t)hp.n_used * hp.expert_ff * 4;
     return LFM_OK;
 }
 

@@ -75,7 +75,8 @@ struct QkvArgs {
 struct AttnArgs {
     const float *qkv;
     const float *q_norm, *k_norm;
-    float eps, tscale, scale;
+    const float *rope;         // [ctx][32] (cos, sin) of theta = pos * tscale^p
+    float eps, scale;
     uint16_t *kcache, *vcache; // [kv][ctx][64] binary16
     float *part;               // [kv][nchunk][4][66]: max, sum, o[64]
     uint32_t ctx, heads, kv, nchunk;

@@ -567,31 +567,17 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_qkv(const QkvArgs a)
 
 // Per-head RMSNorm then NEOX RoPE of one 64-wide head held one value per lane
 // (lfm.rs:270-286 then 248-267): v *= inv * w[d]; pairs (d, d+32) rotated by
-// theta = pos * tscale^(d%32) with tscale^p by square-and-multiply.
-__device__ __forceinline__ float f32_powi(float a, int b)
-{
-    float r = 1.0f;
-    for (;;) {
-        if (b & 1)
-            r *= a;
-        b /= 2;
-        if (b == 0)
-            break;
-        a *= a;
-    }
-    return r;
-}
-
-__device__ __forceinline__ float head_norm_rope(float v, const float *w, float eps, float tscale,
-                                                uint32_t pos, uint32_t d)
+// theta = pos * tscale^(d%32).  cs_sn is the position's row of the (cos, sin)
+// table the host fills at finalize with the reference's own arithmetic.
+__device__ __forceinline__ float head_norm_rope(float v, const float *w, float eps,
+                                                const float *cs_sn, uint32_t d)
 {
     const float ss = wave_sum(v * v);
     const float inv = 1.0f / sqrtf(ss / 64.0f + eps);
     v *= inv * w[d];
     const float other = __shfl_xor(v, 32, 64);
     const uint32_t p = d & 31;
-    const float theta = (float)pos * f32_powi(tscale, (int)p);
-    const float sn = sinf(theta), cs = cosf(theta);
+    const float cs = cs_sn[2 * p], sn = cs_sn[2 * p + 1];
     // lane d < 32 holds x0 (partner x1); lane d >= 32 holds x1 (partner x0)
     return d < 32 ? v * cs - other * sn : other * sn + v * cs;
 }
@@ -648,11 +634,11 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     }
     if (wave < G) {
         const float v = a.qkv[(kh * G + wave) * 64 + lane];
-        qr[wave][lane] = head_norm_rope(v, a.q_norm, a.eps, a.tscale, p, lane);
+        qr[wave][lane] = head_norm_rope(v, a.q_norm, a.eps, a.rope + (size_t)p * 64, lane);
     }
     if (cur && wave == 0) {
         const float kraw = a.qkv[dim + kh * 64 + lane];
-        const float kr = head_norm_rope(kraw, a.k_norm, a.eps, a.tscale, p, lane);
+        const float kr = head_norm_rope(kraw, a.k_norm, a.eps, a.rope + (size_t)p * 64, lane);
         const uint16_t kb = float_to_half_bits(kr);
         const uint16_t vb = float_to_half_bits(a.qkv[dim + hdkv + kh * 64 + lane]);
         a.kcache[((size_t)kh * a.ctx + p) * 64 + lane] = kb;

@@ -12,7 +12,6 @@ from __future__ import annotations
 
 import ctypes as C
 import os
-from dataclasses import dataclass, field
 from typing import Iterable, List, Optional, Sequence
 
 import numpy as np
@@ -122,6 +121,7 @@ def lib():
         "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
+        "lfm_engine_time_moe_gateup": (i32, [P, u32, pf32, C.POINTER(u64)]),
         "lfm_dev_alloc": (i32, [sz, C.POINTER(P)]), "lfm_dev_free": (i32, [P]),
         "lfm_memcpy_htod": (i32, [P, P, sz]), "lfm_memcpy_dtoh": (i32, [P, P, sz]),
         "lfm_dev_synchronize": (i32, []),
@@ -441,6 +441,12 @@ class GpuEngine:
         w = np.zeros(8, dtype=np.float32)
         _check(lib().lfm_engine_last_route(self._e, _u32p(ids), _f32p(w), 8))
         return [int(i) for i in ids[: self.hp.n_used]], w[: self.hp.n_used].copy()
+
+    def time_moe_gateup(self, reps: int = 10):
+        """(us per launch, algorithmic bytes per launch) of the routed gate/up kernel."""
+        us, nb = C.c_float(0), C.c_uint64(0)
+        _check(lib().lfm_engine_time_moe_gateup(self._e, reps, C.byref(us), C.byref(nb)))
+        return us.value, nb.value
 
     def close(self):
         if self._e:
