@@ -137,10 +137,12 @@ def main():
         eng.restore_session(n_prompt, state.astype(np.float16).astype(np.float32).tobytes())
         first = prompt[-1]
     else:
-        pos, first = 0, None
-        for c in range(0, n_prompt, 64):  # api_stream.rs:58-63 chunked prefill
-            first = eng.forward_token(prompt[c:c + 64], pos)
-            pos += len(prompt[c:c + 64])
+        eng.forward(prompt[:256], 0)  # untimed: first launches of the prefill kernels
+        eng.reset_session()
+        lfm_hip.lib().lfm_dev_synchronize()
+        t = time.perf_counter()
+        logits = eng.forward(prompt, 0)  # one batched matrix-core prefill of the prompt
+        first = int(np.argmax(logits))
     prefill_s = time.perf_counter() - t
     log(f"[bench] {'state restore' if args.synthetic_state else 'prefill'} {n_prompt} tokens: "
         f"{prefill_s * 1e3:.1f} ms")

@@ -121,6 +121,10 @@ int lfm_snapshot_cache(lfm_engine *e, uint32_t valid_tokens, uint8_t *buf, size_
 int lfm_restore_session(lfm_engine *e, uint32_t valid_tokens, const uint8_t *buf, size_t len);
 /* snapshot_resident_logits (resident_graph.rs:561-568): last full logits. */
 int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap);
+/* Multi-token forwards (n >= 2) run the batched matrix-core prefill by default
+ * (stepwise = 0); stepwise = 1 runs them as one captured decode step per token
+ * instead (the reference's token-by-token equivalence, used by parity tests). */
+int lfm_engine_set_prefill_mode(lfm_engine *e, int stepwise);
 /* gpu.dispatch_count(): kernels launched by this engine so far. */
 uint64_t lfm_dispatch_count(const lfm_engine *e);
 /* device_name (gpu_lfm.rs:126-128). */
@@ -169,6 +173,12 @@ int lfm_q6k_matvec(const void *packed_dev, uint64_t rows, uint64_t in_dim, const
  * 256 MB Infinity Cache when ncopies * size exceeds it). */
 int lfm_q6k_matvec_time(const void *packed_dev, uint32_t ncopies, uint64_t rows, uint64_t in_dim,
                         const float *x_dev, float *y_dev, uint32_t iters, float *ms_per_launch);
+
+/* Prefill GEMM on the matrix cores: y[t][r] = sum_k W[r][k] * x[t][k] for T
+ * activation rows x (f32 [T][in_dim], device) into y (f32 [T][rows], device);
+ * the multi-token q6k_prompt path of engine/src/ops.rs:350-373. */
+int lfm_q6k_gemm(const void *packed_dev, uint64_t rows, uint64_t in_dim, const float *x_dev,
+                 uint32_t T, float *y_dev, void *stream);
 
 /* ---- argmax (engine/src/kernels/persistent.rs:11-53 semantics) ------------ */
 int lfm_argmax(const float *v_dev, uint32_t n, uint32_t *index, float *value);

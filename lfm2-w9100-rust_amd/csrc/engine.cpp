@@ -70,7 +70,9 @@ extern "C" int lfm_device_count(int *count)
 
 // ------------------------------------------------------------------ kernels
 struct Kernels {
-    hipModule_t mod = nullptr;
+    hipModule_t mod = nullptr, pmod = nullptr;
+    hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
+        swiglu_split, router_prefill, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec, matvec_ks, conv, qkv, attn, attn_merge, router, gateup, moe_down, head,
         argmax, argmax_final, advance, dequant;
 };
@@ -91,6 +93,14 @@ static std::string code_object_path()
         return dir + "/lfm_kernels.hsaco";
     }
     return "lfm_kernels.hsaco";
+}
+
+// The prefill kernels live in a second code object next to the first.
+static std::string prefill_object_path()
+{
+    std::string p = code_object_path();
+    const size_t slash = p.rfind('/');
+    return (slash == std::string::npos ? std::string(".") : p.substr(0, slash)) + "/lfm_prefill.hsaco";
 }
 
 // Loads the code object on the current device (once per device).
@@ -125,6 +135,31 @@ static int get_kernels(Kernels **out)
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
             (void)hipModuleUnload(k->mod);
+            delete k;
+            return fail(LFM_EDEVICE, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
+        }
+    }
+    const std::string ppath = prefill_object_path();
+    e = hipModuleLoad(&k->pmod, ppath.c_str());
+    if (e != hipSuccess) {
+        (void)hipModuleUnload(k->mod);
+        delete k;
+        return fail(LFM_EDEVICE, "hipModuleLoad(%s): %s", ppath.c_str(), hipGetErrorString(e));
+    }
+    struct {
+        hipFunction_t *f;
+        const char *name;
+    } pfns[] = {{&k->split_rows, "k_split_rows"},       {&k->gemm_q6, "k_gemm_q6"},
+                {&k->conv_prefill, "k_conv_prefill"},   {&k->conv_state, "k_conv_state"},
+                {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
+                {&k->swiglu_split, "k_swiglu_split"},   {&k->router_prefill, "k_router_prefill"},
+                {&k->route_group, "k_route_group"},     {&k->combine_prefill, "k_combine_prefill"},
+                {&k->embed_rows, "k_embed_rows"}};
+    for (auto &f : pfns) {
+        e = hipModuleGetFunction(f.f, k->pmod, f.name);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(k->mod);
+            (void)hipModuleUnload(k->pmod);
             delete k;
             return fail(LFM_EDEVICE, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
         }
@@ -365,6 +400,52 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
     return LFM_OK;
 }
 
+// ------------------------------------------------------------------ MFMA GEMM
+#define GEMM_TILE 128
+static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz)
+{
+    return dim3((rows + GEMM_TILE - 1) / GEMM_TILE, (ntok + GEMM_TILE - 1) / GEMM_TILE, nz);
+}
+
+// Y[t][r] = sum_k W[r][k] X[t][k] for T token rows (prefill GEMM, op level).
+extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, const float *x,
+                            uint32_t T, float *y, void *stream)
+{
+    RC(check_q6_args(packed, rows, in_dim));
+    if (!x || !y || T == 0)
+        return fail(LFM_EINVAL, "lfm_q6k_gemm: empty input");
+    if (in_dim > 8192)
+        return fail(LFM_EINVAL, "lfm_q6k_gemm: in_dim up to 8192");
+    Kernels *K;
+    RC(get_kernels(&K));
+    hipStream_t s = (hipStream_t)stream;
+    uint16_t *hi = nullptr, *lo = nullptr;
+    float *scale = nullptr;
+    HIPCHK(hipMalloc(&hi, (size_t)T * in_dim * 2));
+    HIPCHK(hipMalloc(&lo, (size_t)T * in_dim * 2));
+    HIPCHK(hipMalloc(&scale, (size_t)T * 4));
+    SplitArgs sa{x, nullptr, 0.f, hi, lo, scale, T, (uint32_t)in_dim};
+    int rc = launch(K->split_rows, dim3(T), 0, s, sa);
+    GemmArgs ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.w = q6view(packed, rows, in_dim);
+    ga.x_hi = hi;
+    ga.x_lo = lo;
+    ga.xscale = scale;
+    ga.ntok = T;
+    ga.zrows = (uint32_t)rows;
+    ga.c = y;
+    ga.ldc = (uint32_t)rows;
+    if (rc == LFM_OK)
+        rc = launch(K->gemm_q6, gemm_grid((uint32_t)rows, T, 1), 0, s, ga);
+    if (rc == LFM_OK && hipStreamSynchronize(s) != hipSuccess)
+        rc = fail(LFM_EDEVICE, "lfm_q6k_gemm: synchronize failed");
+    (void)hipFree(hi);
+    (void)hipFree(lo);
+    (void)hipFree(scale);
+    return rc;
+}
+
 // Stand-alone argmax uses a small private state block per device.
 extern "C" int lfm_argmax(const float *v, uint32_t n, uint32_t *index, float *value)
 {
@@ -426,11 +507,19 @@ struct lfm_engine {
     uint32_t head_grid = 1, nchunk = 1;
     float *rope = nullptr; // [ctx][32] (cos, sin)
     DevState *host_st = nullptr;    // pinned staging for state copies
+    // batched prefill buffers (capacity: ctx tokens per call)
+    struct {
+        float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *u = nullptr, *d = nullptr;
+        float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
+        uint16_t *hi = nullptr, *lo = nullptr;
+        uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr;
+    } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
     hipGraphExec_t g_layers = nullptr, g_decode = nullptr;
     uint64_t nodes_layers = 0, nodes_decode = 0;
     uint64_t dispatches = 0;
+    bool stepwise_prefill = false; // true: prompts run as one decode step per token
 };
 
 static int engine_dev(lfm_engine *e)
@@ -874,6 +963,28 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
             HIPCHK(hipMemset(e->conv[l], 0, (size_t)dim * 2 * 4));
         }
     }
+    {
+        // batched prefill buffers, sized for a whole context in one call
+        const size_t TC = e->ctx, E = hp.n_expert;
+        const size_t wide = std::max<size_t>((size_t)hp.n_ff, 4 * (size_t)hp.expert_ff);
+        const size_t hmax = std::max<size_t>({TC * dim, TC * hp.n_ff, TC * 4 * hp.expert_ff});
+        const size_t bcxw = std::max<size_t>(3 * (size_t)dim, (size_t)dim + 2 * max_hdkv);
+        HIPCHK(hipMalloc(&e->pf.x, TC * dim * 4));
+        HIPCHK(hipMalloc(&e->pf.bcx, TC * bcxw * 4));
+        HIPCHK(hipMalloc(&e->pf.y, TC * dim * 4));
+        HIPCHK(hipMalloc(&e->pf.g, TC * wide * 4));
+        HIPCHK(hipMalloc(&e->pf.u, TC * wide * 4));
+        HIPCHK(hipMalloc(&e->pf.d, TC * 4 * dim * 4));
+        HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
+        HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
+        HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));
+        HIPCHK(hipMalloc(&e->pf.logits, TC * E * 4));
+        HIPCHK(hipMalloc(&e->pf.wsel, TC * 4 * 4));
+        HIPCHK(hipMalloc(&e->pf.sel, TC * 4 * 4));
+        HIPCHK(hipMalloc(&e->pf.counts, E * 4));
+        HIPCHK(hipMalloc(&e->pf.tok, E * TC * 4));
+        HIPCHK(hipMalloc(&e->pf.slot, E * TC * 4));
+    }
     HIPCHK(hipDeviceSynchronize());
     RC(capture(e, false, &e->g_layers, &e->nodes_layers));
     RC(capture(e, true, &e->g_decode, &e->nodes_decode));
@@ -895,7 +1006,10 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (auto &kv : e->tensors)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
-                    e->rlogits, e->logits, e->hpart, e->apart, e->rope};
+                    e->rlogits, e->logits, e->hpart, e->apart, e->rope,
+                    e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.u, e->pf.d, e->pf.hi, e->pf.lo,
+                    e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
+                    e->pf.slot};
     for (void *p : bufs)
         if (p)
             (void)hipFree(p);
@@ -915,6 +1029,151 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     if (e->stream)
         (void)hipStreamDestroy(e->stream);
     delete e;
+}
+
+// ------------------------------------------------------------------ batched prefill
+// The multi-token forward (lfm.rs:290-694 with n > 1): every projection is a
+// matrix-core GEMM over the T tokens of the call, the conv is parallel in t,
+// attention is causal over the binary16 cache.  Leaves the last token's
+// residual in e->x (the decode path's residual) for the head.
+static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t T, uint32_t K)
+{
+    SplitArgs a{x, norm, e->hp.eps, e->pf.hi, e->pf.lo, e->pf.scale, T, K};
+    RC(launch(e->K->split_rows, dim3(T), 0, e->stream, a));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
+                   uint32_t mode)
+{
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w = w;
+    g.x_hi = e->pf.hi;
+    g.x_lo = e->pf.lo;
+    g.xscale = e->pf.scale;
+    g.ntok = T;
+    g.zrows = w.rows;
+    g.c = c;
+    g.ldc = ldc;
+    g.col0 = col0;
+    g.mode = mode;
+    RC(launch(e->K->gemm_q6, gemm_grid(w.rows, T, 1), 0, e->stream, g));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+// Grouped expert GEMM: z = expert, rows zrows per expert, activation rows from
+// `tok`, output rows `slot`, counts per expert on the device.
+static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t T,
+                           const uint32_t *tok, float *c, uint32_t ldc)
+{
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w = w;
+    g.x_hi = e->pf.hi;
+    g.x_lo = e->pf.lo;
+    g.xscale = e->pf.scale;
+    g.tok = tok;
+    g.slot = e->pf.slot;
+    g.counts = e->pf.counts;
+    g.list_stride = e->ctx;
+    g.zrows = zrows;
+    g.c = c;
+    g.ldc = ldc;
+    RC(launch(e->K->gemm_q6, gemm_grid(zrows, T, e->hp.n_expert), 0, e->stream, g));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
+{
+    const lfm_hparams &hp = e->hp;
+    const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
+    RC(pf_split(e, e->pf.x, f32(e, "blk.%u.attn_norm.weight", l), T, dim));
+    if (kv == 0) {
+        RC(pf_gemm(e, q6(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0));
+        ConvPrefillArgs c{e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l], e->pf.y, T,
+                          dim};
+        RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
+        RC(launch(e->K->conv_state, dim3((dim + 255) / 256), 0, e->stream, c));
+        RC(pf_split(e, e->pf.y, nullptr, T, dim));
+        RC(pf_gemm(e, q6(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
+        e->dispatches += 2;
+        return LFM_OK;
+    }
+    const uint32_t hdkv = 64 * kv, w = dim + 2 * hdkv;
+    RC(pf_gemm(e, q6(e, "blk.%u.attn_q.weight", l), T, e->pf.bcx, w, 0, 0));
+    RC(pf_gemm(e, q6(e, "blk.%u.attn_k.weight", l), T, e->pf.bcx, w, dim, 0));
+    RC(pf_gemm(e, q6(e, "blk.%u.attn_v.weight", l), T, e->pf.bcx, w, dim + hdkv, 0));
+    RopeKvArgs r{e->pf.bcx, f32(e, "blk.%u.attn_q_norm.weight", l),
+                 f32(e, "blk.%u.attn_k_norm.weight", l), e->rope, hp.eps, e->kc[l], e->vc[l], T,
+                 start, hp.heads, kv, e->ctx};
+    RC(launch(e->K->rope_kv_prefill, dim3(T), 0, e->stream, r));
+    AttnPrefillArgs at{e->pf.bcx, e->kc[l], e->vc[l], e->pf.y, 1.0f / sqrtf((float)hp.head_dim), T,
+                       start, hp.heads, kv, e->ctx};
+    RC(launch(e->K->attn_prefill, dim3((T + 63) / 64, kv), 0, e->stream, at));
+    RC(pf_split(e, e->pf.y, nullptr, T, dim));
+    RC(pf_gemm(e, q6(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
+    e->dispatches += 2;
+    return LFM_OK;
+}
+
+// FFN over T rows starting at x (the last layer runs only the last row).
+static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
+{
+    const lfm_hparams &hp = e->hp;
+    const uint32_t dim = hp.dim;
+    const float *norm = f32(e, "blk.%u.ffn_norm.weight", l);
+    if (l < hp.dense_lead) {
+        const uint32_t ff = hp.n_ff;
+        RC(pf_split(e, x, norm, T, dim));
+        RC(pf_gemm(e, q6(e, "blk.%u.ffn_gate.weight", l), T, e->pf.g, ff, 0, 0));
+        RC(pf_gemm(e, q6(e, "blk.%u.ffn_up.weight", l), T, e->pf.u, ff, 0, 0));
+        SwigluSplitArgs sw{e->pf.g, e->pf.u, e->pf.hi, e->pf.lo, e->pf.scale, T, ff};
+        RC(launch(e->K->swiglu_split, dim3(T), 0, e->stream, sw));
+        RC(pf_gemm(e, q6(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
+        e->dispatches += 1;
+        return LFM_OK;
+    }
+    const uint32_t eff = hp.expert_ff, E = hp.n_expert;
+    RouterPrefillArgs ra{x, norm, f32(e, "blk.%u.ffn_gate_inp.weight", l), hp.eps, e->pf.logits, T,
+                         dim, E};
+    RC(launch(e->K->router_prefill, dim3(T), dim * 4, e->stream, ra));
+    RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
+                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx};
+    RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
+    RC(pf_split(e, x, norm, T, dim));
+    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), eff, T, e->pf.tok, e->pf.g, eff));
+    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_up_exps.weight", l), eff, T, e->pf.tok, e->pf.u, eff));
+    SwigluSplitArgs sw{e->pf.g, e->pf.u, e->pf.hi, e->pf.lo, e->pf.scale, 4 * T, eff};
+    RC(launch(e->K->swiglu_split, dim3(4 * T), 0, e->stream, sw));
+    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim));
+    CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
+    RC(launch(e->K->combine_prefill, dim3((dim + 255) / 256, T), 0, e->stream, cb));
+    e->dispatches += 4;
+    return LFM_OK;
+}
+
+// Runs the layer stack for e->ids[0..T) at positions start.. and leaves the
+// last token's residual in e->x.
+static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
+{
+    const lfm_hparams &hp = e->hp;
+    EmbedRowsArgs em{q6(e, "token_embd.weight"), e->ids, e->pf.x, T};
+    RC(launch(e->K->embed_rows, dim3((T + 3) / 4), 0, e->stream, em));
+    e->dispatches += 1;
+    for (uint32_t l = 0; l < hp.n_layers; ++l) {
+        RC(pf_mixer(e, l, T, start));
+        if (l + 1 < hp.n_layers)
+            RC(pf_ffn(e, l, e->pf.x, T));
+        else
+            RC(pf_ffn(e, l, e->pf.x + (size_t)(T - 1) * hp.dim, 1));
+    }
+    HIPCHK(hipMemcpyAsync(e->x, e->pf.x + (size_t)(T - 1) * hp.dim, hp.dim * 4,
+                          hipMemcpyDeviceToDevice, e->stream));
+    return LFM_OK;
 }
 
 // ------------------------------------------------------------------ forward
@@ -970,9 +1229,13 @@ static int run_prompt(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t s
     RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu)); // also waits for prior use of host_ids
     memcpy(e->host_ids, ids, (size_t)n * 4);
     HIPCHK(hipMemcpyAsync(e->ids, e->host_ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
-    for (uint32_t j = 0; j < n; ++j) {
-        HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
-        e->dispatches += e->nodes_layers;
+    if (n >= 2 && !e->stepwise_prefill) {
+        RC(enq_prefill(e, n, start)); // matrix-core path
+    } else {
+        for (uint32_t j = 0; j < n; ++j) { // one captured decode step per token
+            HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
+            e->dispatches += e->nodes_layers;
+        }
     }
     RC(enq_head(e, 0));
     return LFM_OK;
@@ -1139,6 +1402,14 @@ extern "C" int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap)
 }
 
 extern "C" uint64_t lfm_dispatch_count(const lfm_engine *e) { return e ? e->dispatches : 0; }
+
+extern "C" int lfm_engine_set_prefill_mode(lfm_engine *e, int stepwise)
+{
+    if (!e)
+        return fail(LFM_EINVAL, "engine is null");
+    e->stepwise_prefill = stepwise != 0;
+    return LFM_OK;
+}
 
 extern "C" int lfm_device_name(const lfm_engine *e, char *buf, size_t cap)
 {

@@ -159,3 +159,93 @@ struct DequantArgs {
     float *out;
     uint32_t in_dim;
 };
+
+// ---- prefill (multi-token) path ----------------------------------------------
+// RMSNorm (optional) + binary16 hi/lo split of T rows of K floats, with a per-row
+// power-of-two scale so that |x / scale| < 2^14 (hi/lo then hold ~22 bits).
+struct SplitArgs {
+    const float *x;      // [T][K]
+    const float *norm_w; // nullable
+    float eps;
+    uint16_t *hi, *lo;   // [T][K] binary16
+    float *scale;        // [T]
+    uint32_t T, K;
+};
+
+// C[slot(n)][col0 + r] (+)= scale[tok(n)] * sum_k W[z*zrows + r][k] * X[tok(n)][k]
+// for r < zrows, n < count; blockIdx.z = z selects a weight slice (expert) and
+// its token list (grouped GEMM).  Plain GEMM: zrows = w.rows, lists null.
+struct GemmArgs {
+    Q6T w;
+    const uint16_t *x_hi, *x_lo;
+    const float *xscale;
+    const uint32_t *tok;    // [z][list_stride] activation rows, nullable
+    const uint32_t *slot;   // [z][list_stride] output rows, nullable
+    const uint32_t *counts; // [z] token counts, nullable (then ntok)
+    uint32_t ntok, list_stride, zrows;
+    float *c;
+    uint32_t ldc, col0, mode;
+};
+
+struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t
+    const float *bcx;     // [T][3*dim] in_proj rows B, C, X
+    const float *conv_w;  // [dim][3]
+    float *state;         // [dim][2] in: before the chunk, out: after it
+    float *y;             // [T][dim]
+    uint32_t T, dim;
+};
+
+struct RopeKvArgs {       // per token: q/k head norm + RoPE, K/V to the binary16 cache
+    float *qkv;           // [T][dim + 2*hdkv], q rotated in place
+    const float *q_norm, *k_norm, *rope;
+    float eps;
+    uint16_t *kcache, *vcache;  // [kv][ctx][64]
+    uint32_t T, start, heads, kv, ctx;
+};
+
+struct AttnPrefillArgs {  // causal GQA attention of T queries at positions start + t
+    const float *qkv;     // [T][dim + 2*hdkv] (q already normed + rotated)
+    const uint16_t *kcache, *vcache;
+    float *out;           // [T][dim]
+    float scale;
+    uint32_t T, start, heads, kv, ctx;
+};
+
+struct SwigluSplitArgs {  // sw = silu(g) * u, then binary16 hi/lo split with row scale
+    const float *g, *u;   // [T][ff]
+    uint16_t *hi, *lo;
+    float *scale;
+    uint32_t T, ff;
+};
+
+struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)
+    const float *x;         // [T][dim]
+    const float *norm_w, *w;
+    float eps;
+    float *logits;          // [T][n_expert]
+    uint32_t T, dim, n_expert;
+};
+
+struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token, rank) list
+    const float *logits, *bias;
+    uint32_t *sel;        // [T][4] ids
+    float *wsel;          // [T][4] weights
+    uint32_t *counts;     // [n_expert]
+    uint32_t *tok;        // [n_expert][list_stride] activation row (token)
+    uint32_t *slot;       // [n_expert][list_stride] slot = t*4 + rank
+    uint32_t T, n_expert, n_used, list_stride;
+};
+
+struct CombinePrefillArgs {  // x[t] += sum_r w[t][r] * D[t*4 + r] (rank order)
+    const float *d;          // [T*4][dim]
+    const float *wsel;       // [T][4]
+    float *x;                // [T][dim]
+    uint32_t T, dim, n_used;
+};
+
+struct EmbedRowsArgs {
+    Q6T emb;
+    const uint32_t *ids;  // [T]
+    float *x;             // [T][dim]
+    uint32_t T;
+};

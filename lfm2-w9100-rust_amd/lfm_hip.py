@@ -118,6 +118,7 @@ def lib():
         "lfm_restore_session": (i32, [P, u32, pu8, sz]),
         "lfm_snapshot_logits": (i32, [P, pf32, sz]),
         "lfm_dispatch_count": (u64, [P]), "lfm_device_name": (i32, [P, C.c_char_p, sz]),
+        "lfm_engine_set_prefill_mode": (i32, [P, i32]),
         "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
@@ -130,6 +131,7 @@ def lib():
         "lfm_q6k_dequant": (i32, [P, u64, u64, P, P]),
         "lfm_q6k_matvec": (i32, [P, u64, u64, P, P, P]),
         "lfm_q6k_matvec_time": (i32, [P, u32, u64, u64, P, P, u32, pf32]),
+        "lfm_q6k_gemm": (i32, [P, u64, u64, P, u32, P, P]),
         "lfm_argmax": (i32, [P, u32, pu32, pf32]),
         "lfm_synth_default_opts": (None, [C.POINTER(SynthOpts)]),
         "lfm_model_tensor_count": (i32, [C.POINTER(Hparams)]),
@@ -307,6 +309,18 @@ class Q6Weight:
         return yb.download(np.float32)
 
 
+def q6k_gemm(w: "Q6Weight", x: np.ndarray) -> np.ndarray:
+    """Prefill GEMM: y[t] = W x[t] for every row t of x [T][in_dim] (matrix cores)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    if x.ndim != 2 or x.shape[1] != w.in_dim:
+        raise LfmError(LFM_EINVAL, "x must be [T][in_dim]")
+    xb = DeviceBuffer.from_array(x)
+    yb = DeviceBuffer(T * w.rows * 4)
+    _check(lib().lfm_q6k_gemm(w.buf.ptr, w.rows, w.in_dim, xb.ptr, T, yb.ptr, None))
+    return yb.download(np.float32).reshape(T, w.rows)
+
+
 def q6k_matvec_time(weights: DeviceBuffer, ncopies: int, rows: int, in_dim: int,
                     x: DeviceBuffer, y: DeviceBuffer, iters: int) -> float:
     ms = C.c_float(0)
@@ -415,6 +429,10 @@ class GpuEngine:
         out = np.empty(self.hp.vocab, dtype=np.float32)
         _check(lib().lfm_snapshot_logits(self._e, _f32p(out), out.size))
         return out
+
+    def set_prefill_mode(self, stepwise: bool):
+        """False: batched matrix-core prefill (default); True: one decode step per token."""
+        _check(lib().lfm_engine_set_prefill_mode(self._e, 1 if stepwise else 0))
 
     def dispatch_count(self) -> int:
         return int(lib().lfm_dispatch_count(self._e))

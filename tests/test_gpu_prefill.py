@@ -1,0 +1,99 @@
+"""GPU parity of the batched (matrix-core) prefill against the oracle.
+
+A multi-token forward (lfm.rs:290-694 with n > 1) runs every projection as a
+Q6_K GEMM over the chunk's tokens.  Bars: last-token logits rel-L2 <= 1e-3
+against the oracle's token-by-token forward and against the engine's own
+one-decode-step-per-token mode; resident KV / conv state rel-L2 <= 1e-3;
+greedy continuation equal wherever the oracle's top-2 margin exceeds
+1e-3 * max|logit|.  Relative L2 = ||gpu - oracle|| / ||oracle||
+(bin/q6_check.rs:120-136 convention).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from model_util import gpu_engine, model_tensors, oracle_engine, top2_margin
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def real_width(gpu):
+    """Real widths (dim 2048, 32 experts top-4, ff 1792 / 7168), four layers."""
+    hp = gpu.make_hparams(dim=2048, heads=32, n_layers=4, attention_layers=(1, 3), kv=8,
+                          vocab=8192, eos=1 << 30, n_expert=32, n_used=4, expert_ff=1792,
+                          n_ff=7168, dense_lead=2)
+    return hp, model_tensors(hp)
+
+
+@pytest.fixture(scope="module")
+def crowded(gpu):
+    """8 experts top-2 so that experts take more than one 128-token tile."""
+    hp = gpu.make_hparams(dim=512, heads=8, n_layers=4, attention_layers=(1, 3), kv=2,
+                          vocab=1000, eos=1 << 30, n_expert=8, n_used=2, expert_ff=512,
+                          n_ff=1024, dense_lead=1)
+    return hp, model_tensors(hp, gpu.synth_opts(0x9E3779B97F4A7C15, bias_sigma=0.1))
+
+
+def check_prefill(gpu, oracle, hp, tensors, n, ctx):
+    prompt = [int(t) for t in np.random.default_rng(n).integers(0, hp.vocab, n)]
+    g = gpu_engine(hp, tensors, ctx=ctx)
+    o = oracle_engine(oracle, hp, tensors, ctx=ctx)
+    lg = g.forward(prompt, 0)
+    lo = o.forward(prompt, 0)
+    err = rel_l2(lg, lo)
+    sg = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    so = np.frombuffer(o.snapshot(n), np.float32)
+    serr = rel_l2(sg, so)
+    print(f"T={n}: logits rel-L2 {err:.3e}, state rel-L2 {serr:.3e}")
+    assert err <= 1e-3
+    assert serr <= 1e-3
+    # the engine's token-by-token mode gives the same answer
+    s = gpu_engine(hp, tensors, ctx=ctx)
+    s.set_prefill_mode(True)
+    ls = s.forward(prompt, 0)
+    assert rel_l2(lg, ls) <= 1e-3
+    return g, o, prompt, lg, lo
+
+
+@pytest.mark.parametrize("n", [2, 24, 300])
+def test_prefill_real_width(gpu, oracle, real_width, n):
+    hp, tensors = real_width
+    check_prefill(gpu, oracle, hp, tensors, n, ctx=512)
+
+
+@pytest.mark.parametrize("n", [129, 400])
+def test_prefill_crowded_experts(gpu, oracle, crowded, n):
+    hp, tensors = crowded
+    check_prefill(gpu, oracle, hp, tensors, n, ctx=512)
+
+
+def test_prefill_chunks_then_decode(gpu, oracle, real_width):
+    """Two batched chunks (the second at start > 0 reads the first's KV and conv
+    state), then the device-resident greedy loop."""
+    hp, tensors = real_width
+    n, cut = 200, 130
+    prompt = [int(t) for t in np.random.default_rng(7).integers(0, hp.vocab, n)]
+    g = gpu_engine(hp, tensors, ctx=512)
+    o = oracle_engine(oracle, hp, tensors, ctx=512)
+    g.forward(prompt[:cut], 0)
+    lg = g.forward(prompt[cut:], cut)
+    lo = o.forward(prompt, 0)
+    err = rel_l2(lg, lo)
+    print(f"chunked prefill logits rel-L2 {err:.3e}")
+    assert err <= 1e-3
+    tol = 1e-3 * float(np.abs(lo).max())
+    first = int(oracle.argmax(lg))
+    if top2_margin(lo) > tol:
+        assert first == oracle.argmax(lo)
+    steps = 16
+    toks = g.decode_run(first, n, steps)
+    assert len(toks) == steps
+    feed, compared = first, 0
+    for s in range(steps):
+        lo = o.forward([feed], n + s)
+        if top2_margin(lo) > tol:
+            assert toks[s] == oracle.argmax(lo), (s, toks[s], oracle.argmax(lo))
+            compared += 1
+        feed = toks[s]
+    assert compared >= steps // 2
