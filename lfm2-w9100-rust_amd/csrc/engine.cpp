@@ -69,13 +69,65 @@ extern "C" int lfm_device_count(int *count)
 }
 
 // ------------------------------------------------------------------ kernels
+// Launch shape of a decode matvec kernel: waves per workgroup (4 or 16, the
+// kernel variant) and target rows (work items) per wave, which set the grid.
+struct Shape {
+    hipFunction_t f4 = nullptr, f16 = nullptr;
+    uint32_t nw = 4, rpw = 1;
+    hipFunction_t fn() const { return nw == 16 ? f16 : f4; }
+    uint32_t threads() const { return 64 * nw; }
+    uint32_t grid(uint32_t items) const
+    {
+        const uint32_t per = nw * rpw;
+        return std::max(1u, (items + per - 1) / per);
+    }
+};
+
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
         swiglu_split, router_prefill, route_group, combine_prefill, embed_rows;
-    hipFunction_t matvec, matvec_ks, conv, qkv, attn, attn_merge, router, gateup, moe_down, head,
-        argmax, argmax_final, advance, dequant;
+    hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
+        dequant;
+    Shape matvec, conv, qkv, gateup, head;
 };
+
+// Shapes measured best on MI355X for the LFM2-8B widths; LFM_DECODE_SHAPES
+// ("matvec=4x1,conv=4x1,qkv=4x1,gateup=4x2,head=16x4") overrides them.
+static void set_shapes(Kernels *k)
+{
+    k->matvec.nw = 4, k->matvec.rpw = 1;
+    k->conv.nw = 4, k->conv.rpw = 1;
+    k->qkv.nw = 4, k->qkv.rpw = 1;
+    k->gateup.nw = 4, k->gateup.rpw = 2;
+    k->head.nw = 16, k->head.rpw = 4;
+    const char *env = getenv("LFM_DECODE_SHAPES");
+    if (!env)
+        return;
+    struct {
+        const char *name;
+        Shape *s;
+    } tab[] = {{"matvec", &k->matvec}, {"conv", &k->conv}, {"qkv", &k->qkv},
+               {"gateup", &k->gateup}, {"head", &k->head}};
+    std::string spec(env);
+    size_t pos = 0;
+    while (pos < spec.size()) {
+        size_t end = spec.find(',', pos);
+        if (end == std::string::npos)
+            end = spec.size();
+        const std::string item = spec.substr(pos, end - pos);
+        const size_t eq = item.find('='), x = item.find('x');
+        if (eq != std::string::npos && x != std::string::npos && x > eq)
+            for (auto &t : tab)
+                if (item.compare(0, eq, t.name) == 0) {
+                    const uint32_t nw = (uint32_t)atoi(item.c_str() + eq + 1);
+                    const uint32_t rpw = (uint32_t)atoi(item.c_str() + x + 1);
+                    if ((nw == 4 || nw == 16) && rpw >= 1 && rpw <= 64)
+                        t.s->nw = nw, t.s->rpw = rpw;
+                }
+        pos = end + 1;
+    }
+}
 
 static std::mutex g_kmu;
 static std::unordered_map<int, Kernels *> g_kernels;
@@ -124,13 +176,16 @@ static int get_kernels(Kernels **out)
     struct {
         hipFunction_t *f;
         const char *name;
-    } fns[] = {{&k->matvec, "k_q6_matvec"},     {&k->matvec_ks, "k_q6_matvec_ks"},
-               {&k->conv, "k_conv_inproj"},     {&k->qkv, "k_qkv"},
-               {&k->attn, "k_attn"},            {&k->attn_merge, "k_attn_merge"},
-               {&k->router, "k_router"},        {&k->gateup, "k_gateup"},
-               {&k->moe_down, "k_moe_down"},    {&k->head, "k_head"},
-               {&k->argmax, "k_argmax"},        {&k->argmax_final, "k_argmax_final"},
-               {&k->advance, "k_advance"},      {&k->dequant, "k_q6_dequant"}};
+    } fns[] = {{&k->matvec.f4, "k_q6_matvec4"},   {&k->matvec.f16, "k_q6_matvec16"},
+               {&k->matvec_ks, "k_q6_matvec_ks"}, {&k->conv.f4, "k_conv_inproj4"},
+               {&k->conv.f16, "k_conv_inproj16"}, {&k->qkv.f4, "k_qkv4"},
+               {&k->qkv.f16, "k_qkv16"},          {&k->attn, "k_attn"},
+               {&k->attn_merge, "k_attn_merge"},  {&k->router, "k_router"},
+               {&k->gateup.f4, "k_gateup4"},      {&k->gateup.f16, "k_gateup16"},
+               {&k->moe_down, "k_moe_down"},      {&k->head.f4, "k_head4"},
+               {&k->head.f16, "k_head16"},        {&k->argmax, "k_argmax"},
+               {&k->argmax_final, "k_argmax_final"}, {&k->advance, "k_advance"},
+               {&k->dequant, "k_q6_dequant"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -164,17 +219,32 @@ static int get_kernels(Kernels **out)
             return fail(LFM_EDEVICE, "hipModuleGetFunction(%s): %s", f.name, hipGetErrorString(e));
         }
     }
+    set_shapes(k);
     g_kernels[dev] = k;
     *out = k;
     return LFM_OK;
 }
 
 template <typename A>
-static int launch(hipFunction_t f, dim3 grid, uint32_t smem, hipStream_t s, const A &args)
+static int launch_t(hipFunction_t f, dim3 grid, uint32_t threads, uint32_t smem, hipStream_t s,
+                    const A &args)
 {
     void *params[] = {(void *)&args};
-    HIPCHK(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, 256, 1, 1, smem, s, params, nullptr));
+    HIPCHK(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, threads, 1, 1, smem, s, params, nullptr));
     return LFM_OK;
+}
+
+template <typename A>
+static int launch(hipFunction_t f, dim3 grid, uint32_t smem, hipStream_t s, const A &args)
+{
+    return launch_t(f, grid, 256, smem, s, args);
+}
+
+// A decode matvec kernel over `items` work items, in its tuned shape.
+template <typename A>
+static int launch_shape(const Shape &sh, uint32_t items, hipStream_t s, const A &args)
+{
+    return launch_t(sh.fn(), dim3(sh.grid(items)), sh.threads(), 0, s, args);
 }
 
 // ------------------------------------------------------------------ Q6_K layout
@@ -285,19 +355,12 @@ static uint32_t matvec_grid(uint32_t rows, uint32_t ks)
     return std::max(1u, std::min(groups, 65535u));
 }
 
-// Workgroups (4 waves) for `items` work items at about `per_wave` items per wave.
-static uint32_t wave_grid(uint32_t items, uint32_t per_wave, uint32_t cap = 4096)
-{
-    const uint32_t waves = (items + per_wave - 1) / per_wave;
-    return std::max(1u, std::min((waves + 3) / 4, cap));
-}
-
 // Launches y = W x (mode 0) or y += W x (mode 1): the one-wave-per-row kernel for
 // rows of up to 8 blocks, the split-row kernel for longer rows.
 static int launch_matvec(Kernels *K, MatvecArgs &m, hipStream_t s)
 {
     if (m.w.nb <= 8)
-        return launch(K->matvec, dim3(wave_grid(m.w.rows, 2)), 0, s, m);
+        return launch_shape(K->matvec, m.w.rows, s, m);
     RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
     return launch(K->matvec_ks, dim3(matvec_grid(m.w.rows, m.ksplit)), (m.in_dim + 16) * 4, s, m);
 }
@@ -708,7 +771,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
         a.y = e->y;
         a.dim = dim;
         a.st = e->st;
-        RC(launch(e->K->conv, dim3(wave_grid(dim, 1)), 0, e->stream, a));
+        RC(launch_shape(e->K->conv, dim, e->stream, a));
         m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
         RC(launch_matvec(e->K, m, e->stream));
         e->dispatches += 2;
@@ -724,7 +787,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     q.dim = dim;
     q.hdkv = hdkv;
     q.st = e->st;
-    RC(launch(e->K->qkv, dim3(wave_grid(dim + 2 * hdkv, 2)), 0, e->stream, q));
+    RC(launch_shape(e->K->qkv, dim + 2 * hdkv, e->stream, q));
     AttnArgs at;
     at.qkv = e->qkv;
     at.q_norm = f32(e, "blk.%u.attn_q_norm.weight", l);
@@ -782,7 +845,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
         g.wg = q6(e, "blk.%u.ffn_gate.weight", l);
         g.wu = q6(e, "blk.%u.ffn_up.weight", l);
         g.ff = hp.n_ff;
-        RC(launch(e->K->gateup, dim3(wave_grid(hp.n_ff, 2)), 0, e->stream, g));
+        RC(launch_shape(e->K->gateup, hp.n_ff, e->stream, g));
         MatvecArgs m;
         memset(&m, 0, sizeof(m));
         m.w = q6(e, "blk.%u.ffn_down.weight", l);
@@ -805,17 +868,19 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
     RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), 0, e->stream, r));
     g = moe_gateup_args(e, l);
     const Route route = g.route;
-    RC(launch(e->K->gateup, dim3(wave_grid(hp.n_used * hp.expert_ff, 2)), 0, e->stream, g));
+    RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));
     MoeDownArgs d;
     d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
     d.sw = e->sw;
     d.route = route;
-    d.route.sel_out = nullptr;
+    d.route.sel_out = e->sel; // routing stored by the gate/up kernel
     d.x = e->x;
     d.dim = dim;
     d.ff = hp.expert_ff;
     d.st = e->st;
-    RC(launch(e->K->moe_down, dim3(std::max(1u, std::min((dim + 7) / 8, 4096u))), 0, e->stream, d));
+    if (!d.route.sel_out)
+        return fail(LFM_EINTERNAL, "down projection launched without the routing buffer");
+    RC(launch_t(e->K->moe_down, dim3((dim + 7) / 8), 1024, 0, e->stream, d));
     e->dispatches += 3;
     return LFM_OK;
 }
@@ -829,7 +894,7 @@ static int enq_head(lfm_engine *e, uint32_t advance)
     h.partial = e->hpart;
     h.vocab = e->hp.vocab;
     h.st = e->st;
-    RC(launch(e->K->head, dim3(e->head_grid), 0, e->stream, h));
+    RC(launch_t(e->K->head.fn(), dim3(e->head_grid), e->K->head.threads(), 0, e->stream, h));
     FinalArgs f{e->hpart, e->head_grid, e->out_tokens, advance, e->st};
     RC(launch(e->K->argmax_final, dim3(1), 0, e->stream, f));
     e->dispatches += 2;
@@ -904,7 +969,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     for (uint32_t l = 0; l < hp.n_layers; ++l)
         max_hdkv = std::max(max_hdkv, 64 * hp.kv_heads[l]);
     e->nchunk = (e->ctx + 127) / 128;
-    e->head_grid = wave_grid(hp.vocab, 16, 1024);
+    e->head_grid = e->K->head.grid(hp.vocab);
     {
         // NEOX RoPE angles as lfm.rs:251-256 computes them: tscale = theta^(-2/hd)
         // (powf), theta_p = pos * tscale^p with f32 square-and-multiply powi, then
@@ -1445,7 +1510,7 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
     for (uint32_t r = 0; r < reps && rc == LFM_OK; ++r)
         for (uint32_t l = hp.dense_lead; l < hp.n_layers && rc == LFM_OK; ++l) {
             GateUpArgs a = moe_gateup_args(e, l);
-            rc = launch(e->K->gateup, dim3(wave_grid(hp.n_used * hp.expert_ff, 2)), 0, e->stream, a);
+            rc = launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, a);
         }
     hipError_t ce = hipStreamEndCapture(e->stream, &g);
     if (rc != LFM_OK || ce != hipSuccess) {

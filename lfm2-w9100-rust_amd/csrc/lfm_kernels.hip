@@ -109,73 +109,106 @@ __device__ __forceinline__ float lane_dot(const Lane &w, const LaneX &X)
     return half_bits_to_float(w.d) * part;
 }
 
-// ------------------------------------------------------------ input vector
-// A wave holds the input vector in registers: lane (b, c) owns the 32 values
-// at lane_pos(b, c, s, i), i.e. exactly the positions its Q6_K chunk multiplies.
-// RMSNorm x * (1 / sqrt(sum x^2 / n + eps)) * w (lfm.rs:231-244) is a wave
-// reduction, identical in every wave.  For the first kernel of a step the
-// vector is the dequantized embedding row DevState::tok (lfm.rs:310-320); wave
-// 0 of workgroup 0 also stores it as the residual.
-__device__ __forceinline__ void wave_x(const XSrc &src, uint32_t nb, const DevState *st, LaneX &X,
-                                       bool writer)
+// ------------------------------------------------------------ staged input
+// The input vector of a decode matvec (n <= 2048 values) is staged once per
+// workgroup in LDS: xs[k] = x[k] * w[k] with w the RMSNorm weight, or x[k].
+// RMSNorm's scalar inv = 1 / sqrt(sum x^2 / n + eps) (lfm.rs:231-244) then
+// multiplies each finished dot product: row = inv * (W (x . w)).  That keeps
+// the reduction off the path of the weight loads, which every kernel issues
+// before staging.
+#define XS_MAX 2048
+
+struct XRaw {
+    float4 x0, x1, w0, w1;
+};
+
+// Issues the loads of this thread's 8 values (positions 8t .. 8t+7).
+__device__ __forceinline__ void x_issue(const XSrc &s, uint32_t n, XRaw &r)
 {
-    const uint32_t lane = threadIdx.x & 63, b = lane >> 3, c = lane & 7;
-    const bool active = b < nb;
-    const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i)
-        v[i] = 0.f;
-    if (src.embed) {
-        if (active) {
-            lane_dequant(load_lane(src.emb, st->tok, b, c), v);
-            if (writer && src.x_out)
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        src.x_out[base + s * 32 + i] = v[s * 8 + i];
-        }
-    } else if (active) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float4 a = *reinterpret_cast<const float4 *>(src.x + base + s * 32);
-            const float4 bb = *reinterpret_cast<const float4 *>(src.x + base + s * 32 + 4);
-            v[s * 8 + 0] = a.x, v[s * 8 + 1] = a.y, v[s * 8 + 2] = a.z, v[s * 8 + 3] = a.w;
-            v[s * 8 + 4] = bb.x, v[s * 8 + 5] = bb.y, v[s * 8 + 6] = bb.z, v[s * 8 + 7] = bb.w;
-        }
-    }
-    if (src.norm_w) {
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            ss += v[i] * v[i];
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)(nb * 256) + src.eps);
-        if (active) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const float4 a = *reinterpret_cast<const float4 *>(src.norm_w + base + s * 32);
-                const float4 bb = *reinterpret_cast<const float4 *>(src.norm_w + base + s * 32 + 4);
-                const float w8[8] = {a.x, a.y, a.z, a.w, bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    v[s * 8 + i] = v[s * 8 + i] * inv * w8[i];
-            }
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        float t = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            X.v[s * 8 + i] = v[s * 8 + i];
-            t += v[s * 8 + i];
-        }
-        X.s32[s] = 32.f * t;
+    const uint32_t k = threadIdx.x * 8;
+    if (s.embed || k >= n)
+        return;
+    r.x0 = *reinterpret_cast<const float4 *>(s.x + k);
+    r.x1 = *reinterpret_cast<const float4 *>(s.x + k + 4);
+    if (s.norm_w) {
+        r.w0 = *reinterpret_cast<const float4 *>(s.norm_w + k);
+        r.w1 = *reinterpret_cast<const float4 *>(s.norm_w + k + 4);
     }
 }
 
+// Writes the staged vector, synchronizes the workgroup (every thread must
+// call it) and returns inv (1 without a norm).  For the first kernel of a step
+// the vector is the dequantized embedding row DevState::tok (lfm.rs:310-320),
+// built by wave 0; workgroup 0 also stores it as the residual x_out.
+template <int NW>
+__device__ __forceinline__ float x_stage(const XSrc &s, uint32_t n, const DevState *st,
+                                         const XRaw &r, float *xs, float *red)
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float ss = 0.f;
+    if (s.embed) {
+        const uint32_t b = lane >> 3, c = lane & 7;
+        if (wave == 0 && b < n / 256) {
+            float v[32];
+            lane_dequant(load_lane(s.emb, st->tok, b, c), v);
+            const bool writer = blockIdx.x == 0 && s.x_out != nullptr;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t pos = lane_pos(b, c, s4, i);
+                    const float val = v[s4 * 8 + i];
+                    if (writer)
+                        s.x_out[pos] = val;
+                    ss += val * val;
+                    xs[pos] = s.norm_w ? val * s.norm_w[pos] : val;
+                }
+        }
+    } else {
+        const uint32_t k = tid * 8;
+        if (k < n) {
+            const float v[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+            float o[8];
+            if (s.norm_w) {
+                const float w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    ss += v[i] * v[i];
+                    o[i] = v[i] * w[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    o[i] = v[i];
+            }
+            *reinterpret_cast<float4 *>(xs + k) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4 *>(xs + k + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+    }
+    if (s.norm_w) {
+        ss = wave_sum(ss);
+        if (lane == 0)
+            red[wave] = ss;
+    }
+    __syncthreads();
+    if (!s.norm_w)
+        return 1.0f;
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+        tot += red[w];
+    return 1.0f / sqrtf(tot / (float)n + s.eps);
+}
+
+// A lane's 32 staged values (zero for lanes past the row's blocks).
+__device__ __forceinline__ void lanex_lds(LaneX &X, const float *xs, uint32_t b, uint32_t c,
+                                          bool active)
+{
+    if (active)
+        load_lanex(X, xs, b, c);
+    else
+        zero_lanex(X);
+}
 // Sums two per-lane partials across the wave (results in every lane).
 __device__ __forceinline__ void wave_sum2(float &a, float &b)
 {
@@ -196,11 +229,14 @@ __device__ __forceinline__ void wave_sum3(float &a, float &b, float &c)
     }
 }
 
-// MoE routing of one token (lfm.rs:613-637, resident.rs:58-99), computed by a
-// whole wave from the router logits: sigmoid probabilities, score = p + bias,
-// n_used rounds of (max score, then lowest id among equals), weights
-// p / max(sum in rank order, 2^-14).  The results are wave-uniform and kept in
-// scalar registers (no small arrays: dynamically indexed ones end up in memory).
+// MoE routing of one token (lfm.rs:613-637, resident.rs:58-99), computed by
+// every wave from the router logits: p = sigmoid(logit), score = p + bias.
+// Expert e's place in the stable descending sort of the scores is
+//   #{j : s_j > s_e} + #{j < e : s_j == s_e},
+// counted over readlanes of the scores; places 0 .. n_used-1 are selected and
+// weighted p / max(sum in rank order, 2^-14).  With NaN scores the ids are
+// still valid experts.  Results are wave-uniform scalars (small arrays would
+// be placed in memory).
 struct Routed {
     uint32_t id0, id1, id2, id3;
     float w0, w1, w2, w3;
@@ -214,42 +250,34 @@ struct Routed {
     }
 };
 
-__device__ __forceinline__ uint32_t uniform_u32(uint32_t v)
+__device__ __forceinline__ float lane_f32(float v, uint32_t j)
 {
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
-}
-
-__device__ __forceinline__ float uniform_f32(float v)
-{
-    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)j));
 }
 
 __device__ __forceinline__ Routed wave_route(const Route &r)
 {
     const uint32_t lane = threadIdx.x & 63;
+    const bool valid = lane < r.n_expert;
     float prob = 0.f, score = -INFINITY;
-    if (lane < r.n_expert) {
+    if (valid) {
         const float lg = r.logits[lane];
         prob = 1.0f / (1.0f + expf(-lg));
         score = prob + r.bias[lane];
+    }
+    uint32_t place = 0;
+    for (uint32_t j = 0; j < r.n_expert; ++j) {
+        const float sj = lane_f32(score, j);
+        place += (sj > score || (sj == score && j < lane)) ? 1u : 0u;
     }
     uint32_t id[4];
     float p[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        id[k] = 0;
-        p[k] = 0.f;
-        if ((uint32_t)k < r.n_used) {
-            const float best = wave_max(score);
-            const uint32_t cand = (lane < r.n_expert && score == best) ? lane : 0xFFFFFFFFu;
-            uint32_t e = wave_min_u32(cand);
-            if (e >= r.n_expert) // only with NaN logits: fall back to a valid expert
-                e = 0;
-            id[k] = uniform_u32(e);
-            p[k] = uniform_f32(__shfl(prob, (int)e, 64));
-            if (lane == e)
-                score = -INFINITY;
-        }
+        const uint64_t m = __ballot(valid && place == (uint32_t)k);
+        const uint32_t e = ((uint32_t)k < r.n_used && m) ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
+        id[k] = e;
+        p[k] = (uint32_t)k < r.n_used ? lane_f32(prob, e) : 0.f;
     }
     float wsum = 0.f;
 #pragma unroll
@@ -264,49 +292,24 @@ __device__ __forceinline__ Routed wave_route(const Route &r)
     return o;
 }
 
-// Double-buffered streaming of one wave's work items.  The wave's items are
-// it = first + k*W (k = 0, 1, ...) below `total`; each item is NR Q6_K rows.
-// Two groups of G items are in flight: group A is reduced while group B's loads
-// are outstanding, then A is refilled, so the wave keeps up to 2*G items of
-// weights in flight without copying registers between iterations (a copy
-// would force a wait for the loads just issued).  `prologue` runs after the
-// first loads are issued (it builds the input vector meanwhile).
+// One wave's work items are it = first + k*W (k = 0, 1, ...) below `total`;
+// each item is NR Q6_K rows.  Kernels load G items, reduce them, load the
+// next G; the first group's loads are issued before the input is staged.
 template <int NR> struct Item {
     Lane l[NR];
 };
 
-template <int NR, int G, typename LoadF, typename PrologueF, typename UseF>
-__device__ __forceinline__ void stream_items(uint32_t first, uint32_t W, uint32_t total, LoadF load,
-                                             PrologueF prologue, UseF use)
+template <int NR, int G, typename LoadF>
+__device__ __forceinline__ void fill_items(Item<NR> (&buf)[G], uint32_t it0, uint32_t W,
+                                           uint32_t total, LoadF load)
 {
-    Item<NR> A[G], B[G];
-    const uint32_t nitems = first < total ? (total - first + W - 1) / W : 0;
-    const uint32_t ngroups = (nitems + G - 1) / G;
-    auto fill = [&](Item<NR> *buf, uint32_t g) {
 #pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const uint32_t k = g * G + j;
-            if (k < nitems)
-                load(first + k * W, buf[j]);
-        }
-    };
-    if (ngroups > 0)
-        fill(A, 0);
-    if (ngroups > 1)
-        fill(B, 1);
-    prologue();
-    for (uint32_t g = 0; g < ngroups; g += 2) {
-        use(A, g * G, nitems);
-        if (g + 2 < ngroups)
-            fill(A, g + 2);
-        if (g + 1 < ngroups) {
-            use(B, (g + 1) * G, nitems);
-            if (g + 3 < ngroups)
-                fill(B, g + 3);
-        }
+    for (int g = 0; g < G; ++g) {
+        const uint32_t it = it0 + g * W;
+        if (it < total)
+            load(it, buf[g]);
     }
 }
-
 // Wave sum of N per-lane values at once (results in every lane).
 template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 {
@@ -319,39 +322,55 @@ template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 
 // ------------------------------------------------------------------ kernels
 // Q6_K matvec y = W x (mode 0) or y += W x (mode 1), rows of up to 8 blocks:
-// one wave per row, rows streamed two at a time with two more in flight.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec(const MatvecArgs a)
+// one wave per row, G rows in flight per wave, input staged per workgroup.
+template <int NW, int G>
+__device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
 {
     if (a.st && a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
-    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave, rows = a.w.rows;
+    auto load = [&](uint32_t r, Item<1> &it) {
+        if (active)
+            it.l[0] = load_lane(a.w, r, b, c);
+    };
+    XRaw raw;
+    x_issue(a.src, a.in_dim, raw);
+    Item<1> buf[G];
+    fill_items(buf, first, W, rows, load);
+    const float inv = x_stage<NW>(a.src, a.in_dim, a.st, raw, xs, red);
     LaneX X;
-    stream_items<1, 2>(
-        first, W, a.w.rows,
-        [&](uint32_t r, Item<1> &it) {
-            if (active)
-                it.l[0] = load_lane(a.w, r, b, c);
-        },
-        [&]() { wave_x(a.src, a.w.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
-        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
-            float p[2];
+    lanex_lds(X, xs, b, c, active);
+    for (uint32_t it0 = first; it0 < rows; it0 += G * W) {
+        if (it0 != first)
+            fill_items(buf, it0, W, rows, load);
+        float p[G];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
-            wave_sum_n<2>(p);
-            if (lane == 0)
+        for (int g = 0; g < G; ++g)
+            p[g] = (active && it0 + g * W < rows) ? lane_dot(buf[g].l[0], X) : 0.f;
+        wave_sum_n<G>(p);
+        if (lane == 0)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    if (k0 + j < n) {
-                        const uint32_t r = first + (k0 + j) * W;
-                        a.y[r] = a.mode ? a.y[r] + p[j] : p[j];
-                    }
-        });
+            for (int g = 0; g < G; ++g) {
+                const uint32_t r = it0 + g * W;
+                if (r < rows)
+                    a.y[r] = a.mode ? a.y[r] + inv * p[g] : inv * p[g];
+            }
+    }
 }
 
+extern "C" __global__ __launch_bounds__(256) void k_q6_matvec4(const MatvecArgs a)
+{
+    q6_matvec_body<4, 2>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArgs a)
+{
+    q6_matvec_body<16, 2>(a);
+}
 // Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
 // `ksplit` waves share a row (nbw blocks each); x staged in LDS; partials
 // combined in wave order.
@@ -423,41 +442,64 @@ __device__ __forceinline__ void conv_step(float B, float C, float Xv, const floa
     s2[1] = bx;
 }
 
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_inproj(const ConvInprojArgs a)
+// in_proj rows B[ch], C[ch], X[ch] of channel ch form one work item.
+template <int NW, int G>
+__device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
 {
     if (a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
-    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave, dim = a.dim;
+    const uint32_t dim = a.dim, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
+    auto load = [&](uint32_t ch, Item<3> &it) {
+        if (active) {
+            it.l[0] = load_lane(a.w, ch, b, c);
+            it.l[1] = load_lane(a.w, dim + ch, b, c);
+            it.l[2] = load_lane(a.w, 2 * dim + ch, b, c);
+        }
+    };
+    XRaw raw;
+    x_issue(a.src, dim, raw);
+    Item<3> buf[G];
+    fill_items(buf, first, W, dim, load);
+    const float inv = x_stage<NW>(a.src, dim, a.st, raw, xs, red);
     LaneX X;
-    stream_items<3, 1>(
-        first, W, dim,
-        [&](uint32_t ch, Item<3> &it) {
-            if (active) {
-                it.l[0] = load_lane(a.w, ch, b, c);
-                it.l[1] = load_lane(a.w, dim + ch, b, c);
-                it.l[2] = load_lane(a.w, 2 * dim + ch, b, c);
-            }
-        },
-        [&]() { wave_x(a.src, a.w.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
-        [&](Item<3> *buf, uint32_t k0, uint32_t n) {
-            float p[3] = {0.f, 0.f, 0.f};
-            if (active && k0 < n)
+    lanex_lds(X, xs, b, c, active);
+    for (uint32_t it0 = first; it0 < dim; it0 += G * W) {
+        if (it0 != first)
+            fill_items(buf, it0, W, dim, load);
+        float p[3 * G];
 #pragma unroll
-                for (int j = 0; j < 3; ++j)
-                    p[j] = lane_dot(buf[0].l[j], X);
-            wave_sum_n<3>(p);
-            if (lane == 0 && k0 < n) {
-                const uint32_t ch = first + k0 * W;
-                conv_step(p[0], p[1], p[2], a.conv_w + ch * 3, a.state + ch * 2, a.y + ch);
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                p[3 * g + j] = (active && it0 + g * W < dim) ? lane_dot(buf[g].l[j], X) : 0.f;
+        wave_sum_n<3 * G>(p);
+        if (lane == 0)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const uint32_t ch = it0 + g * W;
+                if (ch < dim)
+                    conv_step(inv * p[3 * g], inv * p[3 * g + 1], inv * p[3 * g + 2],
+                              a.conv_w + ch * 3, a.state + ch * 2, a.y + ch);
             }
-        });
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void k_conv_inproj4(const ConvInprojArgs a)
+{
+    conv_inproj_body<4, 1>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_conv_inproj16(const ConvInprojArgs a)
+{
+    conv_inproj_body<16, 1>(a);
 }
 
 // Attention projections: rows of q (dim), k and v (hdkv each) of the normed
-// input, written raw to qkv[0 .. dim + 2*hdkv).
+// input, written to qkv[0 .. dim + 2*hdkv).
 __device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t b, uint32_t c)
 {
     if (r < a.dim)
@@ -467,36 +509,52 @@ __device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t 
     return load_lane(a.wv, r - a.dim - a.hdkv, b, c);
 }
 
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_qkv(const QkvArgs a)
+template <int NW, int G>
+__device__ __forceinline__ void qkv_body(const QkvArgs &a)
 {
     if (a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wq.nb;
-    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    const uint32_t rows = a.dim + 2 * a.hdkv, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
+    auto load = [&](uint32_t r, Item<1> &it) {
+        if (active)
+            it.l[0] = qkv_lane(a, r, b, c);
+    };
+    XRaw raw;
+    x_issue(a.src, a.dim, raw);
+    Item<1> buf[G];
+    fill_items(buf, first, W, rows, load);
+    const float inv = x_stage<NW>(a.src, a.dim, a.st, raw, xs, red);
     LaneX X;
-    stream_items<1, 2>(
-        first, W, a.dim + 2 * a.hdkv,
-        [&](uint32_t r, Item<1> &it) {
-            if (active)
-                it.l[0] = qkv_lane(a, r, b, c);
-        },
-        [&]() { wave_x(a.src, a.wq.nb, a.st, X, blockIdx.x == 0 && wave == 0); },
-        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
-            float p[2];
+    lanex_lds(X, xs, b, c, active);
+    for (uint32_t it0 = first; it0 < rows; it0 += G * W) {
+        if (it0 != first)
+            fill_items(buf, it0, W, rows, load);
+        float p[G];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
-            wave_sum_n<2>(p);
-            if (lane == 0)
+        for (int g = 0; g < G; ++g)
+            p[g] = (active && it0 + g * W < rows) ? lane_dot(buf[g].l[0], X) : 0.f;
+        wave_sum_n<G>(p);
+        if (lane == 0)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    if (k0 + j < n)
-                        a.qkv[first + (k0 + j) * W] = p[j];
-        });
+            for (int g = 0; g < G; ++g)
+                if (it0 + g * W < rows)
+                    a.qkv[it0 + g * W] = inv * p[g];
+    }
 }
 
+extern "C" __global__ __launch_bounds__(256) void k_qkv4(const QkvArgs a)
+{
+    qkv_body<4, 2>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_qkv16(const QkvArgs a)
+{
+    qkv_body<16, 2>(a);
+}
 // Per-head RMSNorm then NEOX RoPE of one 64-wide head held one value per lane
 // (lfm.rs:270-286 then 248-267): v *= inv * w[d]; pairs (d, d+32) rotated by
 // theta = pos * tscale^(d%32).  cs_sn is the position's row of the (cos, sin)
@@ -681,19 +739,22 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge(const Attn
 
 // MoE router logits W_r h (f32 weights [n_expert][dim], lfm.rs:599-607): one
 // wave per expert row.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router(const RouterArgs a)
+extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 {
     if (a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[4];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7, nb = a.dim / 256;
     const uint32_t e = blockIdx.x * 4 + wave;
-    if (e >= a.n_expert)
-        return;
+    const bool active = e < a.n_expert && b < nb;
+    XRaw raw;
+    x_issue(a.src, a.dim, raw);
     float wv[32];
-    const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
-    const float *w = a.w + (size_t)e * a.dim;
-    if (b < nb) {
+    if (active) {
+        const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
+        const float *w = a.w + (size_t)e * a.dim;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const float4 x0 = *reinterpret_cast<const float4 *>(w + base + s * 32);
@@ -702,28 +763,36 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router(const RouterAr
             wv[s * 8 + 4] = x1.x, wv[s * 8 + 5] = x1.y, wv[s * 8 + 6] = x1.z, wv[s * 8 + 7] = x1.w;
         }
     }
+    const float inv = x_stage<4>(a.src, a.dim, a.st, raw, xs, red);
     LaneX X;
-    wave_x(a.src, nb, a.st, X, false);
+    lanex_lds(X, xs, b, c, active);
     float acc = 0.f;
-    if (b < nb)
+    if (active)
 #pragma unroll
         for (int i = 0; i < 32; ++i)
             acc += wv[i] * X.v[i];
     acc = wave_sum(acc);
-    if (lane == 0)
-        a.logits[e] = acc;
+    if (lane == 0 && e < a.n_expert)
+        a.logits[e] = inv * acc;
 }
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
-// Routed: work item (rank, row) reads expert ids[rank]'s rows.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gateup(const GateUpArgs a)
+// Routed: work item (rank, row) reads expert ids[rank]'s rows; workgroup 0
+// stores the routing (ids, weights) for the down projection.
+template <int NW, int G>
+__device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
     if (a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wg.nb;
     const bool routed = a.route.logits != nullptr;
+    const uint32_t n = a.wg.nb * 256;
+    XRaw raw;
+    x_issue(a.src, n, raw);
     Routed rt = {0, 0, 0, 0, 0.f, 0.f, 0.f, 0.f};
     uint32_t nrank = 1;
     if (routed) {
@@ -734,34 +803,57 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gateup(const GateUpAr
             a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
         }
     }
-    const uint32_t ff = a.ff, W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    const uint32_t ff = a.ff, total = nrank * ff;
+    const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
+    auto load = [&](uint32_t it, Item<2> &buf) {
+        const uint32_t rank = it / ff, r = it - rank * ff;
+        const uint32_t row = routed ? rt.id(rank) * ff + r : r;
+        if (active) {
+            buf.l[0] = load_lane(a.wg, row, b, c);
+            buf.l[1] = load_lane(a.wu, row, b, c);
+        }
+    };
+    Item<2> buf[G];
+    fill_items(buf, first, W, total, load);
+    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     LaneX X;
-    stream_items<2, 1>(
-        first, W, nrank * ff,
-        [&](uint32_t it, Item<2> &buf) {
-            const uint32_t rank = it / ff, r = it - rank * ff;
-            const uint32_t row = routed ? rt.id(rank) * ff + r : r;
-            if (active) {
-                buf.l[0] = load_lane(a.wg, row, b, c);
-                buf.l[1] = load_lane(a.wu, row, b, c);
-            }
-        },
-        [&]() { wave_x(a.src, a.wg.nb, a.st, X, false); },
-        [&](Item<2> *buf, uint32_t k0, uint32_t n) {
-            float p[2] = {0.f, 0.f};
-            if (active && k0 < n) {
-                p[0] = lane_dot(buf[0].l[0], X);
-                p[1] = lane_dot(buf[0].l[1], X);
-            }
-            wave_sum_n<2>(p);
-            if (lane == 0 && k0 < n)
-                a.sw[first + k0 * W] = p[0] / (1.0f + expf(-p[0])) * p[1];
-        });
+    lanex_lds(X, xs, b, c, active);
+    for (uint32_t it0 = first; it0 < total; it0 += G * W) {
+        if (it0 != first)
+            fill_items(buf, it0, W, total, load);
+        float p[2 * G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const bool ok = active && it0 + g * W < total;
+            p[2 * g] = ok ? lane_dot(buf[g].l[0], X) : 0.f;
+            p[2 * g + 1] = ok ? lane_dot(buf[g].l[1], X) : 0.f;
+        }
+        wave_sum_n<2 * G>(p);
+        if (lane == 0)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                if (it0 + g * W < total) {
+                    const float gv = inv * p[2 * g], uv = inv * p[2 * g + 1];
+                    a.sw[it0 + g * W] = gv / (1.0f + expf(-gv)) * uv;
+                }
+    }
 }
 
-// Routed down projections and combine (lfm.rs:660-668, resident.rs:101-117):
-// wave r computes d_r = (Wd[e_r] sw_r)[k] for 4 rows; then per row
-// x[k] += ((((0 + d_0 w_0) + d_1 w_1) + d_2 w_2) + d_3 w_3)  (no contraction).
+extern "C" __global__ __launch_bounds__(256) void k_gateup4(const GateUpArgs a)
+{
+    gateup_body<4, 1>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_gateup16(const GateUpArgs a)
+{
+    gateup_body<16, 1>(a);
+}
+
+// Routed down projections and combine (lfm.rs:660-668, resident.rs:101-117).
+// A workgroup of 16 waves owns DOWN_ROWS output rows: wave w computes rows
+// k0 + w/4 and k0 + w/4 + 4 of the expert of rank w%4, from that rank's sw
+// staged in LDS; then per row
+//   x[k] += ((((0 + d_0 w_0) + d_1 w_1) + d_2 w_2) + d_3 w_3)  (no contraction).
+// The routing comes from the gate/up kernel (ids, then weight bits).
 __device__ __forceinline__ float combine(const float *dv, const float *wv, uint32_t n, float x)
 {
 #pragma clang fp contract(off)
@@ -771,50 +863,48 @@ __device__ __forceinline__ float combine(const float *dv, const float *wv, uint3
     return x + s;
 }
 
-#define DOWN_ROWS 8 // output rows per workgroup pass (each wave: its expert's 8 rows)
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_moe_down(const MoeDownArgs a)
+#define DOWN_ROWS 8
+extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs a)
 {
-    if (a.st->halt)
+    if (a.st->halt || !a.route.sel_out)
         return;
-    __shared__ float red[DOWN_ROWS][4];
+    __shared__ __attribute__((aligned(16))) float xs[4 * XS_MAX];
+    __shared__ float dsh[DOWN_ROWS][4];
     __shared__ float wsh[4];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t b = lane >> 3, c = lane & 7;
-    const Routed rt = wave_route(a.route);
-    const uint32_t n_used = a.route.n_used;
-    const bool active = b < a.wd.nb && wave < n_used;
-    const uint32_t e = rt.id(wave);
-    if (tid < 4)
-        wsh[tid] = rt.w(tid);
-    const uint32_t dim = a.dim;
-    for (uint32_t k0 = blockIdx.x * DOWN_ROWS; k0 < dim; k0 += gridDim.x * DOWN_ROWS) {
-        Lane l[DOWN_ROWS];
-        if (active)
+    const uint32_t rank = wave & 3, slot = wave >> 2;
+    const uint32_t n_used = a.route.n_used, ff = a.ff, dim = a.dim;
+    const bool active = b < a.wd.nb && rank < n_used;
+    const uint32_t e = min(a.route.sel_out[rank], a.route.n_expert - 1);
+    const uint32_t k0 = blockIdx.x * DOWN_ROWS;
+    Item<1> buf[2];
 #pragma unroll
-            for (int i = 0; i < DOWN_ROWS; ++i)
-                if (k0 + i < dim)
-                    l[i] = load_lane(a.wd, e * dim + k0 + i, b, c);
-        LaneX X;
-        if (active)
-            load_lanex(X, a.sw + (size_t)wave * a.ff, b, c);
-        else
-            zero_lanex(X);
-        float p[DOWN_ROWS];
-#pragma unroll
-        for (int i = 0; i < DOWN_ROWS; ++i)
-            p[i] = (active && k0 + i < dim) ? lane_dot(l[i], X) : 0.f;
-        wave_sum_n<DOWN_ROWS>(p);
-        if (lane == 0)
-#pragma unroll
-            for (int i = 0; i < DOWN_ROWS; ++i)
-                red[i][wave] = p[i];
-        __syncthreads();
-        if (tid < DOWN_ROWS && k0 + tid < dim)
-            a.x[k0 + tid] = combine(red[tid], wsh, n_used, a.x[k0 + tid]);
-        __syncthreads();
+    for (int g = 0; g < 2; ++g) {
+        const uint32_t k = k0 + slot + 4 * g;
+        if (active && k < dim)
+            buf[g].l[0] = load_lane(a.wd, e * dim + k, b, c);
     }
+    if (tid < 4)
+        wsh[tid] = __uint_as_float(a.route.sel_out[8 + tid]);
+    for (uint32_t i = tid * 4; i < n_used * ff; i += 1024 * 4)
+        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.sw + i);
+    __syncthreads();
+    LaneX X;
+    lanex_lds(X, xs + rank * ff, b, c, active);
+    float p[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+        p[g] = (active && k0 + slot + 4 * g < dim) ? lane_dot(buf[g].l[0], X) : 0.f;
+    wave_sum_n<2>(p);
+    if (lane == 0) {
+        dsh[slot][rank] = p[0];
+        dsh[slot + 4][rank] = p[1];
+    }
+    __syncthreads();
+    if (tid < DOWN_ROWS && k0 + tid < dim)
+        a.x[k0 + tid] = combine(dsh[tid], wsh, n_used, a.x[k0 + tid]);
 }
-
 // (value, index) merge for greedy argmax (main.rs:112-141): the larger value
 // wins; equal values keep the lower index; -inf is "no candidate" and NaN
 // never wins; with no candidate the index is 0.
@@ -837,10 +927,10 @@ __device__ __forceinline__ void amax_wave(float &bv, uint32_t &bi)
 }
 
 // Workgroup-level merge of per-wave (value, index); result in thread 0.
-__device__ __forceinline__ void amax_block(float &bv, uint32_t &bi)
+template <int NW = 4> __device__ __forceinline__ void amax_block(float &bv, uint32_t &bi)
 {
-    __shared__ float rv[4];
-    __shared__ uint32_t ri[4];
+    __shared__ float rv[NW];
+    __shared__ uint32_t ri[NW];
     const uint32_t tid = threadIdx.x;
     amax_wave(bv, bi);
     if ((tid & 63) == 0) {
@@ -849,54 +939,72 @@ __device__ __forceinline__ void amax_block(float &bv, uint32_t &bi)
     }
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < NW; ++w)
             amax_merge(bv, bi, rv[w], ri[w]);
     }
 }
 
-// Final RMSNorm + tied Q6_K head (lfm.rs:676-693): one wave per row, rows
-// streamed two at a time with two more in flight; each workgroup leaves its
-// argmax (value, index) partial for k_argmax_final.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_head(const HeadArgs a)
+// Final RMSNorm + tied Q6_K head (lfm.rs:676-693): one wave per row, G rows
+// in flight; each workgroup leaves its argmax (value, index) partial for
+// k_argmax_final.
+template <int NW, int G>
+__device__ __forceinline__ void head_body(const HeadArgs &a)
 {
     if (a.st->halt)
         return;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.emb.nb;
-    const uint32_t W = gridDim.x * 4, first = blockIdx.x * 4 + wave;
+    const uint32_t rows = a.vocab, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
+    auto load = [&](uint32_t r, Item<1> &it) {
+        if (active)
+            it.l[0] = load_lane(a.emb, r, b, c);
+    };
+    XRaw raw;
+    x_issue(a.src, a.emb.nb * 256, raw);
+    Item<1> buf[G];
+    fill_items(buf, first, W, rows, load);
+    const float inv = x_stage<NW>(a.src, a.emb.nb * 256, a.st, raw, xs, red);
     LaneX X;
+    lanex_lds(X, xs, b, c, active);
     float bv = -INFINITY;
     uint32_t bi = 0;
-    stream_items<1, 2>(
-        first, W, a.vocab,
-        [&](uint32_t r, Item<1> &it) {
-            if (active)
-                it.l[0] = load_lane(a.emb, r, b, c);
-        },
-        [&]() { wave_x(a.src, a.emb.nb, a.st, X, false); },
-        [&](Item<1> *buf, uint32_t k0, uint32_t n) {
-            float p[2];
+    for (uint32_t it0 = first; it0 < rows; it0 += G * W) {
+        if (it0 != first)
+            fill_items(buf, it0, W, rows, load);
+        float p[G];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                p[j] = (active && k0 + j < n) ? lane_dot(buf[j].l[0], X) : 0.f;
-            wave_sum_n<2>(p);
+        for (int g = 0; g < G; ++g)
+            p[g] = (active && it0 + g * W < rows) ? lane_dot(buf[g].l[0], X) : 0.f;
+        wave_sum_n<G>(p);
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                if (k0 + j < n) {
-                    const uint32_t r = first + (k0 + j) * W;
-                    if (lane == 0)
-                        a.logits[r] = p[j];
-                    amax_merge(bv, bi, p[j], r);
-                }
-        });
-    amax_block(bv, bi);
+        for (int g = 0; g < G; ++g) {
+            const uint32_t r = it0 + g * W;
+            if (r < rows) {
+                const float v = inv * p[g];
+                if (lane == 0)
+                    a.logits[r] = v;
+                amax_merge(bv, bi, v, r);
+            }
+        }
+    }
+    amax_block<NW>(bv, bi);
     if (threadIdx.x == 0) {
         a.partial[2 * blockIdx.x] = bv;
         a.partial[2 * blockIdx.x + 1] = __uint_as_float(bi);
     }
 }
 
+extern "C" __global__ __launch_bounds__(256) void k_head4(const HeadArgs a)
+{
+    head_body<4, 2>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_head16(const HeadArgs a)
+{
+    head_body<16, 2>(a);
+}
 // Per-workgroup argmax partials of a plain vector.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax(const ArgmaxArgs a)
 {
@@ -904,7 +1012,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax(const ArgmaxAr
     uint32_t bi = 0;
     for (uint32_t i = blockIdx.x * WG_THREADS + threadIdx.x; i < a.n; i += gridDim.x * WG_THREADS)
         amax_merge(bv, bi, a.v[i], i);
-    amax_block(bv, bi);
+    amax_block<>(bv, bi);
     if (threadIdx.x == 0) {
         a.partial[2 * blockIdx.x] = bv;
         a.partial[2 * blockIdx.x + 1] = __uint_as_float(bi);
@@ -921,7 +1029,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax_final(const Fi
     uint32_t bi = 0;
     for (uint32_t i = threadIdx.x; i < a.n_partial; i += WG_THREADS)
         amax_merge(bv, bi, a.partial[2 * i], __float_as_uint(a.partial[2 * i + 1]));
-    amax_block(bv, bi);
+    amax_block<>(bv, bi);
     if (threadIdx.x == 0) {
         if (!(bv > -INFINITY))
             bi = 0;
