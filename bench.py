@@ -10,7 +10,8 @@ prompt of (4096 - steps) uniform ids prefilled, then `steps` greedy tokens at
 positions 3840..4095.  Warmup steps run first and the resident state is then
 restored to the end of the prompt, so the timed steps are exactly the workload.
 
-Prints one JSON line (see DESIGN.md for the fields).
+Prints one JSON line: metric, value (tok/s), ms_per_step, roofline of the dominant
+kernel, the CPU baseline and prefill figures.
 """
 import argparse
 import json
@@ -116,8 +117,8 @@ def main():
                          "prompt positions instead (isolates decode kernels for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: the batch-1 decode path is not sharded across GPUs "
-              "(see DESIGN.md, 'Sharding'); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the batch-1 decode path runs on a single GPU and is "
+              "not sharded here; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     assert lfm_hip.device_count() > 0, "no HIP device"
     if args.steps < 1 or args.steps + 1 > args.ctx:

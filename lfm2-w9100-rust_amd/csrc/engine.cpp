@@ -90,17 +90,18 @@ struct Kernels {
     hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant;
     Shape matvec, conv, qkv, gateup, head;
+    DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
 };
 
 // Shapes measured best on MI355X for the LFM2-8B widths; LFM_DECODE_SHAPES
-// ("matvec=4x1,conv=4x1,qkv=4x1,gateup=4x2,head=16x4") overrides them.
+// ("matvec=4x1,conv=4x1,qkv=4x1,gateup=4x2,head=4x16") overrides them.
 static void set_shapes(Kernels *k)
 {
     k->matvec.nw = 4, k->matvec.rpw = 1;
     k->conv.nw = 4, k->conv.rpw = 1;
     k->qkv.nw = 4, k->qkv.rpw = 1;
     k->gateup.nw = 4, k->gateup.rpw = 2;
-    k->head.nw = 16, k->head.rpw = 4;
+    k->head.nw = 4, k->head.rpw = 16;
     const char *env = getenv("LFM_DECODE_SHAPES");
     if (!env)
         return;
@@ -220,6 +221,13 @@ static int get_kernels(Kernels **out)
         }
     }
     set_shapes(k);
+    if (hipMalloc(&k->idle_st, sizeof(DevState)) != hipSuccess ||
+        hipMemset(k->idle_st, 0, sizeof(DevState)) != hipSuccess) {
+        (void)hipModuleUnload(k->mod);
+        (void)hipModuleUnload(k->pmod);
+        delete k;
+        return fail(LFM_EDEVICE, "device state allocation failed");
+    }
     g_kernels[dev] = k;
     *out = k;
     return LFM_OK;
@@ -359,6 +367,8 @@ static uint32_t matvec_grid(uint32_t rows, uint32_t ks)
 // rows of up to 8 blocks, the split-row kernel for longer rows.
 static int launch_matvec(Kernels *K, MatvecArgs &m, hipStream_t s)
 {
+    if (!m.st)
+        m.st = K->idle_st;
     if (m.w.nb <= 8)
         return launch_shape(K->matvec, m.w.rows, s, m);
     RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
@@ -805,7 +815,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     at.st = e->st;
     RC(launch(e->K->attn, dim3(e->nchunk, kv), 0, e->stream, at));
     AttnMergeArgs mg{e->apart, e->y, hp.heads, kv, e->nchunk, e->st};
-    RC(launch(e->K->attn_merge, dim3(kv), 0, e->stream, mg));
+    RC(launch(e->K->attn_merge, dim3(kv, hp.heads / kv), 0, e->stream, mg));
     m.w = q6(e, "blk.%u.attn_output.weight", l);
     RC(launch_matvec(e->K, m, e->stream));
     e->dispatches += 4;
@@ -865,7 +875,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
     r.dim = dim;
     r.n_expert = hp.n_expert;
     r.st = e->st;
-    RC(launch(e->K->router, dim3((hp.n_expert + 3) / 4), 0, e->stream, r));
+    RC(launch(e->K->router, dim3(hp.n_expert), 0, e->stream, r));
     g = moe_gateup_args(e, l);
     const Route route = g.route;
     RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));

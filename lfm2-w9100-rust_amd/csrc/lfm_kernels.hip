@@ -28,32 +28,42 @@
 #define ATT_KROW 72 // LDS row stride of a K row, in halves (144 B: conflict-free 16-B reads)
 
 // ---------------------------------------------------------------- wave helpers
+// Wave-wide reductions with DPP lane moves (quad permutes, row shifts, row
+// broadcasts: all VALU, no LDS round trips); the total lands in lane 63 and
+// is broadcast with readlane.  Every lane of the wave must be active.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v, float old)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL,
+                                                                 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane63(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        v += __shfl_xor(v, off, 64);
-    return v;
+    v += dpp_mov<0xb1>(v, 0.f);  // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4e>(v, 0.f);  // quad_perm [2,3,0,1]
+    v += dpp_mov<0x114>(v, 0.f); // row_shr:4
+    v += dpp_mov<0x118>(v, 0.f); // row_shr:8
+    v += dpp_mov<0x142>(v, 0.f); // row_bcast:15
+    v += dpp_mov<0x143>(v, 0.f); // row_bcast:31
+    return lane63(v);
 }
 
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, dpp_mov<0xb1>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x4e>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x114>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x118>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x142>(v, -INFINITY));
+    v = fmaxf(v, dpp_mov<0x143>(v, -INFINITY));
+    return lane63(v);
 }
-
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-        v = o < v ? o : v;
-    }
-    return v;
-}
-
 
 // Activation values of a lane's 32 positions plus 32 * (sum of each group of 8).
 struct LaneX {
@@ -107,6 +117,14 @@ __device__ __forceinline__ float lane_dot(const Lane &w, const LaneX &X)
         part += scv * (acc - X.s32[s]);
     }
     return half_bits_to_float(w.d) * part;
+}
+
+// The step's halt flag, read with a vector load: waiting for it (vmcnt counts
+// in issue order) then leaves the weight loads issued after it in flight,
+// where a scalar load's wait would also hold back everything issued later.
+__device__ __forceinline__ uint32_t load_halt(const DevState *st)
+{
+    return __hip_atomic_load(&st->halt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------ staged input
@@ -209,34 +227,27 @@ __device__ __forceinline__ void lanex_lds(LaneX &X, const float *xs, uint32_t b,
     else
         zero_lanex(X);
 }
-// Sums two per-lane partials across the wave (results in every lane).
+// Sums of two / three per-lane partials across the wave (results in every lane).
 __device__ __forceinline__ void wave_sum2(float &a, float &b)
 {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        a += __shfl_xor(a, off, 64);
-        b += __shfl_xor(b, off, 64);
-    }
+    a = wave_sum(a);
+    b = wave_sum(b);
 }
 
 __device__ __forceinline__ void wave_sum3(float &a, float &b, float &c)
 {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        a += __shfl_xor(a, off, 64);
-        b += __shfl_xor(b, off, 64);
-        c += __shfl_xor(c, off, 64);
-    }
+    a = wave_sum(a);
+    b = wave_sum(b);
+    c = wave_sum(c);
 }
 
 // MoE routing of one token (lfm.rs:613-637, resident.rs:58-99), computed by
 // every wave from the router logits: p = sigmoid(logit), score = p + bias.
-// Expert e's place in the stable descending sort of the scores is
-//   #{j : s_j > s_e} + #{j < e : s_j == s_e},
-// counted over readlanes of the scores; places 0 .. n_used-1 are selected and
-// weighted p / max(sum in rank order, 2^-14).  With NaN scores the ids are
-// still valid experts.  Results are wave-uniform scalars (small arrays would
-// be placed in memory).
+// Round k takes the largest remaining score, the lowest expert id among equal
+// scores (the order of a stable descending sort); the n_used picks are
+// weighted p / max(sum in rank order, 2^-14).  NaN scores are never picked
+// while a finite one remains; the ids are always valid experts.  Results are
+// wave-uniform scalars (small arrays would be placed in memory).
 struct Routed {
     uint32_t id0, id1, id2, id3;
     float w0, w1, w2, w3;
@@ -265,19 +276,21 @@ __device__ __forceinline__ Routed wave_route(const Route &r)
         prob = 1.0f / (1.0f + expf(-lg));
         score = prob + r.bias[lane];
     }
-    uint32_t place = 0;
-    for (uint32_t j = 0; j < r.n_expert; ++j) {
-        const float sj = lane_f32(score, j);
-        place += (sj > score || (sj == score && j < lane)) ? 1u : 0u;
-    }
     uint32_t id[4];
     float p[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint64_t m = __ballot(valid && place == (uint32_t)k);
-        const uint32_t e = ((uint32_t)k < r.n_used && m) ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
-        id[k] = e;
-        p[k] = (uint32_t)k < r.n_used ? lane_f32(prob, e) : 0.f;
+        id[k] = 0;
+        p[k] = 0.f;
+        if ((uint32_t)k < r.n_used) {
+            const float best = wave_max(score);
+            const uint64_t m = __ballot(valid && score == best);
+            const uint32_t e = m ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
+            id[k] = e;
+            p[k] = lane_f32(prob, e);
+            if (lane == e)
+                score = -INFINITY;
+        }
     }
     float wsum = 0.f;
 #pragma unroll
@@ -314,10 +327,8 @@ __device__ __forceinline__ void fill_items(Item<NR> (&buf)[G], uint32_t it0, uin
 template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int i = 0; i < N; ++i)
-            v[i] += __shfl_xor(v[i], off, 64);
+    for (int i = 0; i < N; ++i)
+        v[i] = wave_sum(v[i]);
 }
 
 // ------------------------------------------------------------------ kernels
@@ -326,8 +337,7 @@ template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 template <int NW, int G>
 __device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
 {
-    if (a.st && a.st->halt)
-        return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -342,6 +352,8 @@ __device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
     x_issue(a.src, a.in_dim, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    if (halted) // checked after the loads are issued (the flag's latency overlaps them)
+        return;
     const float inv = x_stage<NW>(a.src, a.in_dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
@@ -446,8 +458,7 @@ __device__ __forceinline__ void conv_step(float B, float C, float Xv, const floa
 template <int NW, int G>
 __device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
 {
-    if (a.st->halt)
-        return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -465,6 +476,8 @@ __device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
     x_issue(a.src, dim, raw);
     Item<3> buf[G];
     fill_items(buf, first, W, dim, load);
+    if (halted)
+        return;
     const float inv = x_stage<NW>(a.src, dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
@@ -512,8 +525,7 @@ __device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t 
 template <int NW, int G>
 __device__ __forceinline__ void qkv_body(const QkvArgs &a)
 {
-    if (a.st->halt)
-        return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -528,6 +540,8 @@ __device__ __forceinline__ void qkv_body(const QkvArgs &a)
     x_issue(a.src, a.dim, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    if (halted)
+        return;
     const float inv = x_stage<NW>(a.src, a.dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
@@ -697,24 +711,30 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     }
 }
 
-// Combines the chunk partials of each head: out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.
+// Combines the chunk partials of one head (workgroup (kv head, q head of the
+// group)): out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c.  Four groups of
+// 64 threads take every fourth chunk, all loads in flight at once, then the
+// four partial merges are combined.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge(const AttnMergeArgs a)
 {
     if (a.st->halt)
         return;
-    const uint32_t kh = blockIdx.x, hh = threadIdx.x >> 6, d = threadIdx.x & 63;
+    const uint32_t kh = blockIdx.x, hh = blockIdx.y;
     const uint32_t G = a.heads / a.kv;
     if (hh >= G)
         return;
+    __shared__ float gm[4], gl[4], go[4][64];
+    const uint32_t grp = threadIdx.x >> 6, d = threadIdx.x & 63;
     const uint32_t nact = a.st->pos / ATT_CH + 1;
     const float *pb = a.part + ((size_t)kh * a.nchunk * 4 + hh) * 66;
     float M = -INFINITY, acc = 0.f, L = 0.f;
-    for (uint32_t c0 = 0; c0 < nact; c0 += 8) { // 8 chunks' loads in flight
+    for (uint32_t c0 = grp; c0 < nact; c0 += 4 * 8) {
         float m[8], l[8], o[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float *pc = pb + (size_t)(c0 + j) * 4 * 66;
-            const bool ok = c0 + j < nact;
+            const uint32_t cc = c0 + 4 * j;
+            const bool ok = cc < nact;
+            const float *pc = pb + (size_t)(ok ? cc : 0) * 4 * 66;
             m[j] = ok ? pc[0] : -INFINITY;
             l[j] = ok ? pc[1] : 0.f;
             o[j] = ok ? pc[2 + d] : 0.f;
@@ -723,57 +743,75 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge(const Attn
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             mn = fmaxf(mn, m[j]);
-        const float r = expf(M - mn); // rescale the running sums (M = -inf first: 0)
+        const float r = M > -INFINITY ? expf(M - mn) : 0.f;
         acc *= r;
         L *= r;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float f = expf(m[j] - mn);
+            const float f = m[j] > -INFINITY ? expf(m[j] - mn) : 0.f;
             L += f * l[j];
             acc += f * o[j];
         }
         M = mn;
     }
-    a.out[(kh * G + hh) * 64 + d] = acc / L;
+    if (d == 0) {
+        gm[grp] = M;
+        gl[grp] = L;
+    }
+    go[grp][d] = acc;
+    __syncthreads();
+    if (grp == 0) {
+        const float mx = fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3]));
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float f = gm[g] > -INFINITY ? expf(gm[g] - mx) : 0.f;
+            num += f * go[g][d];
+            den += f * gl[g];
+        }
+        a.out[(kh * G + hh) * 64 + d] = num / den;
+    }
 }
 
 // MoE router logits W_r h (f32 weights [n_expert][dim], lfm.rs:599-607): one
-// wave per expert row.
+// workgroup per expert; thread t covers inputs 8t .. 8t+7, so the workgroup
+// also sums x^2 over the whole vector for the RMSNorm scale.
 extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 {
-    if (a.st->halt)
-        return;
-    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
-    __shared__ float red[4];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t b = lane >> 3, c = lane & 7, nb = a.dim / 256;
-    const uint32_t e = blockIdx.x * 4 + wave;
-    const bool active = e < a.n_expert && b < nb;
-    XRaw raw;
-    x_issue(a.src, a.dim, raw);
-    float wv[32];
-    if (active) {
-        const uint32_t base = b * 256 + (c >> 2) * 128 + (c & 3) * 8;
-        const float *w = a.w + (size_t)e * a.dim;
+    const uint32_t halted = load_halt(a.st);
+    __shared__ float red[2][4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, e = blockIdx.x;
+    const float *w = a.w + (size_t)e * a.dim;
+    float ss = 0.f, acc = 0.f;
+    for (uint32_t k = tid * 8; k < a.dim; k += 256 * 8) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(a.src.x + k);
+        const float4 x1 = *reinterpret_cast<const float4 *>(a.src.x + k + 4);
+        const float4 n0 = *reinterpret_cast<const float4 *>(a.src.norm_w + k);
+        const float4 n1 = *reinterpret_cast<const float4 *>(a.src.norm_w + k + 4);
+        const float4 w0 = *reinterpret_cast<const float4 *>(w + k);
+        const float4 w1 = *reinterpret_cast<const float4 *>(w + k + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float nv[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+        const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(w + base + s * 32);
-            const float4 x1 = *reinterpret_cast<const float4 *>(w + base + s * 32 + 4);
-            wv[s * 8 + 0] = x0.x, wv[s * 8 + 1] = x0.y, wv[s * 8 + 2] = x0.z, wv[s * 8 + 3] = x0.w;
-            wv[s * 8 + 4] = x1.x, wv[s * 8 + 5] = x1.y, wv[s * 8 + 6] = x1.z, wv[s * 8 + 7] = x1.w;
+        for (int i = 0; i < 8; ++i) {
+            ss += xv[i] * xv[i];
+            acc += wv[i] * (xv[i] * nv[i]);
         }
     }
-    const float inv = x_stage<4>(a.src, a.dim, a.st, raw, xs, red);
-    LaneX X;
-    lanex_lds(X, xs, b, c, active);
-    float acc = 0.f;
-    if (active)
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            acc += wv[i] * X.v[i];
-    acc = wave_sum(acc);
-    if (lane == 0 && e < a.n_expert)
-        a.logits[e] = inv * acc;
+    if (halted)
+        return;
+    wave_sum2(ss, acc);
+    if (lane == 0) {
+        red[0][wave] = ss;
+        red[1][wave] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float tot = ((red[0][0] + red[0][1]) + red[0][2]) + red[0][3];
+        const float dot = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+        a.logits[e] = dot / sqrtf(tot / (float)a.dim + a.src.eps);
+    }
 }
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
@@ -782,8 +820,7 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 template <int NW, int G>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
-    if (a.st->halt)
-        return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -798,10 +835,6 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     if (routed) {
         rt = wave_route(a.route);
         nrank = a.route.n_used;
-        if (blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
-            a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
-            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
-        }
     }
     const uint32_t ff = a.ff, total = nrank * ff;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
@@ -815,6 +848,12 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     };
     Item<2> buf[G];
     fill_items(buf, first, W, total, load);
+    if (halted)
+        return;
+    if (routed && blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
+        a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
+        a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
+    }
     const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
@@ -866,8 +905,9 @@ __device__ __forceinline__ float combine(const float *dv, const float *wv, uint3
 #define DOWN_ROWS 8
 extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs a)
 {
-    if (a.st->halt || !a.route.sel_out)
+    if (!a.route.sel_out)
         return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[4 * XS_MAX];
     __shared__ float dsh[DOWN_ROWS][4];
     __shared__ float wsh[4];
@@ -885,6 +925,8 @@ extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs 
         if (active && k < dim)
             buf[g].l[0] = load_lane(a.wd, e * dim + k, b, c);
     }
+    if (halted)
+        return;
     if (tid < 4)
         wsh[tid] = __uint_as_float(a.route.sel_out[8 + tid]);
     for (uint32_t i = tid * 4; i < n_used * ff; i += 1024 * 4)
@@ -950,8 +992,7 @@ template <int NW = 4> __device__ __forceinline__ void amax_block(float &bv, uint
 template <int NW, int G>
 __device__ __forceinline__ void head_body(const HeadArgs &a)
 {
-    if (a.st->halt)
-        return;
+    const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -966,6 +1007,8 @@ __device__ __forceinline__ void head_body(const HeadArgs &a)
     x_issue(a.src, a.emb.nb * 256, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    if (halted)
+        return;
     const float inv = x_stage<NW>(a.src, a.emb.nb * 256, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
@@ -1027,8 +1070,19 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax_final(const Fi
         return;
     float bv = -INFINITY;
     uint32_t bi = 0;
-    for (uint32_t i = threadIdx.x; i < a.n_partial; i += WG_THREADS)
-        amax_merge(bv, bi, a.partial[2 * i], __float_as_uint(a.partial[2 * i + 1]));
+    for (uint32_t i0 = threadIdx.x; i0 < a.n_partial; i0 += 4 * WG_THREADS) {
+        float v[4];
+        uint32_t ix[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = i0 + j * WG_THREADS;
+            v[j] = i < a.n_partial ? a.partial[2 * i] : -INFINITY;
+            ix[j] = i < a.n_partial ? __float_as_uint(a.partial[2 * i + 1]) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            amax_merge(bv, bi, v[j], ix[j]);
+    }
     amax_block<>(bv, bi);
     if (threadIdx.x == 0) {
         if (!(bv > -INFINITY))
