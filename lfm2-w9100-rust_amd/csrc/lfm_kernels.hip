@@ -593,19 +593,38 @@ __device__ __forceinline__ float head_norm_rope(float v, const float *w, float e
 // writes (max, sum, o[64]) per head; k_attn_merge combines the chunks.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a)
 {
-    if (a.st->halt)
-        return;
-    const uint32_t p = a.st->pos;
     const uint32_t kh = blockIdx.y, chunk = blockIdx.x;
     const uint32_t t0 = chunk * ATT_CH;
-    if (t0 > p)
-        return;
-    const uint32_t nact = p / ATT_CH + 1;
     const uint32_t G = a.heads / a.kv;
-    const uint32_t nt = min((uint32_t)ATT_CH, p + 1 - t0);
-    const bool cur = (chunk == nact - 1);
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t dim = a.heads * 64, hdkv = a.kv * 64;
+    // Position and halt flag with vector loads; the chunk's K/V rows, q and the
+    // new K/V values are issued before the position is known (rows past the
+    // cache end re-read its last row and are never used).
+    const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)__hip_atomic_load(&a.st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const uint32_t halted = load_halt(a.st);
+    constexpr int PASSES = ATT_CH * 8 / WG_THREADS; // 16-B pieces per thread
+    uint4 kr[PASSES], vr[PASSES];
+    {
+        const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
+        const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
+#pragma unroll
+        for (int i = 0; i < PASSES; ++i) {
+            const uint32_t u = tid + i * WG_THREADS, seg = u & 7;
+            const uint32_t row = min(t0 + (u >> 3), a.ctx - 1);
+            kr[i] = *reinterpret_cast<const uint4 *>(kg + (size_t)row * 64 + seg * 8);
+            vr[i] = *reinterpret_cast<const uint4 *>(vg + (size_t)row * 64 + seg * 8);
+        }
+    }
+    const float qraw = wave < G ? a.qkv[(kh * G + wave) * 64 + lane] : 0.f;
+    const float kraw = wave == 0 ? a.qkv[dim + kh * 64 + lane] : 0.f;
+    const float vraw = wave == 0 ? a.qkv[dim + hdkv + kh * 64 + lane] : 0.f;
+    if (halted || t0 > p)
+        return;
+    const uint32_t nact = p / ATT_CH + 1;
+    const uint32_t nt = min((uint32_t)ATT_CH, p + 1 - t0);
+    const bool cur = (chunk == nact - 1);
 
     __shared__ float qr[4][64];
     __shared__ float knew[64], vnew[64];
@@ -614,37 +633,20 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     __shared__ float sc[4][ATT_CH];
     __shared__ float stat[4][2];
 
-    // K/V rows of this chunk -> LDS (16 B per thread per pass), issued first.
-    const uint16_t *kg = a.kcache + ((size_t)kh * a.ctx + t0) * 64;
-    const uint16_t *vg = a.vcache + ((size_t)kh * a.ctx + t0) * 64;
-    {
-        constexpr int PASSES = ATT_CH * 8 / WG_THREADS; // 16-B pieces per thread
-        uint4 kr[PASSES], vr[PASSES];
 #pragma unroll
-        for (int i = 0; i < PASSES; ++i) { // rows past the chunk re-read row 0 (unused)
-            const uint32_t u = tid + i * WG_THREADS, seg = u & 7;
-            const uint32_t t = (u >> 3) < nt ? (u >> 3) : 0;
-            kr[i] = *reinterpret_cast<const uint4 *>(kg + t * 64 + seg * 8);
-            vr[i] = *reinterpret_cast<const uint4 *>(vg + t * 64 + seg * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < PASSES; ++i) {
-            const uint32_t u = tid + i * WG_THREADS, t = u >> 3, seg = u & 7;
-            if (t < nt && t0 + t != p) {
-                *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) = kr[i];
-                *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) = vr[i];
-            }
+    for (int i = 0; i < PASSES; ++i) {
+        const uint32_t u = tid + i * WG_THREADS, t = u >> 3, seg = u & 7;
+        if (t < nt && t0 + t != p) {
+            *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) = kr[i];
+            *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) = vr[i];
         }
     }
-    if (wave < G) {
-        const float v = a.qkv[(kh * G + wave) * 64 + lane];
-        qr[wave][lane] = head_norm_rope(v, a.q_norm, a.eps, a.rope + (size_t)p * 64, lane);
-    }
+    if (wave < G)
+        qr[wave][lane] = head_norm_rope(qraw, a.q_norm, a.eps, a.rope + (size_t)p * 64, lane);
     if (cur && wave == 0) {
-        const float kraw = a.qkv[dim + kh * 64 + lane];
-        const float kr = head_norm_rope(kraw, a.k_norm, a.eps, a.rope + (size_t)p * 64, lane);
-        const uint16_t kb = float_to_half_bits(kr);
-        const uint16_t vb = float_to_half_bits(a.qkv[dim + hdkv + kh * 64 + lane]);
+        const float krot = head_norm_rope(kraw, a.k_norm, a.eps, a.rope + (size_t)p * 64, lane);
+        const uint16_t kb = float_to_half_bits(krot);
+        const uint16_t vb = float_to_half_bits(vraw);
         a.kcache[((size_t)kh * a.ctx + p) * 64 + lane] = kb;
         a.vcache[((size_t)kh * a.ctx + p) * 64 + lane] = vb;
         knew[lane] = half_bits_to_float(kb);
@@ -698,6 +700,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     const uint32_t hh = tid >> 6, d = tid & 63;
     if (hh < G) {
         float acc = 0.f;
+#pragma unroll 8
         for (uint32_t t = 0; t < nt; ++t) {
             const float vv = (t0 + t == p) ? vnew[d] : half_bits_to_float(Vs[t * 64 + d]);
             acc += sc[hh][t] * vv;
@@ -815,29 +818,29 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 }
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
-// Routed: work item (rank, row) reads expert ids[rank]'s rows; workgroup 0
-// stores the routing (ids, weights) for the down projection.
+// Routed: work item (rank, row) reads expert ids[rank]'s rows.  Wave 0 of each
+// workgroup computes the routing while the input vector is staged; the other
+// waves read it from LDS after the barrier (one routing per workgroup keeps
+// the SIMDs free for the loads).  Workgroup 0 stores the routing (ids, weight
+// bits) for the down projection.  Dense: the weight loads go out first.
 template <int NW, int G>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
+    __shared__ uint32_t rid[4];
+    __shared__ float rwt[4];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wg.nb;
     const bool routed = a.route.logits != nullptr;
     const uint32_t n = a.wg.nb * 256;
+    const uint32_t ff = a.ff, total = (routed ? a.route.n_used : 1u) * ff;
+    const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     XRaw raw;
     x_issue(a.src, n, raw);
     Routed rt = {0, 0, 0, 0, 0.f, 0.f, 0.f, 0.f};
-    uint32_t nrank = 1;
-    if (routed) {
-        rt = wave_route(a.route);
-        nrank = a.route.n_used;
-    }
-    const uint32_t ff = a.ff, total = nrank * ff;
-    const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     auto load = [&](uint32_t it, Item<2> &buf) {
         const uint32_t rank = it / ff, r = it - rank * ff;
         const uint32_t row = routed ? rt.id(rank) * ff + r : r;
@@ -847,14 +850,32 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
         }
     };
     Item<2> buf[G];
-    fill_items(buf, first, W, total, load);
+    if (routed) {
+        if (wave == 0) {
+            const Routed r0 = wave_route(a.route);
+            if (lane < 4) {
+                rid[lane] = r0.id(lane);
+                rwt[lane] = r0.w(lane);
+            }
+        }
+    } else {
+        fill_items(buf, first, W, total, load);
+    }
     if (halted)
         return;
-    if (routed && blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
-        a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
-        a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
+    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red); // barrier: routing visible
+    if (routed) {
+        rt.id0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[0]);
+        rt.id1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[1]);
+        rt.id2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[2]);
+        rt.id3 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[3]);
+        rt.w0 = rwt[0], rt.w1 = rwt[1], rt.w2 = rwt[2], rt.w3 = rwt[3];
+        fill_items(buf, first, W, total, load);
+        if (blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
+            a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
+            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
+        }
     }
-    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < total; it0 += G * W) {
