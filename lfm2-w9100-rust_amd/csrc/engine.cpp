@@ -86,7 +86,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        swiglu_split, router_prefill, route_group, combine_prefill, embed_rows;
+        swiglu_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant;
     Shape matvec, conv, qkv, gateup, head;
@@ -209,7 +209,8 @@ static int get_kernels(Kernels **out)
                 {&k->conv_prefill, "k_conv_prefill"},   {&k->conv_state, "k_conv_state"},
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
                 {&k->swiglu_split, "k_swiglu_split"},   {&k->router_prefill, "k_router_prefill"},
-                {&k->route_group, "k_route_group"},     {&k->combine_prefill, "k_combine_prefill"},
+                {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
+                {&k->combine_prefill, "k_combine_prefill"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
@@ -1215,9 +1216,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
     RouterPrefillArgs ra{x, norm, f32(e, "blk.%u.ffn_gate_inp.weight", l), hp.eps, e->pf.logits, T,
                          dim, E};
-    RC(launch(e->K->router_prefill, dim3(T), dim * 4, e->stream, ra));
+    RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
     RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
                       e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx};
+    RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
     RC(pf_split(e, x, norm, T, dim));
     RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), eff, T, e->pf.tok, e->pf.g, eff));
@@ -1227,7 +1229,7 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim));
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
     RC(launch(e->K->combine_prefill, dim3((dim + 255) / 256, T), 0, e->stream, cb));
-    e->dispatches += 4;
+    e->dispatches += 5;
     return LFM_OK;
 }
 

@@ -22,48 +22,11 @@
 
 #include "kargs.h"
 #include "q6_device.h"
+#include "wave_ops.h"
 
 #define WG_THREADS 256
 #define ATT_CH 128  // attention positions per workgroup
 #define ATT_KROW 72 // LDS row stride of a K row, in halves (144 B: conflict-free 16-B reads)
-
-// ---------------------------------------------------------------- wave helpers
-// Wave-wide reductions with DPP lane moves (quad permutes, row shifts, row
-// broadcasts: all VALU, no LDS round trips); the total lands in lane 63 and
-// is broadcast with readlane.  Every lane of the wave must be active.
-template <int CTRL> __device__ __forceinline__ float dpp_mov(float v, float old)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
-                                                                 __builtin_bit_cast(int, v), CTRL,
-                                                                 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float lane63(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-__device__ __forceinline__ float wave_sum(float v)
-{
-    v += dpp_mov<0xb1>(v, 0.f);  // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4e>(v, 0.f);  // quad_perm [2,3,0,1]
-    v += dpp_mov<0x114>(v, 0.f); // row_shr:4
-    v += dpp_mov<0x118>(v, 0.f); // row_shr:8
-    v += dpp_mov<0x142>(v, 0.f); // row_bcast:15
-    v += dpp_mov<0x143>(v, 0.f); // row_bcast:31
-    return lane63(v);
-}
-
-__device__ __forceinline__ float wave_max(float v)
-{
-    v = fmaxf(v, dpp_mov<0xb1>(v, -INFINITY));
-    v = fmaxf(v, dpp_mov<0x4e>(v, -INFINITY));
-    v = fmaxf(v, dpp_mov<0x114>(v, -INFINITY));
-    v = fmaxf(v, dpp_mov<0x118>(v, -INFINITY));
-    v = fmaxf(v, dpp_mov<0x142>(v, -INFINITY));
-    v = fmaxf(v, dpp_mov<0x143>(v, -INFINITY));
-    return lane63(v);
-}
 
 // Activation values of a lane's 32 positions plus 32 * (sum of each group of 8).
 struct LaneX {
@@ -239,70 +202,6 @@ __device__ __forceinline__ void wave_sum3(float &a, float &b, float &c)
     a = wave_sum(a);
     b = wave_sum(b);
     c = wave_sum(c);
-}
-
-// MoE routing of one token (lfm.rs:613-637, resident.rs:58-99), computed by
-// every wave from the router logits: p = sigmoid(logit), score = p + bias.
-// Round k takes the largest remaining score, the lowest expert id among equal
-// scores (the order of a stable descending sort); the n_used picks are
-// weighted p / max(sum in rank order, 2^-14).  NaN scores are never picked
-// while a finite one remains; the ids are always valid experts.  Results are
-// wave-uniform scalars (small arrays would be placed in memory).
-struct Routed {
-    uint32_t id0, id1, id2, id3;
-    float w0, w1, w2, w3;
-    __device__ __forceinline__ uint32_t id(uint32_t k) const
-    {
-        return k == 0 ? id0 : k == 1 ? id1 : k == 2 ? id2 : id3;
-    }
-    __device__ __forceinline__ float w(uint32_t k) const
-    {
-        return k == 0 ? w0 : k == 1 ? w1 : k == 2 ? w2 : w3;
-    }
-};
-
-__device__ __forceinline__ float lane_f32(float v, uint32_t j)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)j));
-}
-
-__device__ __forceinline__ Routed wave_route(const Route &r)
-{
-    const uint32_t lane = threadIdx.x & 63;
-    const bool valid = lane < r.n_expert;
-    float prob = 0.f, score = -INFINITY;
-    if (valid) {
-        const float lg = r.logits[lane];
-        prob = 1.0f / (1.0f + expf(-lg));
-        score = prob + r.bias[lane];
-    }
-    uint32_t id[4];
-    float p[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        id[k] = 0;
-        p[k] = 0.f;
-        if ((uint32_t)k < r.n_used) {
-            const float best = wave_max(score);
-            const uint64_t m = __ballot(valid && score == best);
-            const uint32_t e = m ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
-            id[k] = e;
-            p[k] = lane_f32(prob, e);
-            if (lane == e)
-                score = -INFINITY;
-        }
-    }
-    float wsum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if ((uint32_t)k < r.n_used)
-            wsum = wsum + p[k];
-    if (wsum < 6.103515625e-5f)
-        wsum = 6.103515625e-5f;
-    Routed o;
-    o.id0 = id[0], o.id1 = id[1], o.id2 = id[2], o.id3 = id[3];
-    o.w0 = p[0] / wsum, o.w1 = p[1] / wsum, o.w2 = p[2] / wsum, o.w3 = p[3] / wsum;
-    return o;
 }
 
 // One wave's work items are it = first + k*W (k = 0, 1, ...) below `total`;

@@ -16,6 +16,7 @@
 
 #include "kargs.h"
 #include "q6_device.h"
+#include "wave_ops.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -47,9 +48,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     float ss = 0.f;
     for (uint32_t k = threadIdx.x; k < a.K; k += WG_THREADS)
         ss += x[k] * x[k];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        ss += __shfl_xor(ss, off, 64);
+    ss = wave_sum(ss);
     if ((threadIdx.x & 63) == 0)
         red[threadIdx.x >> 6] = ss;
     __syncthreads();
@@ -60,9 +59,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
         const float v = a.norm_w ? x[k] * inv * a.norm_w[k] : x[k];
         amax = fmaxf(amax, fabsf(v));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    amax = wave_max(amax);
     if ((threadIdx.x & 63) == 0)
         redm[threadIdx.x >> 6] = amax;
     __syncthreads();
@@ -275,13 +272,6 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_state(const Conv
 }
 
 // ------------------------------------------------------------------ attention
-__device__ __forceinline__ float wsum64(float v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        v += __shfl_xor(v, off, 64);
-    return v;
-}
 
 // Per token: q heads and k heads RMS-normed over head_dim and NEOX-rotated at
 // position start + t (table row), q written back, K and V rounded to binary16 and
@@ -297,7 +287,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_rope_kv_prefill(const
     for (uint32_t h = wave; h < a.heads + a.kv; h += 4) {
         const bool isq = h < a.heads;
         float v = row[(isq ? 0 : dim) + (isq ? h : h - a.heads) * 64 + lane];
-        const float ss = wsum64(v * v);
+        const float ss = wave_sum(v * v);
         const float inv = 1.0f / sqrtf(ss / 64.0f + a.eps);
         v *= inv * (isq ? a.q_norm : a.k_norm)[lane];
         const float other = __shfl_xor(v, 32, 64);
@@ -398,9 +388,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_swiglu_split(const Sw
         const float gv = g[k];
         amax = fmaxf(amax, fabsf(gv / (1.0f + expf(-gv)) * u[k]));
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    amax = wave_max(amax);
     if ((threadIdx.x & 63) == 0)
         redm[threadIdx.x >> 6] = amax;
     __syncthreads();
@@ -419,44 +407,91 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_swiglu_split(const Sw
     }
 }
 
-// Router logits for T tokens: one workgroup per token (RMSNorm, then one wave
-// per 1/4 of the experts, f32 dots).
+// Router logits for T tokens (lfm.rs:599-607): a workgroup takes 16 tokens.
+// Each wave first finds the RMSNorm scale of 4 of them; then 256-wide slices of
+// x . w and of the f32 router rows are staged in LDS and thread (token, e)
+// accumulates its dot products in k order; logits = inv * sum.
+#define RT_TOK 16
+#define RT_K 256
+#define RT_EMAX 64
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const RouterPrefillArgs a)
 {
-    const uint32_t t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (t >= a.T)
-        return;
-    extern __shared__ float xs[];
-    __shared__ float red[4];
-    const float *x = a.x + (size_t)t * a.dim;
-    float ss = 0.f;
-    for (uint32_t k = threadIdx.x; k < a.dim; k += WG_THREADS) {
-        xs[k] = x[k];
-        ss += x[k] * x[k];
+    __shared__ float inv[RT_TOK];
+    __shared__ float xs[RT_TOK][RT_K + 1];
+    __shared__ float ws[RT_EMAX][RT_K + 1];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t t0 = blockIdx.x * RT_TOK;
+    for (uint32_t j = 0; j < RT_TOK / 4; ++j) {
+        const uint32_t tt = wave * (RT_TOK / 4) + j, t = t0 + tt;
+        if (t < a.T) { // uniform across the wave
+            const float *x = a.x + (size_t)t * a.dim;
+            float ss = 0.f;
+            for (uint32_t k = lane; k < a.dim; k += 64)
+                ss += x[k] * x[k];
+            ss = wave_sum(ss);
+            if (lane == 0)
+                inv[tt] = 1.0f / sqrtf(ss / (float)a.dim + a.eps);
+        }
     }
-    ss = wsum64(ss);
-    if (lane == 0)
-        red[wave] = ss;
-    __syncthreads();
-    const float inv = 1.0f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)a.dim + a.eps);
-    for (uint32_t k = threadIdx.x; k < a.dim; k += WG_THREADS)
-        xs[k] = xs[k] * inv * a.norm_w[k];
-    __syncthreads();
-    for (uint32_t e = wave; e < a.n_expert; e += 4) {
-        const float *w = a.w + (size_t)e * a.dim;
-        float acc = 0.f;
-        for (uint32_t k = lane; k < a.dim; k += 64)
-            acc += w[k] * xs[k];
-        acc = wsum64(acc);
-        if (lane == 0)
-            a.logits[(size_t)t * a.n_expert + e] = acc;
+    const uint32_t tt = tid / 16, eg = tid % 16;
+    float acc[RT_EMAX / 16];
+#pragma unroll
+    for (int j = 0; j < RT_EMAX / 16; ++j)
+        acc[j] = 0.f;
+    for (uint32_t k0 = 0; k0 < a.dim; k0 += RT_K) {
+        __syncthreads();
+        for (uint32_t u = tid; u < RT_TOK * RT_K; u += WG_THREADS) {
+            const uint32_t r = u / RT_K, kk = u % RT_K, t = t0 + r;
+            xs[r][kk] = t < a.T ? a.x[(size_t)t * a.dim + k0 + kk] * a.norm_w[k0 + kk] : 0.f;
+        }
+        for (uint32_t u = tid; u < a.n_expert * RT_K; u += WG_THREADS) {
+            const uint32_t e = u / RT_K, kk = u % RT_K;
+            ws[e][kk] = a.w[(size_t)e * a.dim + k0 + kk];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < RT_EMAX / 16; ++j) {
+            const uint32_t e = eg + 16 * j;
+            if (e < a.n_expert) {
+                float s = acc[j];
+                for (uint32_t kk = 0; kk < RT_K; ++kk)
+                    s += xs[tt][kk] * ws[e][kk];
+                acc[j] = s;
+            }
+        }
+    }
+    const uint32_t t = t0 + tt;
+    if (t < a.T)
+#pragma unroll
+        for (int j = 0; j < RT_EMAX / 16; ++j) {
+            const uint32_t e = eg + 16 * j;
+            if (e < a.n_expert)
+                a.logits[(size_t)t * a.n_expert + e] = inv[tt] * acc[j];
+        }
+}
+
+// Top-k per token (the decode routing rule, wave_route): one wave per token
+// stores the selected ids and weights [t][4] (unused ranks: id 0, weight 0).
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_topk(const RouteGroupArgs a)
+{
+    const uint32_t lane = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= a.T) // uniform across the wave
+        return;
+    Route r;
+    r.logits = a.logits + (size_t)t * a.n_expert;
+    r.bias = a.bias;
+    r.n_expert = a.n_expert;
+    r.n_used = a.n_used;
+    r.sel_out = nullptr;
+    const Routed rt = wave_route(r);
+    if (lane < 4) {
+        a.sel[(size_t)t * 4 + lane] = rt.id(lane);
+        a.wsel[(size_t)t * 4 + lane] = lane < a.n_used ? rt.w(lane) : 0.f;
     }
 }
 
-// Top-k per token (lfm.rs:613-637: sigmoid, score = p + bias, stable descending
-// order, weights p / max(sum, 2^-14)), then per expert the (token, rank) pairs in
-// token order.  One workgroup per expert; every workgroup recomputes the token
-// selections it scans (identical everywhere), workgroup 0 stores them.
+// Per expert (one workgroup each) the (token, rank) pairs that selected it, in
+// token order: tok[e][i] = token, slot[e][i] = token * 4 + rank; counts[e].
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const RouteGroupArgs a)
 {
     const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -469,41 +504,12 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const Rou
         const uint32_t t = t0 + tid;
         uint32_t rank_of_e = 4; // 4: not selected
         if (t < a.T) {
-            const float *lg = a.logits + (size_t)t * a.n_expert;
-            float prob[64], score[64];
-            for (uint32_t j = 0; j < a.n_expert; ++j) {
-                prob[j] = 1.0f / (1.0f + expf(-lg[j]));
-                score[j] = prob[j] + a.bias[j];
-            }
-            uint32_t ids[4] = {0, 0, 0, 0};
-            float p[4] = {0.f, 0.f, 0.f, 0.f};
-            uint64_t taken = 0;
-            for (uint32_t r = 0; r < a.n_used; ++r) {
-                uint32_t best = 0xFFFFFFFFu;
-                for (uint32_t j = 0; j < a.n_expert; ++j)
-                    if (!((taken >> j) & 1) && (best == 0xFFFFFFFFu || score[j] > score[best]))
-                        best = j;
-                if (best == 0xFFFFFFFFu)
-                    best = 0;
-                taken |= 1ull << best;
-                ids[r] = best;
-                p[r] = prob[best];
-                if (best == e)
-                    rank_of_e = r;
-            }
-            if (e == 0) {
-                float wsum = 0.f;
-                for (uint32_t r = 0; r < a.n_used; ++r)
-                    wsum = wsum + p[r];
-                if (wsum < 6.103515625e-5f)
-                    wsum = 6.103515625e-5f;
-                for (uint32_t r = 0; r < 4; ++r) {
-                    a.sel[(size_t)t * 4 + r] = ids[r];
-                    a.wsel[(size_t)t * 4 + r] = r < a.n_used ? p[r] / wsum : 0.f;
-                }
-            }
+            const uint4 s4 = *reinterpret_cast<const uint4 *>(a.sel + (size_t)t * 4);
+            const uint32_t ids[4] = {s4.x, s4.y, s4.z, s4.w};
+            for (int r = (int)a.n_used - 1; r >= 0; --r)
+                if (ids[r] == e)
+                    rank_of_e = (uint32_t)r;
         }
-        // order-preserving compaction of the tokens that chose expert e
         const bool hit = rank_of_e < 4;
         const uint64_t mask = __ballot(hit);
         const uint32_t before = __popcll(mask & ((1ull << lane) - 1ull));
