@@ -475,10 +475,12 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
-#define GEMM_TILE 128
+#define GEMM_ROWS 256   // weight rows per GEMM workgroup
+#define GEMM_TOKENS 128 // token columns per GEMM workgroup
+#define GEMM_THREADS 512
 static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz)
 {
-    return dim3((rows + GEMM_TILE - 1) / GEMM_TILE, (ntok + GEMM_TILE - 1) / GEMM_TILE, nz);
+    return dim3((rows + GEMM_ROWS - 1) / GEMM_ROWS, (ntok + GEMM_TOKENS - 1) / GEMM_TOKENS, nz);
 }
 
 // Y[t][r] = sum_k W[r][k] X[t][k] for T token rows (prefill GEMM, op level).
@@ -511,7 +513,7 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     ga.c = y;
     ga.ldc = (uint32_t)rows;
     if (rc == LFM_OK)
-        rc = launch(K->gemm_q6, gemm_grid((uint32_t)rows, T, 1), 0, s, ga);
+        rc = launch_t(K->gemm_q6, gemm_grid((uint32_t)rows, T, 1), GEMM_THREADS, 0, s, ga);
     if (rc == LFM_OK && hipStreamSynchronize(s) != hipSuccess)
         rc = fail(LFM_EDEVICE, "lfm_q6k_gemm: synchronize failed");
     (void)hipFree(hi);
@@ -1135,7 +1137,7 @@ static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t l
     g.ldc = ldc;
     g.col0 = col0;
     g.mode = mode;
-    RC(launch(e->K->gemm_q6, gemm_grid(w.rows, T, 1), 0, e->stream, g));
+    RC(launch_t(e->K->gemm_q6, gemm_grid(w.rows, T, 1), GEMM_THREADS, 0, e->stream, g));
     e->dispatches += 1;
     return LFM_OK;
 }
@@ -1158,7 +1160,7 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t
     g.zrows = zrows;
     g.c = c;
     g.ldc = ldc;
-    RC(launch(e->K->gemm_q6, gemm_grid(zrows, T, e->hp.n_expert), 0, e->stream, g));
+    RC(launch_t(e->K->gemm_q6, gemm_grid(zrows, T, e->hp.n_expert), GEMM_THREADS, 0, e->stream, g));
     e->dispatches += 1;
     return LFM_OK;
 }

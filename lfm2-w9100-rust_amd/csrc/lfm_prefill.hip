@@ -22,12 +22,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define WG_THREADS 256
-#define GM 128         // weight rows per workgroup
-#define GN 128         // token columns per workgroup
-#define GK 128         // K elements per LDS stage (half a Q6_K block)
-#define LDS_ROW 136    // halves per LDS row (GK + 8: 272 B rows keep 16-B reads conflict-free)
-
-
 // Split an f32 into binary16 hi + lo with hi = fp16(x), lo = fp16(x - hi).
 __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
 {
@@ -78,47 +72,83 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     }
 }
 
-// Decode one lane chunk (32 weights of block b, chunk c) into binary16 values
-// sc * (q - 32) at LDS row `dst` (positions s*32 + l0 + i within the half block).
-__device__ __forceinline__ void chunk_to_lds(const Q6T &t, uint32_t row, uint32_t b, uint32_t c,
-                                             _Float16 *dst)
+#define TM 256 // weight rows per workgroup (8 waves: 4 along rows x 2 along tokens)
+#define TN 128 // token columns per workgroup
+#define TK 64  // K elements per stage (a quarter Q6_K block)
+
+// LDS tiles are [row][64 halves] = 8 pieces of 16 B per row; piece p of row r
+// holds k-piece p ^ ((r >> 1) & 7), so the 16-B fragment reads of 16
+// consecutive rows fall in distinct banks.
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kp) { return r * TK + ((kp ^ ((r >> 1) & 7)) << 3); }
+
+// Raw Q6_K bytes of a thread's two (row, l0 group) units for one half block,
+// and its B pieces (hi, lo) of one stage.
+struct ARaw {
+    uint4 ql0, ql1;
+    uint2 qh0, qh1;
+    uint32_t sc0, sc1;
+};
+struct BRaw {
+    uint4 h0, h1, l0, l1;
+};
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+// Two codes c0, c1 (bytes 0, 1 or 2, 3 of `c`) -> half2 (c - 32) exactly: the
+// byte permute forms binary16 0x64cc = 1024 + c, then 1056 is subtracted.
+__device__ __forceinline__ half2v codes_lo(uint32_t c)
 {
-    const size_t nblk = (size_t)t.rows * t.nb;
-    const size_t blk = (size_t)row * t.nb + b;
-    const uint4 ql = *reinterpret_cast<const uint4 *>(t.base + blk * 128 + c * 16);
-    const uint2 qh = *reinterpret_cast<const uint2 *>(t.base + nblk * 128 + blk * 64 + c * 8);
-    const uint32_t sc = *reinterpret_cast<const uint32_t *>(t.base + nblk * 192 + blk * 16 + (c >> 1) * 4);
-    const uint32_t l0 = (c & 3) * 8;
+    const uint32_t v = __builtin_amdgcn_perm(c, 0x64646464u, 0x01050004u);
+    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1056.0f, (_Float16)1056.0f};
+}
+__device__ __forceinline__ half2v codes_hi(uint32_t c)
+{
+    const uint32_t v = __builtin_amdgcn_perm(c, 0x64646464u, 0x01070006u);
+    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1056.0f, (_Float16)1056.0f};
+}
+
+// 16 weights of one (row, l0 group) for quarter q of a half block, as binary16
+// sc * (q6 - 32) (exact while |sc * (q6 - 32)| <= 2048): positions j*32 + l0 + i
+// for j = 0, 1 (s = 2q + j), i.e. k-pieces 4j + cq of the stage.
+__device__ __forceinline__ void decode_unit(uint4 ql, uint2 qh, uint32_t sc, uint32_t q, uint32_t r,
+                                            uint32_t cq, _Float16 *A)
+{
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int scv = (int)(int8_t)(sc >> (8 * s));
-        half8 v;
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t s = 2 * q + j;
+        const _Float16 scf = (_Float16)(float)(int)(int8_t)(sc >> (8 * s));
+        const half2v sc2 = {scf, scf};
+        half2v o[4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t A = j ? ql.y : ql.x, B = j ? ql.w : ql.z, H = j ? qh.y : qh.x;
-            uint32_t q;
-            switch (s) {
-            case 0: q = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u); break;
-            case 1: q = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u); break;
-            case 2: q = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u); break;
-            default: q = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u); break;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                v[j * 4 + i] = (_Float16)(float)(scv * ((int)((q >> (8 * i)) & 0xFFu) - 32));
+        for (int w = 0; w < 2; ++w) {
+            const uint32_t Aw = w ? ql.y : ql.x, Bw = w ? ql.w : ql.z, H = w ? qh.y : qh.x;
+            uint32_t c;
+            if (q == 0)
+                c = j == 0 ? ((Aw & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u))
+                           : ((Bw & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u));
+            else
+                c = j == 0 ? (((Aw >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u))
+                           : (((Bw >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u));
+            o[2 * w] = codes_lo(c) * sc2;
+            o[2 * w + 1] = codes_hi(c) * sc2;
         }
-        *reinterpret_cast<half8 *>(dst + s * 32 + l0) = v;
+        half8 v = {o[0][0], o[0][1], o[1][0], o[1][1], o[2][0], o[2][1], o[3][0], o[3][1]};
+        *reinterpret_cast<half8 *>(A + swz(r, 4 * j + cq)) = v;
     }
 }
 
-// C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, w.rows) and token
-// columns n < ntok.  Column n reads activation row (tok ? tok[n] : n) and writes
-// output row (slot ? slot[n] : n).  Tiles of 128 rows x 128 tokens per
-// workgroup; each wave owns 64 x 64 (2 x 2 MFMA 32x32 tiles).
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_q6(const GemmArgs a)
+// C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, zrows) of group
+// z and token columns n < ntok.  Column n reads activation row (tok ? tok[n] :
+// n) and writes output row (slot ? slot[n] : n).  A workgroup computes 256 rows
+// x 128 tokens; each wave 64 x 64 with v_mfma_f32_32x32x16_f16 on the decoded
+// weights and the hi / lo activation halves.  K advances in 64-wide stages
+// through double-buffered LDS: while the matrix cores work on stage s, the
+// wave decodes stage s+1's weights and stores its activations, and the loads
+// for the stage after that are in flight (one barrier per stage).  Each Q6_K
+// block's partial product is scaled by its d in fp32.
+extern "C" __global__ __launch_bounds__(512) void k_gemm_q6(const GemmArgs a)
 {
     const uint32_t z = blockIdx.z;
-    const uint32_t m0 = blockIdx.x * GM, n0 = blockIdx.y * GN;
+    const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
@@ -127,13 +157,62 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_q6(const GemmArg
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
     const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
-    __shared__ __attribute__((aligned(16))) _Float16 As[GM * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 Bh[GN * LDS_ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 Bl[GN * LDS_ROW];
-    __shared__ float dsh[GM];
+    __shared__ __attribute__((aligned(16))) _Float16 As[2][TM * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TN * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TN * TK];
+    __shared__ float dsh[2][TM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
-    const uint32_t K = a.w.nb * 256;
+    const uint32_t wm = (wave & 3) * 64, wn = (wave >> 2) * 64;
+    const uint32_t nb = a.w.nb, K = nb * 256;
+    const size_t nblk = (size_t)a.w.rows * nb;
+    // A units: unit u = tid + 512 v -> row u >> 2, l0 group u & 3
+    const uint32_t ar0 = tid >> 2, ar1 = (tid + 512) >> 2, acq = tid & 3;
+    const uint32_t arow0 = rbase + min(m0 + ar0, a.zrows - 1), arow1 = rbase + min(m0 + ar1, a.zrows - 1);
+    // B pieces: piece u = tid + 512 v -> token row u >> 3, k-piece u & 7
+    const uint32_t bkp = tid & 7, bn0 = tid >> 3, bn1 = (tid + 512) >> 3;
+    uint32_t bsrc0, bsrc1;
+    {
+        uint32_t col;
+        col = min(n0 + bn0, ntok - 1); bsrc0 = tokl ? tokl[col] : col;
+        col = min(n0 + bn1, ntok - 1); bsrc1 = tokl ? tokl[col] : col;
+    }
+    auto loadA = [=](uint32_t half) -> ARaw {
+        ARaw R;
+        const uint32_t kb = half >> 1, c = (half & 1) * 4 + acq;
+        const size_t b0 = (size_t)arow0 * nb + kb, b1 = (size_t)arow1 * nb + kb;
+        R.ql0 = *reinterpret_cast<const uint4 *>(a.w.base + b0 * 128 + c * 16);
+        R.ql1 = *reinterpret_cast<const uint4 *>(a.w.base + b1 * 128 + c * 16);
+        R.qh0 = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + b0 * 64 + c * 8);
+        R.qh1 = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + b1 * 64 + c * 8);
+        R.sc0 = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + b0 * 16 + (c >> 1) * 4);
+        R.sc1 = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + b1 * 16 + (c >> 1) * 4);
+        return R;
+    };
+    auto loadB = [=](uint32_t st) -> BRaw {
+        BRaw R;
+        const size_t k = (size_t)st * TK + bkp * 8;
+        R.h0 = *reinterpret_cast<const uint4 *>(xh + (size_t)bsrc0 * K + k);
+        R.h1 = *reinterpret_cast<const uint4 *>(xh + (size_t)bsrc1 * K + k);
+        R.l0 = *reinterpret_cast<const uint4 *>(xl + (size_t)bsrc0 * K + k);
+        R.l1 = *reinterpret_cast<const uint4 *>(xl + (size_t)bsrc1 * K + k);
+        return R;
+    };
+    auto storeB = [&](const BRaw R, uint32_t buf) {
+        *reinterpret_cast<uint4 *>(&Bh[buf][swz(bn0, bkp)]) = R.h0;
+        *reinterpret_cast<uint4 *>(&Bh[buf][swz(bn1, bkp)]) = R.h1;
+        *reinterpret_cast<uint4 *>(&Bl[buf][swz(bn0, bkp)]) = R.l0;
+        *reinterpret_cast<uint4 *>(&Bl[buf][swz(bn1, bkp)]) = R.l1;
+    };
+    auto loadD = [=](uint32_t kb) -> float {
+        if (tid >= TM)
+            return 0.f;
+        const uint32_t row = rbase + min(m0 + tid, a.zrows - 1);
+        return half_bits_to_float(reinterpret_cast<const uint16_t *>(a.w.base + nblk * 208)[(size_t)row * nb + kb]);
+    };
+    auto decodeA = [&](const ARaw R, uint32_t q, uint32_t buf) {
+        decode_unit(R.ql0, R.qh0, R.sc0, q, ar0, acq, As[buf]);
+        decode_unit(R.ql1, R.qh1, R.sc1, q, ar1, acq, As[buf]);
+    };
     floatx16 acc[2][2], tmp[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -142,73 +221,99 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_q6(const GemmArg
 #pragma unroll
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.f, tmp[i][j][e] = 0.f;
-
-    for (uint32_t kb = 0; kb < a.w.nb; ++kb) {
-        for (uint32_t h = 0; h < 2; ++h) {
-            // A: 128 rows x 4 chunks of this half block, 2 (row, chunk) units per thread
+    auto mfma_half = [&](uint32_t buf, int ks0) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t unit = tid + u * WG_THREADS, r = unit >> 2, c = h * 4 + (unit & 3);
-                const uint32_t row = rbase + (m0 + r < a.zrows ? m0 + r : a.zrows - 1);
-                chunk_to_lds(a.w, row, kb, c, As + r * LDS_ROW);
-                if (h == 0 && (unit & 3) == 0) {
-                    const size_t nblk = (size_t)a.w.rows * a.w.nb;
-                    dsh[r] = half_bits_to_float(
-                        reinterpret_cast<const uint16_t *>(a.w.base + nblk * 208)[(size_t)row * a.w.nb + kb]);
-                }
+        for (int kk = 0; kk < 2; ++kk) {
+            const uint32_t kp = (ks0 + kk) * 2 + (lane >> 5);
+            half8 af[2], bfh[2], bfl[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = *reinterpret_cast<const half8 *>(&As[buf][swz(wm + i * 32 + (lane & 31), kp)]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                bfh[j] = *reinterpret_cast<const half8 *>(&Bh[buf][swz(wn + j * 32 + (lane & 31), kp)]);
+                bfl[j] = *reinterpret_cast<const half8 *>(&Bl[buf][swz(wn + j * 32 + (lane & 31), kp)]);
             }
-            // B: 128 tokens x 128 k of hi and lo (16 B per piece, 8 + 8 pieces per thread)
-            const uint32_t k0 = kb * 256 + h * 128;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t piece = tid + u * WG_THREADS, n = piece >> 4, kk = (piece & 15) * 8;
-                const uint32_t col = n0 + n < ntok ? n0 + n : ntok - 1;
-                const uint32_t src = tokl ? tokl[col] : col;
-                *reinterpret_cast<uint4 *>(Bh + n * LDS_ROW + kk) =
-                    *reinterpret_cast<const uint4 *>(xh + (size_t)src * K + k0 + kk);
-                *reinterpret_cast<uint4 *>(Bl + n * LDS_ROW + kk) =
-                    *reinterpret_cast<const uint4 *>(xl + (size_t)src * K + k0 + kk);
-            }
-            __syncthreads();
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int ks = 0; ks < GK / 16; ++ks) {
-                const uint32_t ko = ks * 16 + (lane >> 5) * 8;
-                half8 af[2], bh[2], bl[2];
+                for (int j = 0; j < 2; ++j)
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfh[j], tmp[i][j], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    af[i] = *reinterpret_cast<const half8 *>(As + (wm + i * 32 + (lane & 31)) * LDS_ROW + ko);
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], tmp[i][j], 0, 0, 0);
+        }
+    };
+    auto apply_d = [&](uint32_t db) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t r = wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                const float d = dsh[db][r];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    bh[j] = *reinterpret_cast<const half8 *>(Bh + (wn + j * 32 + (lane & 31)) * LDS_ROW + ko);
-                    bl[j] = *reinterpret_cast<const half8 *>(Bl + (wn + j * 32 + (lane & 31)) * LDS_ROW + ko);
+                    acc[i][j][e] += d * tmp[i][j][e];
+                    tmp[i][j][e] = 0.f;
                 }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bh[j], tmp[i][j], 0, 0, 0);
-                        tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bl[j], tmp[i][j], 0, 0, 0);
-                    }
             }
-            if (h == 1) {
-                // end of the super-block: acc += d[row] * partial
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const uint32_t r = wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                        const float dv = dsh[r];
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            acc[i][j][e] += dv * tmp[i][j][e];
-                            tmp[i][j][e] = 0.f;
-                        }
-                    }
-            }
-            __syncthreads();
-        }
+    };
+    const uint32_t nstage = nb * 4;
+    ARaw R = loadA(0);
+    BRaw RB = loadB(0);
+    float dreg = loadD(0);
+    decodeA(R, 0, 0);
+    storeB(RB, 0);
+    if (tid < TM)
+        dsh[0][tid] = dreg;
+    __syncthreads();
+    RB = loadB(1);
+    for (uint32_t kb = 0; kb < nb; ++kb) {
+        const uint32_t s0 = kb * 4;
+        const bool more = kb + 1 < nb;
+        // t = 0: MFMA s0 (buf 0); next = half 2kb q1 -> buf 1 (R holds half 2kb)
+        mfma_half(0, 0);
+        decodeA(R, 1, 1);
+        storeB(RB, 1);
+        mfma_half(0, 2);
+        __syncthreads();
+        if (s0 + 2 < nstage)
+            RB = loadB(s0 + 2);
+        R = loadA(2 * kb + 1);
+        if (more)
+            dreg = loadD(kb + 1);
+        // t = 1: MFMA s0+1 (buf 1); next = half 2kb+1 q0 -> buf 0
+        mfma_half(1, 0);
+        decodeA(R, 0, 0);
+        storeB(RB, 0);
+        mfma_half(1, 2);
+        __syncthreads();
+        if (s0 + 3 < nstage)
+            RB = loadB(s0 + 3);
+        // t = 2: MFMA s0+2 (buf 0); next = half 2kb+1 q1 -> buf 1
+        mfma_half(0, 0);
+        decodeA(R, 1, 1);
+        storeB(RB, 1);
+        mfma_half(0, 2);
+        __syncthreads();
+        if (s0 + 4 < nstage)
+            RB = loadB(s0 + 4);
+        if (more)
+            R = loadA(2 * kb + 2);
+        // t = 3: MFMA s0+3 (buf 1); next = half 2kb+2 q0 -> buf 0 (unused after the last block)
+        mfma_half(1, 0);
+        decodeA(R, 0, 0);
+        storeB(RB, 0);
+        if (tid < TM)
+            dsh[(kb + 1) & 1][tid] = dreg;
+        mfma_half(1, 2);
+        apply_d(kb & 1);
+        __syncthreads();
+        if (s0 + 5 < nstage)
+            RB = loadB(s0 + 5);
     }
-    // epilogue: lane holds rows 8*(e/4) + 4*(lane/32) + e%4 of column lane%32
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t n = n0 + wn + j * 32 + (lane & 31);
@@ -228,7 +333,6 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_q6(const GemmArg
             }
     }
 }
-
 // ------------------------------------------------------------------ short conv
 // The LFM2 short conv keeps only the previous two values of bx = B*X, so each
 // (t, ch) output depends on inputs t-2, t-1, t only: the T tokens of a chunk are
