@@ -28,6 +28,10 @@ import lfm_hip  # noqa: E402
 
 METRIC = "decode tok/s (bs=1, ctx 4096) + Q6_K matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
+# HBM bytes per k_gateup launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
+# WRITE_SIZE x 1.0, scales from a plain 512 MiB copy), profiles/k_gateup_traffic.md
+GATEUP_TRAFFIC_BYTES = 24656588
 SEED = 0x9E3779B97F4A7C15
 
 
@@ -50,6 +54,26 @@ def decode_bytes_per_token(hp, positions):
     n_attn = sum(1 for l in range(hp.n_layers) if hp.kv_heads[l])
     kv = np.mean([n_attn * 2 * 8 * 64 * 2 * (p + 1) for p in positions])
     return int(w), float(kv)
+
+
+def prefill_flops(hp, n):
+    """Algorithmic FLOPs of prefilling n tokens (2 per multiply-add): every
+    projection of every token (4 of 32 experts per MoE token), the router, the
+    causal attention scores and value sums, and the head for the last token."""
+    dim, macs = hp.dim, 0
+    for l in range(hp.n_layers):
+        kv = hp.kv_heads[l]
+        if kv:
+            macs += n * (2 * dim * dim + 2 * 64 * kv * dim)
+            macs += 2 * 64 * hp.heads * n * (n + 1) // 2  # q.k and p.v over positions 0..t
+        else:
+            macs += n * 4 * dim * dim
+        if l < hp.dense_lead:
+            macs += n * 3 * hp.n_ff * dim
+        else:
+            macs += n * (hp.n_expert * dim + hp.n_used * 3 * hp.expert_ff * dim)
+    macs += hp.vocab * dim
+    return 2 * macs
 
 
 def matvec_roofline(iters=200):
@@ -145,6 +169,7 @@ def main():
         logits = eng.forward(prompt, 0)  # one batched matrix-core prefill of the prompt
         first = int(np.argmax(logits))
     prefill_s = time.perf_counter() - t
+    pf_flops = prefill_flops(hp, n_prompt)
     log(f"[bench] {'state restore' if args.synthetic_state else 'prefill'} {n_prompt} tokens: "
         f"{prefill_s * 1e3:.1f} ms")
     snap = eng.snapshot_resident_cache(n_prompt)
@@ -173,7 +198,7 @@ def main():
         us, nbytes = eng.time_moe_gateup(reps=10)
         gbs = nbytes / (us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
                 "kernel": "k_gateup (MoE routed gate+up+SwiGLU, 4 experts x 2 x 1792x2048 Q6_K)",
                 "algorithmic_bytes": nbytes, "us_per_launch": round(us, 3)}
         log(f"[bench] k_gateup (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
@@ -184,6 +209,12 @@ def main():
             "hbm_gbs": round(algo / (ms_hbm * 1e-3) / 1e9, 1),
             "cache_resident_gbs": round(algo / (ms_mall * 1e-3) / 1e9, 1),
             "timing": "HIP events over 200 back-to-back launches (launch gaps included)"}
+        copy_bytes = 512 << 20
+        copy_us = lfm_hip.copy_time(copy_bytes, reps=10)
+        extra["hbm_copy"] = {"bytes_each_way": copy_bytes, "us": round(copy_us, 2),
+                             "gbs_read_plus_write": round(2 * copy_bytes / (copy_us * 1e-6) / 1e9, 1)}
+        log(f"[bench] plain copy {copy_bytes >> 20} MiB: {copy_us:.1f} us = "
+            f"{extra['hbm_copy']['gbs_read_plus_write']:.0f} GB/s read+write")
         log(f"[bench] q6k matvec cfg0: {ms_hbm * 1e3:.2f} us/launch = "
             f"{extra['q6k_matvec_cfg0']['hbm_gbs']:.0f} GB/s (HBM, 64 rotating copies), "
             f"{extra['q6k_matvec_cfg0']['cache_resident_gbs']:.0f} GB/s cache-resident")
@@ -206,8 +237,14 @@ def main():
         "roofline": roof, "cpu_baseline": cpu,
         "decode_hbm_gbs": round(decode_gbs, 1),
         "decode_bytes_per_token": int(wbytes + kvbytes),
-        "prefill_ms": None if args.synthetic_state else round(prefill_s * 1e3, 1),
-        "prefill_tok_s": None if args.synthetic_state else round(n_prompt / prefill_s, 1),
+        "prefill": None if args.synthetic_state else {
+            "tokens": n_prompt, "ms": round(prefill_s * 1e3, 1),
+            "tok_s": round(n_prompt / prefill_s, 1),
+            "algorithmic_tflops": round(pf_flops / prefill_s / 1e12, 1),
+            "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS,
+            "mfma_frac": round(pf_flops / prefill_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "note": "algorithmic FLOPs (projections, router, causal attention, last-token head); "
+                    "each GEMM product runs as two binary16 matrix-core passes (hi, lo)"},
         **extra,
     }
     print(json.dumps(line), flush=True)

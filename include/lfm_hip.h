@@ -174,6 +174,12 @@ int lfm_q6k_matvec(const void *packed_dev, uint64_t rows, uint64_t in_dim, const
 int lfm_q6k_matvec_time(const void *packed_dev, uint32_t ncopies, uint64_t rows, uint64_t in_dim,
                         const float *x_dev, float *y_dev, uint32_t iters, float *ms_per_launch);
 
+/* Measurement utility with no counterpart in the reference: mean time of a
+ * plain device copy of `bytes` (multiple of 16) over `reps` launches -- the
+ * achievable HBM rate that roofline figures are read against, and the known
+ * traffic that scales the memory counters of a profile. */
+int lfm_copy_time(uint64_t bytes, uint32_t reps, float *us_per_copy);
+
 /* Prefill GEMM on the matrix cores: y[t][r] = sum_k W[r][k] * x[t][k] for T
  * activation rows x (f32 [T][in_dim], device) into y (f32 [T][rows], device);
  * the multi-token q6k_prompt path of engine/src/ops.rs:350-373. */

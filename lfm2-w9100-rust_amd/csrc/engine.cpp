@@ -88,7 +88,7 @@ struct Kernels {
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
         swiglu_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
-        dequant;
+        dequant, copy;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
 };
@@ -186,7 +186,7 @@ static int get_kernels(Kernels **out)
                {&k->moe_down, "k_moe_down"},      {&k->head.f4, "k_head4"},
                {&k->head.f16, "k_head16"},        {&k->argmax, "k_argmax"},
                {&k->argmax_final, "k_argmax_final"}, {&k->advance, "k_advance"},
-               {&k->dequant, "k_q6_dequant"}};
+               {&k->dequant, "k_q6_dequant"},    {&k->copy, "k_copy"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -435,6 +435,49 @@ extern "C" int lfm_q6k_matvec(const void *packed, uint64_t rows, uint64_t in_dim
     RC(launch_matvec(K, a, (hipStream_t)stream));
     HIPCHK(hipStreamSynchronize((hipStream_t)stream));
     return LFM_OK;
+}
+
+extern "C" int lfm_copy_time(uint64_t bytes, uint32_t reps, float *us_per_copy)
+{
+    if (bytes < 16 || bytes % 16 || reps == 0 || !us_per_copy)
+        return fail(LFM_EINVAL, "copy: bytes must be a positive multiple of 16, reps positive");
+    Kernels *K;
+    RC(get_kernels(&K));
+    void *src = nullptr, *dst = nullptr;
+    HIPCHK(hipMalloc(&src, bytes));
+    if (hipMalloc(&dst, bytes) != hipSuccess) {
+        (void)hipFree(src);
+        return fail(LFM_EDEVICE, "copy: allocation of %llu bytes failed", (unsigned long long)bytes);
+    }
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = LFM_OK;
+    float ms = 0.f;
+    CopyArgs a{(const uint4 *)src, (uint4 *)dst, bytes / 16};
+    const uint32_t grid = 2048;
+    if (hipMemset(src, 1, bytes) != hipSuccess || hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        rc = fail(LFM_EDEVICE, "copy: setup failed");
+    if (rc == LFM_OK)
+        rc = launch(K->copy, dim3(grid), 0, s, a); // warm
+    if (rc == LFM_OK && hipEventRecord(e0, s) != hipSuccess)
+        rc = fail(LFM_EDEVICE, "copy: event record failed");
+    for (uint32_t i = 0; i < reps && rc == LFM_OK; ++i)
+        rc = launch(K->copy, dim3(grid), 0, s, a);
+    if (rc == LFM_OK && (hipEventRecord(e1, s) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                         hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+        rc = fail(LFM_EDEVICE, "copy: timing failed");
+    if (e0)
+        (void)hipEventDestroy(e0);
+    if (e1)
+        (void)hipEventDestroy(e1);
+    if (s)
+        (void)hipStreamDestroy(s);
+    (void)hipFree(src);
+    (void)hipFree(dst);
+    if (rc == LFM_OK)
+        *us_per_copy = ms * 1000.f / (float)reps;
+    return rc;
 }
 
 extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_t rows,

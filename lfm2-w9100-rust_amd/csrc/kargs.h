@@ -160,6 +160,12 @@ struct DequantArgs {
     uint32_t in_dim;
 };
 
+struct CopyArgs { // plain device copy (achievable-bandwidth reference)
+    const uint4 *src;
+    uint4 *dst;
+    uint64_t n16; // 16-byte units
+};
+
 // ---- prefill (multi-token) path ----------------------------------------------
 // RMSNorm (optional) + binary16 hi/lo split of T rows of K floats, with a per-row
 // power-of-two scale so that |x / scale| < 2^14 (hi/lo then hold ~22 bits).

@@ -1055,3 +1055,12 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_dequant(const Dequ
                 o[lane_pos(b, c, s, i)] = v[s * 8 + i];
     }
 }
+
+// Plain streaming copy dst = src in 16-byte units (grid-stride): the reference
+// for the achievable HBM rate and the scale of the memory-traffic counters.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_copy(const CopyArgs a)
+{
+    const uint64_t stride = (uint64_t)gridDim.x * WG_THREADS;
+    for (uint64_t i = (uint64_t)blockIdx.x * WG_THREADS + threadIdx.x; i < a.n16; i += stride)
+        a.dst[i] = a.src[i];
+}

@@ -119,6 +119,7 @@ def lib():
         "lfm_snapshot_logits": (i32, [P, pf32, sz]),
         "lfm_dispatch_count": (u64, [P]), "lfm_device_name": (i32, [P, C.c_char_p, sz]),
         "lfm_engine_set_prefill_mode": (i32, [P, i32]),
+        "lfm_copy_time": (i32, [u64, u32, pf32]),
         "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
@@ -327,6 +328,13 @@ def q6k_matvec_time(weights: DeviceBuffer, ncopies: int, rows: int, in_dim: int,
     _check(lib().lfm_q6k_matvec_time(weights.ptr, ncopies, rows, in_dim, x.ptr, y.ptr, iters,
                                      C.byref(ms)))
     return ms.value
+
+
+def copy_time(nbytes: int, reps: int = 10) -> float:
+    """Mean microseconds of a plain device copy of nbytes (read + write)."""
+    us = C.c_float()
+    _check(lib().lfm_copy_time(nbytes, reps, C.byref(us)))
+    return us.value
 
 
 def argmax(v: np.ndarray):
