@@ -1234,7 +1234,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
     RC(launch(e->K->rope_kv_prefill, dim3(T), 0, e->stream, r));
     AttnPrefillArgs at{e->pf.bcx, e->kc[l], e->vc[l], e->pf.y, 1.0f / sqrtf((float)hp.head_dim), T,
                        start, hp.heads, kv, e->ctx};
-    RC(launch(e->K->attn_prefill, dim3((T + 63) / 64, kv), 0, e->stream, at));
+    RC(launch(e->K->attn_prefill, dim3((T + 31) / 32, kv), 0, e->stream, at));
     RC(pf_split(e, e->pf.y, nullptr, T, dim));
     RC(pf_gemm(e, q6(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
     e->dispatches += 2;

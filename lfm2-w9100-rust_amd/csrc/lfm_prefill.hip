@@ -409,72 +409,149 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_rope_kv_prefill(const
     }
 }
 
-// Causal attention (lfm.rs:395-437): a workgroup takes 64 queries of one kv head;
-// thread = (query, q head of the group).  Keys/values stream through LDS in
-// blocks of 64 positions; online softmax in fp32.
-#define PQ 64
-#define PK 64
+// Causal attention (lfm.rs:395-437) on the matrix cores.  A workgroup takes 32
+// queries of one kv head; wave w is q head kh*G + w.  Keys stream in blocks of
+// 32 through double-buffered LDS (K rows, V transposed), shared by the G heads.
+// Per block a wave computes S^T = K Q^T (keys x queries) with
+// v_mfma_f32_32x32x16_f16 on q split into binary16 hi + lo (K is binary16 in the
+// cache), so each lane holds one query's 16 scores: the online softmax (running
+// max m, sum l, fp32) needs only in-lane work and one swap across lane halves.
+// The lane's probabilities, split hi + lo, are exactly the B operand of
+// v_mfma_f32_32x32x8_f16 for O^T += V^T P^T.  out = O / l.
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef float floatx16a __attribute__((ext_vector_type(16)));
+#define FA_Q 32    // queries per workgroup
+#define FA_K 32    // keys per block
+#define FA_KROW 72 // halves per K row in LDS (64 + 8)
+#define FA_VROW 36 // halves per transposed-V row in LDS (32 + 4)
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const AttnPrefillArgs a)
 {
-    const uint32_t kh = blockIdx.y, q0 = blockIdx.x * PQ;
-    if (q0 >= a.T)
+    const uint32_t kh = blockIdx.y, t0 = blockIdx.x * FA_Q;
+    if (t0 >= a.T)
         return;
-    const uint32_t G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64;
-    const uint32_t tid = threadIdx.x, qi = tid & (PQ - 1), g = tid >> 6;
-    __shared__ __attribute__((aligned(16))) float Ks[PK][64];
-    __shared__ __attribute__((aligned(16))) float Vs[PK][64];
-    const uint32_t t = q0 + qi;
-    const bool live = t < a.T && g < G;
-    const uint32_t pos = a.start + (t < a.T ? t : a.T - 1);
-    float q[64], acc[64];
-    const float *qrow = a.qkv + (size_t)(t < a.T ? t : a.T - 1) * (dim + 2 * hdkv) + (kh * G + (g < G ? g : 0)) * 64;
+    const uint32_t G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64, stride = dim + 2 * hdkv;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_K * FA_KROW];
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[2][64 * FA_VROW];
+    const bool active = wave < G;
+    const uint32_t h = kh * G + (active ? wave : 0);
+    // q fragments (B operand, 16 keys-dims steps): lane holds query lq, dims ks*16 + 8*lh + i
+    const uint32_t tq = t0 + lq;
+    half8 qh[4], ql[4];
+    {
+        const float *qrow = a.qkv + (size_t)(tq < a.T ? tq : a.T - 1) * stride + h * 64;
 #pragma unroll
-    for (int d = 0; d < 64; ++d) {
-        q[d] = qrow[d] * a.scale;
-        acc[d] = 0.f;
-    }
-    float m = -INFINITY, l = 0.f;
-    const uint32_t last_pos = a.start + min(q0 + PQ, a.T) - 1; // highest position in this block
-    for (uint32_t k0 = 0; k0 <= last_pos; k0 += PK) {
-        __syncthreads();
-        for (uint32_t u = tid; u < PK * 64; u += WG_THREADS) {
-            const uint32_t kk = u >> 6, d = u & 63;
-            const uint32_t kp = k0 + kk <= last_pos ? k0 + kk : last_pos;
-            const size_t off = ((size_t)kh * a.ctx + kp) * 64 + d;
-            Ks[kk][d] = (float)__builtin_bit_cast(_Float16, a.kcache[off]);
-            Vs[kk][d] = (float)__builtin_bit_cast(_Float16, a.vcache[off]);
-        }
-        __syncthreads();
-        if (!live)
-            continue;
-        const uint32_t nk = min((uint32_t)PK, pos + 1 > k0 ? pos + 1 - k0 : 0u);
-        for (uint32_t kk = 0; kk < nk; ++kk) {
-            float s = 0.f;
+        for (int ks = 0; ks < 4; ++ks) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh);
+            const float4 v1 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-            for (int d = 0; d < 64; ++d)
-                s += q[d] * Ks[kk][d];
-            if (s > m) {
-                const float r = expf(m - s);
-                l *= r;
-#pragma unroll
-                for (int d = 0; d < 64; ++d)
-                    acc[d] *= r;
-                m = s;
+            for (int i = 0; i < 8; ++i) {
+                const float x = v[i] * a.scale;
+                qh[ks][i] = (_Float16)x;
+                ql[ks][i] = (_Float16)(x - (float)qh[ks][i]);
             }
-            const float p = expf(s - m);
-            l += p;
-#pragma unroll
-            for (int d = 0; d < 64; ++d)
-                acc[d] += p * Vs[kk][d];
         }
     }
-    if (!live)
-        return;
-    float *o = a.out + (size_t)t * dim + (kh * G + g) * 64;
-    const float rl = 1.0f / l;
+    const uint32_t qpos = a.start + tq; // causal limit of this lane's query
+    const uint32_t tmax = min(t0 + FA_Q, a.T) - 1;
+    const uint32_t nblk = (a.start + tmax) / FA_K + 1;
+    // staging: thread -> key row tid / 8, dims (tid % 8) * 8 .. +7
+    const uint32_t sr = tid >> 3, sp = (tid & 7) * 8;
+    const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
+    const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
+    auto load_kv = [&](uint32_t blk, uint4 &kr, uint4 &vr) {
+        const uint32_t pos = min(blk * FA_K + sr, a.ctx - 1);
+        kr = *reinterpret_cast<const uint4 *>(kg + (size_t)pos * 64 + sp);
+        vr = *reinterpret_cast<const uint4 *>(vg + (size_t)pos * 64 + sp);
+    };
+    auto store_kv = [&](uint32_t buf, uint4 kr, uint4 vr) {
+        *reinterpret_cast<uint4 *>(&Ks[buf][sr * FA_KROW + sp]) = kr;
+        const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vr);
 #pragma unroll
-    for (int d = 0; d < 64; ++d)
-        o[d] = acc[d] * rl;
+        for (int i = 0; i < 8; ++i)
+            reinterpret_cast<uint16_t *>(Vt[buf])[(sp + i) * FA_VROW + sr] = v16[i];
+    };
+    floatx16a o0, o1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        o0[e] = 0.f, o1[e] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    uint4 kr, vr;
+    load_kv(0, kr, vr);
+    store_kv(0, kr, vr);
+    if (nblk > 1)
+        load_kv(1, kr, vr);
+    __syncthreads();
+    for (uint32_t blk = 0; blk < nblk; ++blk) {
+        const uint32_t buf = blk & 1;
+        if (active) {
+            // S^T[key][query] for the block's 32 keys
+            floatx16a sacc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                sacc[e] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const half8 kf = *reinterpret_cast<const half8 *>(&Ks[buf][lq * FA_KROW + ks * 16 + 8 * lh]);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], sacc, 0, 0, 0);
+            }
+            // lane's items: keys 8*(e/4) + 4*lh + e%4 of the block, query lq
+            float bm = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t kpos = blk * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
+                if (kpos > qpos)
+                    sacc[e] = -INFINITY;
+                bm = fmaxf(bm, sacc[e]);
+            }
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float mn = fmaxf(m, bm);
+            const float r = m > -INFINITY ? expf(m - mn) : 0.f;
+            float ps = 0.f;
+            half4v phi[4], plo[4];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float p = sacc[e] > -INFINITY ? expf(sacc[e] - mn) : 0.f;
+                ps += p;
+                const _Float16 hi = (_Float16)p;
+                phi[e / 4][e % 4] = hi;
+                plo[e / 4][e % 4] = (_Float16)(p - (float)hi);
+            }
+            ps += __shfl_xor(ps, 32, 64);
+            l = l * r + ps;
+            m = mn;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                o0[e] *= r, o1[e] *= r;
+            // O^T[dim][query] += V^T[dim][key] P^T[key][query], keys in groups of 8
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const half4v v0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 8 * g + 4 * lh]);
+                const half4v v1 = *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 8 * g + 4 * lh]);
+                o0 = __builtin_amdgcn_mfma_f32_32x32x8f16(v0, phi[g], o0, 0, 0, 0);
+                o0 = __builtin_amdgcn_mfma_f32_32x32x8f16(v0, plo[g], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x8f16(v1, phi[g], o1, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x8f16(v1, plo[g], o1, 0, 0, 0);
+            }
+        }
+        if (blk + 1 < nblk)
+            store_kv(buf ^ 1, kr, vr);
+        if (blk + 2 < nblk)
+            load_kv(blk + 2, kr, vr);
+        __syncthreads();
+    }
+    if (!active || tq >= a.T)
+        return;
+    const float rl = 1.0f / l;
+    float *orow = a.out + (size_t)tq * dim + h * 64;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
+        orow[d] = o0[e] * rl;
+        orow[32 + d] = o1[e] * rl;
+    }
 }
 
 // ------------------------------------------------------------------ FFN pieces
