@@ -73,8 +73,13 @@ extern "C" int lfm_device_count(int *count)
 // kernel variant) and target rows (work items) per wave, which set the grid.
 struct Shape {
     hipFunction_t f4 = nullptr, f16 = nullptr;
+    hipFunction_t f4e = nullptr, f16e = nullptr; // embedding-input variants (first layer)
     uint32_t nw = 4, rpw = 1;
     hipFunction_t fn() const { return nw == 16 ? f16 : f4; }
+    hipFunction_t fn(bool embed) const
+    {
+        return embed && f4e ? (nw == 16 ? f16e : f4e) : fn();
+    }
     uint32_t threads() const { return 64 * nw; }
     uint32_t grid(uint32_t items) const
     {
@@ -88,7 +93,7 @@ struct Kernels {
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
         swiglu_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
-        dequant, copy;
+        dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
 };
@@ -181,12 +186,15 @@ static int get_kernels(Kernels **out)
                {&k->matvec_ks, "k_q6_matvec_ks"}, {&k->conv.f4, "k_conv_inproj4"},
                {&k->conv.f16, "k_conv_inproj16"}, {&k->qkv.f4, "k_qkv4"},
                {&k->qkv.f16, "k_qkv16"},          {&k->attn, "k_attn"},
+               {&k->conv.f4e, "k_conv_inproj4e"}, {&k->conv.f16e, "k_conv_inproj16e"},
+               {&k->qkv.f4e, "k_qkv4e"},          {&k->qkv.f16e, "k_qkv16e"},
                {&k->attn_merge, "k_attn_merge"},  {&k->router, "k_router"},
                {&k->gateup.f4, "k_gateup4"},      {&k->gateup.f16, "k_gateup16"},
                {&k->moe_down, "k_moe_down"},      {&k->head.f4, "k_head4"},
                {&k->head.f16, "k_head16"},        {&k->argmax, "k_argmax"},
                {&k->argmax_final, "k_argmax_final"}, {&k->advance, "k_advance"},
-               {&k->dequant, "k_q6_dequant"},    {&k->copy, "k_copy"}};
+               {&k->dequant, "k_q6_dequant"},    {&k->copy, "k_copy"},
+               {&k->matvec_route, "k_q6_matvec_route"}, {&k->gateup_f, "k_gateup4f"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -254,6 +262,13 @@ template <typename A>
 static int launch_shape(const Shape &sh, uint32_t items, hipStream_t s, const A &args)
 {
     return launch_t(sh.fn(), dim3(sh.grid(items)), sh.threads(), 0, s, args);
+}
+
+// Mixer kernels: the first layer of a step reads the token's embedding row.
+template <typename A>
+static int launch_mixer(const Shape &sh, uint32_t items, hipStream_t s, const A &args)
+{
+    return launch_t(sh.fn(args.src.embed != 0), dim3(sh.grid(items)), sh.threads(), 0, s, args);
 }
 
 // ------------------------------------------------------------------ Q6_K layout
@@ -621,6 +636,7 @@ struct lfm_engine {
     uint32_t *ids = nullptr, *out_tokens = nullptr, *sel = nullptr;
     float *x = nullptr, *y = nullptr, *qkv = nullptr, *sw = nullptr, *rlogits = nullptr,
           *logits = nullptr, *hpart = nullptr, *apart = nullptr;
+    float *rpart = nullptr; // fused router partial sums [ROUTE_EXPERTS + 1][ROUTE_PARTS]
     std::vector<uint16_t *> kc, vc;
     std::vector<float *> conv;
     uint32_t head_grid = 1, nchunk = 1;
@@ -801,7 +817,35 @@ static XSrc xsrc(const float *x, const float *norm, float eps)
     return s;
 }
 
-static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
+// The router of MoE layer l is fused into the output projection before it and
+// the gate/up kernel (k_q6_matvec_route + k_gateup4f) at the model's shape:
+// 32 experts, width ROUTE_ROWS * ROUTE_PARTS, 4-wave gate/up workgroups.
+static bool fused_router(const lfm_engine *e, uint32_t l)
+{
+    const lfm_hparams &hp = e->hp;
+    return l >= hp.dense_lead && hp.n_expert == ROUTE_EXPERTS &&
+           hp.dim == ROUTE_ROWS * ROUTE_PARTS && e->K->gateup.nw == 4;
+}
+
+// Output projection of layer l's mixer (y += W x); with the fused router it
+// also leaves the router's partial sums.  `fuse` is set when the layer's FFN
+// is enqueued right after (the decode step); the single-layer entry points
+// run each half on its own and keep the separate router kernel.
+static int launch_out_proj(lfm_engine *e, uint32_t l, MatvecArgs &m, bool fuse)
+{
+    if (!fuse || !fused_router(e, l))
+        return launch_matvec(e->K, m, e->stream);
+    if (m.w.rows != ROUTE_ROWS * ROUTE_PARTS || m.w.nb > 8 || m.mode != 1)
+        return fail(LFM_EINTERNAL, "fused router: unexpected output projection shape");
+    MatvecRouteArgs ra;
+    ra.m = m;
+    ra.rw = f32(e, "blk.%u.ffn_gate_inp.weight", l);
+    ra.rnorm = f32(e, "blk.%u.ffn_norm.weight", l);
+    ra.rpart = e->rpart;
+    return launch_t(e->K->matvec_route, dim3(ROUTE_PARTS), 64 * ROUTE_ROWS, 0, e->stream, ra);
+}
+
+static int enq_mixer(lfm_engine *e, uint32_t l, bool embed, bool fuse)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
@@ -827,9 +871,9 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
         a.y = e->y;
         a.dim = dim;
         a.st = e->st;
-        RC(launch_shape(e->K->conv, dim, e->stream, a));
+        RC(launch_mixer(e->K->conv, dim, e->stream, a));
         m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
-        RC(launch_matvec(e->K, m, e->stream));
+        RC(launch_out_proj(e, l, m, fuse));
         e->dispatches += 2;
         return LFM_OK;
     }
@@ -843,7 +887,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     q.dim = dim;
     q.hdkv = hdkv;
     q.st = e->st;
-    RC(launch_shape(e->K->qkv, dim + 2 * hdkv, e->stream, q));
+    RC(launch_mixer(e->K->qkv, dim + 2 * hdkv, e->stream, q));
     AttnArgs at;
     at.qkv = e->qkv;
     at.q_norm = f32(e, "blk.%u.attn_q_norm.weight", l);
@@ -863,7 +907,7 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed)
     AttnMergeArgs mg{e->apart, e->y, hp.heads, kv, e->nchunk, e->st};
     RC(launch(e->K->attn_merge, dim3(kv, hp.heads / kv), 0, e->stream, mg));
     m.w = q6(e, "blk.%u.attn_output.weight", l);
-    RC(launch_matvec(e->K, m, e->stream));
+    RC(launch_out_proj(e, l, m, fuse));
     e->dispatches += 4;
     return LFM_OK;
 }
@@ -887,7 +931,7 @@ static GateUpArgs moe_gateup_args(lfm_engine *e, uint32_t l)
     return g;
 }
 
-static int enq_ffn(lfm_engine *e, uint32_t l)
+static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim;
@@ -914,17 +958,28 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
         e->dispatches += 2;
         return LFM_OK;
     }
-    RouterArgs r;
-    r.src = src;
-    r.w = f32(e, "blk.%u.ffn_gate_inp.weight", l);
-    r.logits = e->rlogits;
-    r.dim = dim;
-    r.n_expert = hp.n_expert;
-    r.st = e->st;
-    RC(launch(e->K->router, dim3(hp.n_expert), 0, e->stream, r));
+    const bool fused = fuse && fused_router(e, l);
+    if (!fused) {
+        RouterArgs r;
+        r.src = src;
+        r.w = f32(e, "blk.%u.ffn_gate_inp.weight", l);
+        r.logits = e->rlogits;
+        r.dim = dim;
+        r.n_expert = hp.n_expert;
+        r.st = e->st;
+        RC(launch(e->K->router, dim3(hp.n_expert), 0, e->stream, r));
+    }
     g = moe_gateup_args(e, l);
+    if (fused) {
+        g.route.logits = nullptr;
+        g.route.rpart = e->rpart;
+        const Shape &sh = e->K->gateup;
+        RC(launch_t(e->K->gateup_f, dim3(sh.grid(hp.n_used * hp.expert_ff)), sh.threads(), 0,
+                    e->stream, g));
+    } else {
+        RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));
+    }
     const Route route = g.route;
-    RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));
     MoeDownArgs d;
     d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
     d.sw = e->sw;
@@ -937,7 +992,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l)
     if (!d.route.sel_out)
         return fail(LFM_EINTERNAL, "down projection launched without the routing buffer");
     RC(launch_t(e->K->moe_down, dim3((dim + 7) / 8), 1024, 0, e->stream, d));
-    e->dispatches += 3;
+    e->dispatches += fused ? 2 : 3;
     return LFM_OK;
 }
 
@@ -968,8 +1023,8 @@ static int enq_advance(lfm_engine *e)
 static int enq_layers(lfm_engine *e)
 {
     for (uint32_t l = 0; l < e->hp.n_layers; ++l) {
-        RC(enq_mixer(e, l, l == 0));
-        RC(enq_ffn(e, l));
+        RC(enq_mixer(e, l, l == 0, true));
+        RC(enq_ffn(e, l, true));
     }
     return LFM_OK;
 }
@@ -1065,6 +1120,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMalloc(&e->qkv, (dim + 2 * max_hdkv) * 4));
     HIPCHK(hipMalloc(&e->sw, swn * 4));
     HIPCHK(hipMalloc(&e->rlogits, 64 * 4));
+    HIPCHK(hipMalloc(&e->rpart, (ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4));
     HIPCHK(hipMalloc(&e->logits, (size_t)hp.vocab * 4));
     HIPCHK(hipMemset(e->logits, 0, (size_t)hp.vocab * 4));
     HIPCHK(hipMalloc(&e->hpart, e->head_grid * 2 * 4));
@@ -1127,7 +1183,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (auto &kv : e->tensors)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
-                    e->rlogits, e->logits, e->hpart, e->apart, e->rope,
+                    e->rlogits, e->rpart, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.u, e->pf.d, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot};
@@ -1612,7 +1668,7 @@ static int run_layer_part(lfm_engine *e, uint32_t layer, float *x, uint32_t pos,
         return fail(LFM_ERANGE, "position %u >= ctx %u", pos, e->ctx);
     HIPCHK(hipMemcpyAsync(e->x, x, (size_t)e->hp.dim * 4, hipMemcpyHostToDevice, e->stream));
     RC(set_state(e, 0, pos, 0, 0xFFFFFFFFu));
-    RC(mixer ? enq_mixer(e, layer, false) : enq_ffn(e, layer));
+    RC(mixer ? enq_mixer(e, layer, false, false) : enq_ffn(e, layer, false));
     HIPCHK(hipMemcpyAsync(x, e->x, (size_t)e->hp.dim * 4, hipMemcpyDeviceToHost, e->stream));
     HIPCHK(hipStreamSynchronize(e->stream));
     return LFM_OK;

@@ -101,10 +101,26 @@ struct RouterArgs {
 };
 
 struct Route {
-    const float *logits; // nullptr = dense layer
+    const float *logits; // nullptr = dense layer (or the fused router below)
     const float *bias;
     uint32_t n_expert, n_used;
     uint32_t *sel_out;   // written by one wave: ids[8] then weights[8] (float bits)
+    const float *rpart;  // fused router: [ROUTE_EXPERTS + 1][ROUTE_PARTS] partial sums
+};
+
+// Fused router (the model's 32 experts at width 2048): the output projection
+// before the FFN runs ROUTE_PARTS workgroups of ROUTE_ROWS rows; each leaves
+// the partial dots sum_r R[e][r] * (x_new[r] * w_norm[r]) and sum_r x_new[r]^2
+// of its rows, which the gate/up kernel adds up.
+#define ROUTE_EXPERTS 32
+#define ROUTE_ROWS 16
+#define ROUTE_PARTS 128
+
+struct MatvecRouteArgs { // y += W x (mode 1) and the router partial sums of the new y
+    MatvecArgs m;
+    const float *rw;     // router weights [ROUTE_EXPERTS][rows] f32
+    const float *rnorm;  // RMSNorm weight of the FFN input [rows]
+    float *rpart;        // [ROUTE_EXPERTS + 1][ROUTE_PARTS]
 };
 
 struct GateUpArgs {      // sw = silu(Wg h) * (Wu h), dense or routed

@@ -13,6 +13,7 @@
 //   decode attention              engine/src/lfm.rs:395-437, kernels.rs:672-763
 //   short conv                    engine/src/lfm.rs:450-533, kernels/resident.rs:33-56
 //   router / top-k                engine/src/lfm.rs:599-637, kernels/resident.rs:58-99
+//                                 (fused: partial sums in the output projection, total in gate/up)
 //   SwiGLU                        engine/src/lfm.rs:578-582, kernels.rs:543-550
 //   expert combine                engine/src/lfm.rs:645-668, kernels/resident.rs:101-117
 //   embedding                     engine/src/lfm.rs:310-320, kernels/resident.rs:7-18
@@ -90,6 +91,19 @@ __device__ __forceinline__ uint32_t load_halt(const DevState *st)
     return __hip_atomic_load(&st->halt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The wave's index in its workgroup as a wave-uniform value, so that row
+// indices derived from it (and the tensor fields selected by them) stay in
+// scalar registers.
+__device__ __forceinline__ uint32_t wave_index()
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+// Compiler-only fence placed between a kernel's issued loads and its halt
+// check: without it the compiler sinks the (unconditional) loads below the
+// early return, so they would wait for the flag.
+__device__ __forceinline__ void keep_issued() { asm volatile("" ::: "memory"); }
+
 // ------------------------------------------------------------ staged input
 // The input vector of a decode matvec (n <= 2048 values) is staged once per
 // workgroup in LDS: xs[k] = x[k] * w[k] with w the RMSNorm weight, or x[k].
@@ -103,31 +117,36 @@ struct XRaw {
     float4 x0, x1, w0, w1;
 };
 
-// Issues the loads of this thread's 8 values (positions 8t .. 8t+7).
+// Issues the loads of this thread's 8 values (positions 8t .. 8t+7).  The
+// decode kernels issue every load without a branch around it (indices clamped
+// into range, unused results ignored): a load under a branch leaves the
+// compiler's wait counts unknown at the join, after which waiting for one
+// early load also waits for every load issued after it.  Threads past n and
+// the embedding case (x_out is then the residual buffer) load stand-ins.
 __device__ __forceinline__ void x_issue(const XSrc &s, uint32_t n, XRaw &r)
 {
-    const uint32_t k = threadIdx.x * 8;
-    if (s.embed || k >= n)
-        return;
-    r.x0 = *reinterpret_cast<const float4 *>(s.x + k);
-    r.x1 = *reinterpret_cast<const float4 *>(s.x + k + 4);
-    if (s.norm_w) {
-        r.w0 = *reinterpret_cast<const float4 *>(s.norm_w + k);
-        r.w1 = *reinterpret_cast<const float4 *>(s.norm_w + k + 4);
-    }
+    const uint32_t k = min(threadIdx.x * 8, n - 8);
+    const float *xp = s.embed ? s.x_out : s.x;
+    const float *wp = s.norm_w ? s.norm_w : xp;
+    r.x0 = *reinterpret_cast<const float4 *>(xp + k);
+    r.x1 = *reinterpret_cast<const float4 *>(xp + k + 4);
+    r.w0 = *reinterpret_cast<const float4 *>(wp + k);
+    r.w1 = *reinterpret_cast<const float4 *>(wp + k + 4);
 }
 
 // Writes the staged vector, synchronizes the workgroup (every thread must
 // call it) and returns inv (1 without a norm).  For the first kernel of a step
 // the vector is the dequantized embedding row DevState::tok (lfm.rs:310-320),
 // built by wave 0; workgroup 0 also stores it as the residual x_out.
-template <int NW>
+// EMB = false compiles the embedding case out (its loads sit under a branch,
+// see x_issue); the kernels of a step's first layer have EMB = true variants.
+template <int NW, bool EMB = false>
 __device__ __forceinline__ float x_stage(const XSrc &s, uint32_t n, const DevState *st,
                                          const XRaw &r, float *xs, float *red)
 {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float ss = 0.f;
-    if (s.embed) {
+    if (EMB && s.embed) {
         const uint32_t b = lane >> 3, c = lane & 7;
         if (wave == 0 && b < n / 256) {
             float v[32];
@@ -207,6 +226,8 @@ __device__ __forceinline__ void wave_sum3(float &a, float &b, float &c)
 // One wave's work items are it = first + k*W (k = 0, 1, ...) below `total`;
 // each item is NR Q6_K rows.  Kernels load G items, reduce them, load the
 // next G; the first group's loads are issued before the input is staged.
+// Items past `total` load the last item again (never used), so no load sits
+// under a branch.
 template <int NR> struct Item {
     Lane l[NR];
 };
@@ -216,11 +237,16 @@ __device__ __forceinline__ void fill_items(Item<NR> (&buf)[G], uint32_t it0, uin
                                            uint32_t total, LoadF load)
 {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint32_t it = it0 + g * W;
-        if (it < total)
-            load(it, buf[g]);
-    }
+    for (int g = 0; g < G; ++g)
+        load(min(it0 + g * W, total - 1), buf[g]);
+}
+
+// A lane's share of a row with the block index clamped into the row: lanes
+// past the row's blocks (b >= nb) re-read its last block, which the dot
+// products then leave out.
+__device__ __forceinline__ Lane load_lane_c(const Q6T &t, uint32_t row, uint32_t b, uint32_t c)
+{
+    return load_lane(t, row, min(b, t.nb - 1), c);
 }
 // Wave sum of N per-lane values at once (results in every lane).
 template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
@@ -228,6 +254,17 @@ template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 #pragma unroll
     for (int i = 0; i < N; ++i)
         v[i] = wave_sum(v[i]);
+}
+
+// Old values y[it0 + g*W] of the rows a wave updates in place (lanes with
+// `on`; others get 0), issued together with the rows' weights.
+template <int G>
+__device__ __forceinline__ void residual_issue(float (&yold)[G], const float *y, uint32_t it0,
+                                               uint32_t W, uint32_t rows)
+{
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        yold[g] = y[min(it0 + g * W, rows - 1)];
 }
 
 // ------------------------------------------------------------------ kernels
@@ -239,26 +276,29 @@ __device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave, rows = a.w.rows;
-    auto load = [&](uint32_t r, Item<1> &it) {
-        if (active)
-            it.l[0] = load_lane(a.w, r, b, c);
-    };
+    auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c(a.w, r, b, c); };
     XRaw raw;
     x_issue(a.src, a.in_dim, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    // mode 1: the rows' old values are loaded with the weights, not after the dot
+    float yold[G];
+    residual_issue<G>(yold, a.y, first, W, rows);
+    keep_issued();
     if (halted) // checked after the loads are issued (the flag's latency overlaps them)
         return;
     const float inv = x_stage<NW>(a.src, a.in_dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < rows; it0 += G * W) {
-        if (it0 != first)
+        if (it0 != first) {
             fill_items(buf, it0, W, rows, load);
+            residual_issue<G>(yold, a.y, it0, W, rows);
+        }
         float p[G];
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -269,18 +309,74 @@ __device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
             for (int g = 0; g < G; ++g) {
                 const uint32_t r = it0 + g * W;
                 if (r < rows)
-                    a.y[r] = a.mode ? a.y[r] + inv * p[g] : inv * p[g];
+                    a.y[r] = a.mode ? yold[g] + inv * p[g] : inv * p[g];
             }
     }
 }
 
 extern "C" __global__ __launch_bounds__(256) void k_q6_matvec4(const MatvecArgs a)
 {
-    q6_matvec_body<4, 2>(a);
+    q6_matvec_body<4, 1>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArgs a)
 {
-    q6_matvec_body<16, 2>(a);
+    q6_matvec_body<16, 1>(a);
+}
+
+// Output projection y += W x (mode 1) with the router's first stage
+// (lfm.rs:599-607): one wave per row, ROUTE_ROWS rows per workgroup; the
+// workgroup's new residual rows give the partial dots
+//   sum_r R[e][r] * (y[r] * w_norm[r])  (e < 32, lane e)   and   sum_r y[r]^2
+// stored column-major in rpart; k_gateup4f adds the ROUTE_PARTS partials and
+// applies the RMSNorm scale.  The grid is exactly rows / ROUTE_ROWS.
+extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_route(const MatvecRouteArgs ra)
+{
+    const MatvecArgs &a = ra.m;
+    const uint32_t halted = load_halt(a.st);
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[16];
+    __shared__ float yn[ROUTE_ROWS];
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
+    const uint32_t b = lane >> 3, c = lane & 7;
+    const bool active = b < a.w.nb;
+    const uint32_t r0 = blockIdx.x * ROUTE_ROWS, r = r0 + wave;
+    XRaw raw;
+    x_issue(a.src, a.in_dim, raw);
+    const Lane w = load_lane_c(a.w, r, b, c);
+    const float yold = a.y[r];
+    // router weights of the workgroup's rows for expert lane % 32 (used by wave 0)
+    const float4 *rwp =
+        reinterpret_cast<const float4 *>(ra.rw + (size_t)(lane & (ROUTE_EXPERTS - 1)) * a.w.rows + r0);
+    const float4 q0 = rwp[0], q1 = rwp[1], q2 = rwp[2], q3 = rwp[3];
+    keep_issued();
+    if (halted)
+        return;
+    const float inv = x_stage<16>(a.src, a.in_dim, a.st, raw, xs, red);
+    LaneX X;
+    lanex_lds(X, xs, b, c, active);
+    const float p = wave_sum(active ? lane_dot(w, X) : 0.f);
+    const float v = yold + inv * p;
+    if (lane == 0) {
+        a.y[r] = v;
+        yn[wave] = v;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float rv[ROUTE_ROWS] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
+                                      q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+        const float *nw = ra.rnorm + r0;
+        float acc = 0.f, ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < ROUTE_ROWS; ++i) {
+            const float xv = yn[i];
+            acc += rv[i] * (xv * nw[i]);
+            ss += xv * xv;
+        }
+        if (lane < ROUTE_EXPERTS)
+            ra.rpart[lane * ROUTE_PARTS + blockIdx.x] = acc;
+        else if (lane == ROUTE_EXPERTS)
+            ra.rpart[ROUTE_EXPERTS * ROUTE_PARTS + blockIdx.x] = ss;
+    }
 }
 // Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
 // `ksplit` waves share a row (nbw blocks each); x staged in LDS; partials
@@ -304,6 +400,8 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const Ma
     Lane cur;
     if (active && g < ngroups && g * rpi + slot < rows)
         cur = load_lane(a.w, g * rpi + slot, b, c);
+    const bool owner = kp == 0 && lane == 0 && a.mode;
+    float yold = (owner && g < ngroups && g * rpi + slot < rows) ? a.y[g * rpi + slot] : 0.f;
     for (uint32_t i = tid * 4; i < a.in_dim; i += WG_THREADS * 4)
         *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.src.x + i);
     __syncthreads();
@@ -318,6 +416,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const Ma
         Lane nxt;
         if (active && gn < ngroups && rown < rows)
             nxt = load_lane(a.w, rown, b, c);
+        const float ynxt = (owner && gn < ngroups && rown < rows) ? a.y[rown] : 0.f;
         float p = (active && row < rows) ? lane_dot(cur, X) : 0.f;
         p = wave_sum(p);
         if (lane == 0)
@@ -327,10 +426,11 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const Ma
             float s = 0.f;
             for (uint32_t k = 0; k < ks; ++k)
                 s += red[slot * ks + k];
-            a.y[row] = a.mode ? a.y[row] + s : s;
+            a.y[row] = a.mode ? yold + s : s;
         }
         __syncthreads();
         cur = nxt;
+        yold = ynxt;
     }
 }
 
@@ -338,51 +438,69 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const Ma
 // computes in_proj rows B[ch], C[ch], X[ch] of the normed input, then
 //   bx = B*X; co = ((0 + s0*w0) + s1*w1) + bx*w2; y = C*co; state = (s1, bx)
 // in the reference's operation order with no contraction.
-__device__ __forceinline__ void conv_step(float B, float C, float Xv, const float *w3, float *s2,
+// A channel's conv weights and state, loaded with its in_proj rows.
+struct ConvCh {
+    float w0, w1, w2, s0, s1;
+};
+
+__device__ __forceinline__ ConvCh conv_ch_load(const ConvInprojArgs &a, uint32_t ch)
+{
+    const uint32_t k = min(ch, a.dim - 1);
+    return ConvCh{a.conv_w[k * 3], a.conv_w[k * 3 + 1], a.conv_w[k * 3 + 2], a.state[k * 2],
+                  a.state[k * 2 + 1]};
+}
+
+__device__ __forceinline__ void conv_step(float B, float C, float Xv, const ConvCh v, float *s2,
                                           float *y)
 {
 #pragma clang fp contract(off)
     const float bx = B * Xv;
-    const float s0 = s2[0], s1 = s2[1];
     float co = 0.0f;
-    co = co + s0 * w3[0];
-    co = co + s1 * w3[1];
-    co = co + bx * w3[2];
+    co = co + v.s0 * v.w0;
+    co = co + v.s1 * v.w1;
+    co = co + bx * v.w2;
     *y = C * co;
-    s2[0] = s1;
+    s2[0] = v.s1;
     s2[1] = bx;
 }
 
 // in_proj rows B[ch], C[ch], X[ch] of channel ch form one work item.
-template <int NW, int G>
+template <int NW, int G, bool EMB>
 __device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
 {
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
     const uint32_t dim = a.dim, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     auto load = [&](uint32_t ch, Item<3> &it) {
-        if (active) {
-            it.l[0] = load_lane(a.w, ch, b, c);
-            it.l[1] = load_lane(a.w, dim + ch, b, c);
-            it.l[2] = load_lane(a.w, 2 * dim + ch, b, c);
-        }
+        it.l[0] = load_lane_c(a.w, ch, b, c);
+        it.l[1] = load_lane_c(a.w, dim + ch, b, c);
+        it.l[2] = load_lane_c(a.w, 2 * dim + ch, b, c);
     };
     XRaw raw;
     x_issue(a.src, dim, raw);
     Item<3> buf[G];
     fill_items(buf, first, W, dim, load);
+    ConvCh cv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        cv[g] = conv_ch_load(a, first + g * W);
+    keep_issued();
     if (halted)
         return;
-    const float inv = x_stage<NW>(a.src, dim, a.st, raw, xs, red);
+    const float inv = x_stage<NW, EMB>(a.src, dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < dim; it0 += G * W) {
-        if (it0 != first)
+        if (it0 != first) {
             fill_items(buf, it0, W, dim, load);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                cv[g] = conv_ch_load(a, it0 + g * W);
+        }
         float p[3 * G];
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -395,53 +513,63 @@ __device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
             for (int g = 0; g < G; ++g) {
                 const uint32_t ch = it0 + g * W;
                 if (ch < dim)
-                    conv_step(inv * p[3 * g], inv * p[3 * g + 1], inv * p[3 * g + 2],
-                              a.conv_w + ch * 3, a.state + ch * 2, a.y + ch);
+                    conv_step(inv * p[3 * g], inv * p[3 * g + 1], inv * p[3 * g + 2], cv[g],
+                              a.state + ch * 2, a.y + ch);
             }
     }
 }
 
 extern "C" __global__ __launch_bounds__(256) void k_conv_inproj4(const ConvInprojArgs a)
 {
-    conv_inproj_body<4, 1>(a);
+    conv_inproj_body<4, 1, false>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void k_conv_inproj16(const ConvInprojArgs a)
 {
-    conv_inproj_body<16, 1>(a);
+    conv_inproj_body<16, 1, false>(a);
+}
+// First layer of a step: the input is the token's embedding row.
+extern "C" __global__ __launch_bounds__(256) void k_conv_inproj4e(const ConvInprojArgs a)
+{
+    conv_inproj_body<4, 1, true>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_conv_inproj16e(const ConvInprojArgs a)
+{
+    conv_inproj_body<16, 1, true>(a);
 }
 
 // Attention projections: rows of q (dim), k and v (hdkv each) of the normed
 // input, written to qkv[0 .. dim + 2*hdkv).
 __device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t b, uint32_t c)
 {
-    if (r < a.dim)
-        return load_lane(a.wq, r, b, c);
-    if (r < a.dim + a.hdkv)
-        return load_lane(a.wk, r - a.dim, b, c);
-    return load_lane(a.wv, r - a.dim - a.hdkv, b, c);
+    // one load, from the tensor that holds row r (fields selected by value)
+    const bool isq = r < a.dim, isk = !isq && r < a.dim + a.hdkv;
+    Q6T t;
+    t.base = isq ? a.wq.base : isk ? a.wk.base : a.wv.base;
+    t.rows = isq ? a.wq.rows : isk ? a.wk.rows : a.wv.rows;
+    t.nb = isq ? a.wq.nb : isk ? a.wk.nb : a.wv.nb;
+    const uint32_t rr = isq ? r : isk ? r - a.dim : r - a.dim - a.hdkv;
+    return load_lane_c(t, rr, b, c);
 }
 
-template <int NW, int G>
+template <int NW, int G, bool EMB>
 __device__ __forceinline__ void qkv_body(const QkvArgs &a)
 {
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wq.nb;
     const uint32_t rows = a.dim + 2 * a.hdkv, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
-    auto load = [&](uint32_t r, Item<1> &it) {
-        if (active)
-            it.l[0] = qkv_lane(a, r, b, c);
-    };
+    auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = qkv_lane(a, r, b, c); };
     XRaw raw;
     x_issue(a.src, a.dim, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    keep_issued();
     if (halted)
         return;
-    const float inv = x_stage<NW>(a.src, a.dim, a.st, raw, xs, red);
+    const float inv = x_stage<NW, EMB>(a.src, a.dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < rows; it0 += G * W) {
@@ -462,11 +590,19 @@ __device__ __forceinline__ void qkv_body(const QkvArgs &a)
 
 extern "C" __global__ __launch_bounds__(256) void k_qkv4(const QkvArgs a)
 {
-    qkv_body<4, 2>(a);
+    qkv_body<4, 1, false>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void k_qkv16(const QkvArgs a)
 {
-    qkv_body<16, 2>(a);
+    qkv_body<16, 1, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void k_qkv4e(const QkvArgs a)
+{
+    qkv_body<4, 1, true>(a);
+}
+extern "C" __global__ __launch_bounds__(1024) void k_qkv16e(const QkvArgs a)
+{
+    qkv_body<16, 1, true>(a);
 }
 // Per-head RMSNorm then NEOX RoPE of one 64-wide head held one value per lane
 // (lfm.rs:270-286 then 248-267): v *= inv * w[d]; pairs (d, d+32) rotated by
@@ -701,6 +837,7 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
             acc += wv[i] * (xv[i] * nv[i]);
         }
     }
+    keep_issued();
     if (halted)
         return;
     wave_sum2(ss, acc);
@@ -717,64 +854,73 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 }
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
-// Routed: work item (rank, row) reads expert ids[rank]'s rows.  Wave 0 of each
-// workgroup computes the routing while the input vector is staged; the other
-// waves read it from LDS after the barrier (one routing per workgroup keeps
-// the SIMDs free for the loads).  Workgroup 0 stores the routing (ids, weight
+// FUSED: the router logits are the sums of the partials left by
+// k_q6_matvec_route (256 threads: thread t adds float4 t + 256k, k < 4, of the
+// 32 expert columns and float4 t % 32 of the x^2 column, then each half-wave
+// sums one column), logit = dot / sqrt(sum x^2 / n + eps) as in k_router.
+// Routed: work item (rank, row) reads expert ids[rank]'s rows.  The router
+// logits are the first load; every wave computes the routing itself as soon as
+// they arrive and issues its weight loads, so the weight stream starts before
+// the input vector is staged.  Workgroup 0 stores the routing (ids, weight
 // bits) for the down projection.  Dense: the weight loads go out first.
-template <int NW, int G>
+template <int NW, int G, bool FUSED>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
+    static_assert(!FUSED || NW == 4, "the fused router reduction assumes 256 threads");
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
-    __shared__ uint32_t rid[4];
-    __shared__ float rwt[4];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ float rsum[ROUTE_EXPERTS + 1];
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.wg.nb;
-    const bool routed = a.route.logits != nullptr;
+    const bool routed = FUSED || a.route.logits != nullptr;
     const uint32_t n = a.wg.nb * 256;
     const uint32_t ff = a.ff, total = (routed ? a.route.n_used : 1u) * ff;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
+    float4 pv[5];
+    if constexpr (FUSED) {
+        const float4 *pp = reinterpret_cast<const float4 *>(a.route.rpart);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            pv[k] = pp[threadIdx.x + 256 * k];
+        pv[4] = pp[ROUTE_EXPERTS * ROUTE_PARTS / 4 + (threadIdx.x & 31)];
+    }
+    RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
     XRaw raw;
     x_issue(a.src, n, raw);
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int k = 0; k < 5; ++k) {
+            const float h = half_wave_sum((pv[k].x + pv[k].y) + (pv[k].z + pv[k].w));
+            if (k < 4 && (lane & 31) == 31)
+                rsum[wave * 2 + (lane >> 5) + 8 * k] = h;
+            if (k == 4 && threadIdx.x == 31)
+                rsum[ROUTE_EXPERTS] = h;
+        }
+        __syncthreads();
+        rin.lg = rsum[min(lane, (uint32_t)ROUTE_EXPERTS - 1)] /
+                 sqrtf(rsum[ROUTE_EXPERTS] / (float)n + a.src.eps);
+    }
     Routed rt = {0, 0, 0, 0, 0.f, 0.f, 0.f, 0.f};
     auto load = [&](uint32_t it, Item<2> &buf) {
         const uint32_t rank = it / ff, r = it - rank * ff;
         const uint32_t row = routed ? rt.id(rank) * ff + r : r;
-        if (active) {
-            buf.l[0] = load_lane(a.wg, row, b, c);
-            buf.l[1] = load_lane(a.wu, row, b, c);
-        }
+        buf.l[0] = load_lane_c(a.wg, row, b, c);
+        buf.l[1] = load_lane_c(a.wu, row, b, c);
     };
     Item<2> buf[G];
-    if (routed) {
-        if (wave == 0) {
-            const Routed r0 = wave_route(a.route);
-            if (lane < 4) {
-                rid[lane] = r0.id(lane);
-                rwt[lane] = r0.w(lane);
-            }
-        }
-    } else {
-        fill_items(buf, first, W, total, load);
+    if (routed)
+        rt = wave_route(a.route, rin);
+    fill_items(buf, first, W, total, load);
+    if (routed && blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
+        a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
+        a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
     }
+    keep_issued();
     if (halted)
         return;
-    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red); // barrier: routing visible
-    if (routed) {
-        rt.id0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[0]);
-        rt.id1 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[1]);
-        rt.id2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[2]);
-        rt.id3 = (uint32_t)__builtin_amdgcn_readfirstlane((int)rid[3]);
-        rt.w0 = rwt[0], rt.w1 = rwt[1], rt.w2 = rwt[2], rt.w3 = rwt[3];
-        fill_items(buf, first, W, total, load);
-        if (blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
-            a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
-            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
-        }
-    }
+    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < total; it0 += G * W) {
@@ -800,11 +946,15 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 
 extern "C" __global__ __launch_bounds__(256) void k_gateup4(const GateUpArgs a)
 {
-    gateup_body<4, 1>(a);
+    gateup_body<4, 2, false>(a);
 }
 extern "C" __global__ __launch_bounds__(1024) void k_gateup16(const GateUpArgs a)
 {
-    gateup_body<16, 1>(a);
+    gateup_body<16, 2, false>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void k_gateup4f(const GateUpArgs a)
+{
+    gateup_body<4, 2, true>(a);
 }
 
 // Routed down projections and combine (lfm.rs:660-668, resident.rs:101-117).
@@ -831,26 +981,37 @@ extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs 
     __shared__ __attribute__((aligned(16))) float xs[4 * XS_MAX];
     __shared__ float dsh[DOWN_ROWS][4];
     __shared__ float wsh[4];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t tid = threadIdx.x, wave = wave_index(), lane = tid & 63;
     const uint32_t b = lane >> 3, c = lane & 7;
     const uint32_t rank = wave & 3, slot = wave >> 2;
     const uint32_t n_used = a.route.n_used, ff = a.ff, dim = a.dim;
     const bool active = b < a.wd.nb && rank < n_used;
-    const uint32_t e = min(a.route.sel_out[rank], a.route.n_expert - 1);
     const uint32_t k0 = blockIdx.x * DOWN_ROWS;
+    // Load order: the expert id (the weight addresses depend on it), then what
+    // does not depend on it (sw, the routing weights, the residual rows this
+    // workgroup updates), then the expert's weights.
+    // Every load is issued without a branch (indices clamped, unused values
+    // ignored) so that the wait for the id does not also wait for the rest.
+    const uint32_t e = min(a.route.sel_out[rank], a.route.n_expert - 1);
+    const uint32_t nsw = n_used * ff; // <= 4 * XS_MAX (n_used <= 4, ff <= 2048)
+    const uint32_t i0 = tid * 4, i1 = i0 + 1024 * 4;
+    const float4 sv0 = *reinterpret_cast<const float4 *>(a.sw + min(i0, nsw - 4));
+    const float4 sv1 = *reinterpret_cast<const float4 *>(a.sw + min(i1, nsw - 4));
+    const uint32_t wbits = a.route.sel_out[8 + (tid & 3)];
+    const float xold = a.x[min(k0 + (tid & (DOWN_ROWS - 1)), dim - 1)];
     Item<1> buf[2];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const uint32_t k = k0 + slot + 4 * g;
-        if (active && k < dim)
-            buf[g].l[0] = load_lane(a.wd, e * dim + k, b, c);
-    }
+    for (int g = 0; g < 2; ++g)
+        buf[g].l[0] = load_lane_c(a.wd, e * dim + min(k0 + slot + 4 * g, dim - 1), b, c);
+    keep_issued();
     if (halted)
         return;
     if (tid < 4)
-        wsh[tid] = __uint_as_float(a.route.sel_out[8 + tid]);
-    for (uint32_t i = tid * 4; i < n_used * ff; i += 1024 * 4)
-        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.sw + i);
+        wsh[tid] = __uint_as_float(wbits);
+    if (i0 < nsw)
+        *reinterpret_cast<float4 *>(xs + i0) = sv0;
+    if (i1 < nsw)
+        *reinterpret_cast<float4 *>(xs + i1) = sv1;
     __syncthreads();
     LaneX X;
     lanex_lds(X, xs + rank * ff, b, c, active);
@@ -865,7 +1026,7 @@ extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs 
     }
     __syncthreads();
     if (tid < DOWN_ROWS && k0 + tid < dim)
-        a.x[k0 + tid] = combine(dsh[tid], wsh, n_used, a.x[k0 + tid]);
+        a.x[k0 + tid] = combine(dsh[tid], wsh, n_used, xold);
 }
 // (value, index) merge for greedy argmax (main.rs:112-141): the larger value
 // wins; equal values keep the lower index; -inf is "no candidate" and NaN
@@ -915,18 +1076,16 @@ __device__ __forceinline__ void head_body(const HeadArgs &a)
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.emb.nb;
     const uint32_t rows = a.vocab, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
-    auto load = [&](uint32_t r, Item<1> &it) {
-        if (active)
-            it.l[0] = load_lane(a.emb, r, b, c);
-    };
+    auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c(a.emb, r, b, c); };
     XRaw raw;
     x_issue(a.src, a.emb.nb * 256, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
+    keep_issued();
     if (halted)
         return;
     const float inv = x_stage<NW>(a.src, a.emb.nb * 256, a.st, raw, xs, red);

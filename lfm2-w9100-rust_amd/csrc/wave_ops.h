@@ -32,6 +32,18 @@ __device__ __forceinline__ float wave_sum(float v)
     return lane63(v);
 }
 
+// Sums over each half of the wave: lanes 0..31 in lane 31, lanes 32..63 in
+// lane 63 (the first five steps of wave_sum).
+__device__ __forceinline__ float half_wave_sum(float v)
+{
+    v += dpp_mov<0xb1>(v, 0.f);
+    v += dpp_mov<0x4e>(v, 0.f);
+    v += dpp_mov<0x114>(v, 0.f);
+    v += dpp_mov<0x118>(v, 0.f);
+    v += dpp_mov<0x142>(v, 0.f);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
     v = fmaxf(v, dpp_mov<0xb1>(v, -INFINITY));
@@ -68,15 +80,42 @@ __device__ __forceinline__ float lane_f32(float v, uint32_t j)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), (int)j));
 }
 
-__device__ __forceinline__ Routed wave_route(const Route &r)
+// The lane's router logit and bias (lane < n_expert), loaded apart from the
+// selection so that a kernel can issue them before its other loads.
+struct RouteIn {
+    float lg, bias;
+};
+
+__device__ __forceinline__ RouteIn route_load(const Route &r)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    RouteIn in = {0.f, 0.f};
+    if (lane < r.n_expert) {
+        in.lg = r.logits[lane];
+        in.bias = r.bias[lane];
+    }
+    return in;
+}
+
+// Decode form: every lane loads (the index clamped to a valid expert; lanes
+// past n_expert are masked by wave_route), with no branch around the loads.
+// `alt` (>= 64 floats) stands in for absent logits / bias (dense layers).
+__device__ __forceinline__ RouteIn route_load_all(const Route &r, const float *alt)
+{
+    const uint32_t j = min(threadIdx.x & 63, r.n_expert - 1);
+    const float *lg = r.logits ? r.logits : alt;
+    const float *bs = r.bias ? r.bias : alt;
+    return RouteIn{lg[j], bs[j]};
+}
+
+__device__ __forceinline__ Routed wave_route(const Route &r, const RouteIn in)
 {
     const uint32_t lane = threadIdx.x & 63;
     const bool valid = lane < r.n_expert;
     float prob = 0.f, score = -INFINITY;
     if (valid) {
-        const float lg = r.logits[lane];
-        prob = 1.0f / (1.0f + expf(-lg));
-        score = prob + r.bias[lane];
+        prob = 1.0f / (1.0f + expf(-in.lg));
+        score = prob + in.bias;
     }
     uint32_t id[4];
     float p[4];
@@ -105,4 +144,9 @@ __device__ __forceinline__ Routed wave_route(const Route &r)
     o.id0 = id[0], o.id1 = id[1], o.id2 = id[2], o.id3 = id[3];
     o.w0 = p[0] / wsum, o.w1 = p[1] / wsum, o.w2 = p[2] / wsum, o.w3 = p[3] / wsum;
     return o;
+}
+
+__device__ __forceinline__ Routed wave_route(const Route &r)
+{
+    return wave_route(r, route_load(r));
 }
