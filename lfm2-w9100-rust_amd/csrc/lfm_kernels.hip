@@ -99,6 +99,27 @@ __device__ __forceinline__ uint32_t wave_index()
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// A zero held in a vector register that the compiler cannot see through.
+// Added to a wave-uniform index it keeps that load on the vector memory path:
+// a scalar load is waited for with the counter that also covers LDS, so the
+// first LDS wait after it (the input staging) would wait for memory too.
+__device__ __forceinline__ uint32_t vzero()
+{
+    uint32_t z;
+    asm("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+// Workgroup barrier with no memory fence: it orders instruction issue only
+// (the loads before it are all issued before any load after it), and waits
+// for no data.
+__device__ __forceinline__ void issue_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Compiler-only fence placed between a kernel's issued loads and its halt
 // check: without it the compiler sinks the (unconditional) loads below the
 // early return, so they would wait for the flag.
@@ -112,6 +133,9 @@ __device__ __forceinline__ void keep_issued() { asm volatile("" ::: "memory"); }
 // the reduction off the path of the weight loads, which every kernel issues
 // before staging.
 #define XS_MAX 2048
+#ifndef ISSUE_ORDER
+#define ISSUE_ORDER() issue_barrier()
+#endif
 
 struct XRaw {
     float4 x0, x1, w0, w1;
@@ -264,7 +288,7 @@ __device__ __forceinline__ void residual_issue(float (&yold)[G], const float *y,
 {
 #pragma unroll
     for (int g = 0; g < G; ++g)
-        yold[g] = y[min(it0 + g * W, rows - 1)];
+        yold[g] = y[min(it0 + g * W, rows - 1) + vzero()];
 }
 
 // ------------------------------------------------------------------ kernels
@@ -324,30 +348,29 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArg
 }
 
 // Output projection y += W x (mode 1) with the router's first stage
-// (lfm.rs:599-607): one wave per row, ROUTE_ROWS rows per workgroup; the
-// workgroup's new residual rows give the partial dots
-//   sum_r R[e][r] * (y[r] * w_norm[r])  (e < 32, lane e)   and   sum_r y[r]^2
-// stored column-major in rpart; k_gateup4f adds the ROUTE_PARTS partials and
-// applies the RMSNorm scale.  The grid is exactly rows / ROUTE_ROWS.
+// (lfm.rs:599-607): one wave per row, ROUTE_ROWS rows per workgroup.  Wave w
+// (row r) loads R[e][r] for e = lane % 32 and w_norm[r] with its weights; once
+// its y[r] is known, lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32
+// y[r]^2, and wave 0 adds the workgroup's rows in order, leaving the partials
+// column-major in rpart for k_gateup4f.  The grid is exactly rows / ROUTE_ROWS.
 extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_route(const MatvecRouteArgs ra)
 {
     const MatvecArgs &a = ra.m;
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[16];
-    __shared__ float yn[ROUTE_ROWS];
+    __shared__ float part[ROUTE_ROWS][ROUTE_EXPERTS + 1];
     const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.w.nb;
-    const uint32_t r0 = blockIdx.x * ROUTE_ROWS, r = r0 + wave;
+    const uint32_t r = blockIdx.x * ROUTE_ROWS + wave;
     XRaw raw;
     x_issue(a.src, a.in_dim, raw);
+    ISSUE_ORDER();
     const Lane w = load_lane_c(a.w, r, b, c);
-    const float yold = a.y[r];
-    // router weights of the workgroup's rows for expert lane % 32 (used by wave 0)
-    const float4 *rwp =
-        reinterpret_cast<const float4 *>(ra.rw + (size_t)(lane & (ROUTE_EXPERTS - 1)) * a.w.rows + r0);
-    const float4 q0 = rwp[0], q1 = rwp[1], q2 = rwp[2], q3 = rwp[3];
+    const float yold = a.y[r + vzero()];
+    const float rwe = ra.rw[(size_t)(lane & (ROUTE_EXPERTS - 1)) * a.w.rows + r];
+    const float nwr = ra.rnorm[r + vzero()];
     keep_issued();
     if (halted)
         return;
@@ -356,26 +379,19 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_route(const Matve
     lanex_lds(X, xs, b, c, active);
     const float p = wave_sum(active ? lane_dot(w, X) : 0.f);
     const float v = yold + inv * p;
-    if (lane == 0) {
+    if (lane == 0)
         a.y[r] = v;
-        yn[wave] = v;
-    }
+    if (lane < ROUTE_EXPERTS)
+        part[wave][lane] = rwe * (v * nwr);
+    else if (lane == ROUTE_EXPERTS)
+        part[wave][lane] = v * v;
     __syncthreads();
-    if (wave == 0) {
-        const float rv[ROUTE_ROWS] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w,
-                                      q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
-        const float *nw = ra.rnorm + r0;
-        float acc = 0.f, ss = 0.f;
+    if (wave == 0 && lane <= ROUTE_EXPERTS) {
+        float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < ROUTE_ROWS; ++i) {
-            const float xv = yn[i];
-            acc += rv[i] * (xv * nw[i]);
-            ss += xv * xv;
-        }
-        if (lane < ROUTE_EXPERTS)
-            ra.rpart[lane * ROUTE_PARTS + blockIdx.x] = acc;
-        else if (lane == ROUTE_EXPERTS)
-            ra.rpart[ROUTE_EXPERTS * ROUTE_PARTS + blockIdx.x] = ss;
+        for (int i = 0; i < ROUTE_ROWS; ++i)
+            acc += part[i][lane];
+        ra.rpart[lane * ROUTE_PARTS + blockIdx.x] = acc;
     }
 }
 // Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
@@ -445,7 +461,7 @@ struct ConvCh {
 
 __device__ __forceinline__ ConvCh conv_ch_load(const ConvInprojArgs &a, uint32_t ch)
 {
-    const uint32_t k = min(ch, a.dim - 1);
+    const uint32_t k = min(ch, a.dim - 1) + vzero();
     return ConvCh{a.conv_w[k * 3], a.conv_w[k * 3 + 1], a.conv_w[k * 3 + 2], a.state[k * 2],
                   a.state[k * 2 + 1]};
 }
@@ -608,17 +624,55 @@ extern "C" __global__ __launch_bounds__(1024) void k_qkv16e(const QkvArgs a)
 // (lfm.rs:270-286 then 248-267): v *= inv * w[d]; pairs (d, d+32) rotated by
 // theta = pos * tscale^(d%32).  cs_sn is the position's row of the (cos, sin)
 // table the host fills at finalize with the reference's own arithmetic.
-__device__ __forceinline__ float head_norm_rope(float v, const float *w, float eps,
-                                                const float *cs_sn, uint32_t d)
+// The lane's norm weight w[d] and its (cos, sin) pair, loaded ahead of use.
+struct HeadIn {
+    float w, cs, sn;
+};
+
+__device__ __forceinline__ HeadIn head_in_load(const float *w, const float *cs_sn, uint32_t d)
+{
+    const uint32_t p = d & 31;
+    return HeadIn{w[d], cs_sn[2 * p], cs_sn[2 * p + 1]};
+}
+
+__device__ __forceinline__ float head_norm_rope(float v, const HeadIn in, float eps, uint32_t d)
 {
     const float ss = wave_sum(v * v);
     const float inv = 1.0f / sqrtf(ss / 64.0f + eps);
-    v *= inv * w[d];
+    v *= inv * in.w;
     const float other = __shfl_xor(v, 32, 64);
-    const uint32_t p = d & 31;
-    const float cs = cs_sn[2 * p], sn = cs_sn[2 * p + 1];
+    const float cs = in.cs, sn = in.sn;
     // lane d < 32 holds x0 (partner x1); lane d >= 32 holds x1 (partner x0)
     return d < 32 ? v * cs - other * sn : other * sn + v * cs;
+}
+
+// 16 bytes of one cached K row and of the V row: piece u of a chunk is row
+// t0 + u/8, halves 8*(u%8) .. +8 (rows past the cache re-read its last row).
+struct KvPiece {
+    uint4 k, v;
+};
+
+__device__ __forceinline__ KvPiece kv_piece(const uint16_t *kg, const uint16_t *vg, uint32_t t0,
+                                            uint32_t ctx, uint32_t u)
+{
+    const size_t off = (size_t)min(t0 + (u >> 3), ctx - 1) * 64 + (u & 7) * 8;
+    return KvPiece{*reinterpret_cast<const uint4 *>(kg + off), *reinterpret_cast<const uint4 *>(vg + off)};
+}
+
+// Stores a piece in LDS: rows past the position as zeros (their weights are
+// zero and the P.V loop runs over the whole chunk); the position's own row is
+// left to the wave that computes it.
+__device__ __forceinline__ void kv_stage(const KvPiece pc, uint16_t *Ks, uint16_t *Vs, uint32_t t0,
+                                         uint32_t nt, uint32_t p, uint32_t u)
+{
+    const uint32_t t = u >> 3, seg = u & 7;
+    if (t0 + t == p)
+        return;
+    const uint32_t m = t < nt ? 0xFFFFFFFFu : 0u; // per-word mask (no aggregate select)
+    *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) =
+        make_uint4(pc.k.x & m, pc.k.y & m, pc.k.z & m, pc.k.w & m);
+    *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) =
+        make_uint4(pc.v.x & m, pc.v.y & m, pc.v.z & m, pc.v.w & m);
 }
 
 // Split-K decode attention over the binary16 KV cache (lfm.rs:395-437): one
@@ -635,26 +689,29 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     const uint32_t dim = a.heads * 64, hdkv = a.kv * 64;
     // Position and halt flag with vector loads; the chunk's K/V rows, q and the
     // new K/V values are issued before the position is known (rows past the
-    // cache end re-read its last row and are never used).
-    const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)__hip_atomic_load(&a.st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    // cache end re-read its last row and are never used), then the norm
+    // weights and the position's RoPE row.
+    const uint32_t pos_raw =
+        __hip_atomic_load(&a.st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t halted = load_halt(a.st);
-    constexpr int PASSES = ATT_CH * 8 / WG_THREADS; // 16-B pieces per thread
-    uint4 kr[PASSES], vr[PASSES];
-    {
-        const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
-        const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
-#pragma unroll
-        for (int i = 0; i < PASSES; ++i) {
-            const uint32_t u = tid + i * WG_THREADS, seg = u & 7;
-            const uint32_t row = min(t0 + (u >> 3), a.ctx - 1);
-            kr[i] = *reinterpret_cast<const uint4 *>(kg + (size_t)row * 64 + seg * 8);
-            vr[i] = *reinterpret_cast<const uint4 *>(vg + (size_t)row * 64 + seg * 8);
-        }
-    }
-    const float qraw = wave < G ? a.qkv[(kh * G + wave) * 64 + lane] : 0.f;
-    const float kraw = wave == 0 ? a.qkv[dim + kh * 64 + lane] : 0.f;
-    const float vraw = wave == 0 ? a.qkv[dim + hdkv + kh * 64 + lane] : 0.f;
+    static_assert(ATT_CH * 8 / WG_THREADS == 4, "four 16-B K and V pieces per thread");
+    const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
+    const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
+    const KvPiece p0 = kv_piece(kg, vg, t0, a.ctx, tid);
+    const KvPiece p1 = kv_piece(kg, vg, t0, a.ctx, tid + WG_THREADS);
+    const KvPiece p2 = kv_piece(kg, vg, t0, a.ctx, tid + 2 * WG_THREADS);
+    const KvPiece p3 = kv_piece(kg, vg, t0, a.ctx, tid + 3 * WG_THREADS);
+    // q, k, v of the new position (clamped indices, no branch around the loads)
+    const float qraw = a.qkv[(kh * G + min(wave, G - 1)) * 64 + lane];
+    const float kraw = a.qkv[dim + kh * 64 + lane];
+    const float vraw = a.qkv[dim + hdkv + kh * 64 + lane];
+    // the position is waited for here, after every load above is issued
+    uint32_t pos_v = pos_raw;
+    asm volatile("" : "+v"(pos_v) : : "memory");
+    const uint32_t p = (uint32_t)__builtin_amdgcn_readfirstlane((int)pos_v);
+    const HeadIn hq = head_in_load(a.q_norm, a.rope + (size_t)p * 64, lane);
+    const HeadIn hk = head_in_load(a.k_norm, a.rope + (size_t)p * 64, lane);
+    keep_issued();
     if (halted || t0 > p)
         return;
     const uint32_t nact = p / ATT_CH + 1;
@@ -662,55 +719,44 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
     const bool cur = (chunk == nact - 1);
 
     __shared__ float qr[4][64];
-    __shared__ float knew[64], vnew[64];
     __shared__ __attribute__((aligned(16))) uint16_t Ks[ATT_CH * ATT_KROW];
     __shared__ __attribute__((aligned(16))) uint16_t Vs[ATT_CH * 64];
     __shared__ float sc[4][ATT_CH];
     __shared__ float stat[4][2];
 
-#pragma unroll
-    for (int i = 0; i < PASSES; ++i) {
-        const uint32_t u = tid + i * WG_THREADS, t = u >> 3, seg = u & 7;
-        if (t < nt && t0 + t != p) {
-            *reinterpret_cast<uint4 *>(Ks + t * ATT_KROW + seg * 8) = kr[i];
-            *reinterpret_cast<uint4 *>(Vs + t * 64 + seg * 8) = vr[i];
-        }
-    }
+    kv_stage(p0, Ks, Vs, t0, nt, p, tid);
+    kv_stage(p1, Ks, Vs, t0, nt, p, tid + WG_THREADS);
+    kv_stage(p2, Ks, Vs, t0, nt, p, tid + 2 * WG_THREADS);
+    kv_stage(p3, Ks, Vs, t0, nt, p, tid + 3 * WG_THREADS);
     if (wave < G)
-        qr[wave][lane] = head_norm_rope(qraw, a.q_norm, a.eps, a.rope + (size_t)p * 64, lane);
+        qr[wave][lane] = head_norm_rope(qraw, hq, a.eps, lane);
     if (cur && wave == 0) {
-        const float krot = head_norm_rope(kraw, a.k_norm, a.eps, a.rope + (size_t)p * 64, lane);
+        const float krot = head_norm_rope(kraw, hk, a.eps, lane);
         const uint16_t kb = float_to_half_bits(krot);
         const uint16_t vb = float_to_half_bits(vraw);
         a.kcache[((size_t)kh * a.ctx + p) * 64 + lane] = kb;
         a.vcache[((size_t)kh * a.ctx + p) * 64 + lane] = vb;
-        knew[lane] = half_bits_to_float(kb);
-        vnew[lane] = half_bits_to_float(vb);
+        Ks[(p - t0) * ATT_KROW + lane] = kb;
+        Vs[(p - t0) * 64 + lane] = vb;
     }
     __syncthreads();
     // scores: thread -> position t, heads 2*hp and 2*hp+1
     {
         const uint32_t t = tid & (ATT_CH - 1), hp = tid >> 7;
-        const bool isnew = (t0 + t == p);
         for (uint32_t hh = 2 * hp; hh < 2 * hp + 2; ++hh) {
             if (hh >= G)
                 break;
             float s = -INFINITY;
             if (t < nt) {
                 float acc = 0.f;
-                if (isnew) {
-                    for (int d = 0; d < 64; ++d)
-                        acc += qr[hh][d] * knew[d];
-                } else {
 #pragma unroll
-                    for (int d8 = 0; d8 < 8; ++d8) {
-                        const uint4 kv8 = *reinterpret_cast<const uint4 *>(Ks + t * ATT_KROW + d8 * 8);
-                        const uint32_t w4[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
+                for (int d8 = 0; d8 < 8; ++d8) {
+                    const uint4 kv8 = *reinterpret_cast<const uint4 *>(Ks + t * ATT_KROW + d8 * 8);
+                    const uint32_t w4[4] = {kv8.x, kv8.y, kv8.z, kv8.w};
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            acc += qr[hh][d8 * 8 + 2 * j] * half_bits_to_float(w4[j] & 0xFFFFu);
-                            acc += qr[hh][d8 * 8 + 2 * j + 1] * half_bits_to_float(w4[j] >> 16);
-                        }
+                    for (int j = 0; j < 4; ++j) {
+                        acc += qr[hh][d8 * 8 + 2 * j] * half_bits_to_float(w4[j] & 0xFFFFu);
+                        acc += qr[hh][d8 * 8 + 2 * j + 1] * half_bits_to_float(w4[j] >> 16);
                     }
                 }
                 s = acc * a.scale;
@@ -732,17 +778,31 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn(const AttnArgs a
         }
     }
     __syncthreads();
-    const uint32_t hh = tid >> 6, d = tid & 63;
-    if (hh < G) {
-        float acc = 0.f;
+    // P.V: wave = head; lane (d4, tq) accumulates dims 4*d4 .. +3 over the
+    // positions t = 4i + tq (a wave reads 512 contiguous bytes of V per step),
+    // then the four position classes are summed across the lane quad.
+    if (wave < G) {
+        const uint32_t hh = wave, tq = lane & 3, d4 = lane >> 2;
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
 #pragma unroll 8
-        for (uint32_t t = 0; t < nt; ++t) {
-            const float vv = (t0 + t == p) ? vnew[d] : half_bits_to_float(Vs[t * 64 + d]);
-            acc += sc[hh][t] * vv;
+        for (uint32_t i = 0; i < ATT_CH / 4; ++i) {
+            const uint32_t t = 4 * i + tq;
+            const uint2 v = *reinterpret_cast<const uint2 *>(Vs + t * 64 + d4 * 4);
+            const float pr = sc[hh][t];
+            o0 += pr * half_bits_to_float(v.x & 0xFFFFu);
+            o1 += pr * half_bits_to_float(v.x >> 16);
+            o2 += pr * half_bits_to_float(v.y & 0xFFFFu);
+            o3 += pr * half_bits_to_float(v.y >> 16);
         }
+        o0 = quad_sum(o0), o1 = quad_sum(o1), o2 = quad_sum(o2), o3 = quad_sum(o3);
         float *part = a.part + (((size_t)kh * a.nchunk + chunk) * 4 + hh) * 66;
-        part[2 + d] = acc;
-        if (d == 0) {
+        if (tq == 0) {
+            part[2 + 4 * d4] = o0;
+            part[3 + 4 * d4] = o1;
+            part[4 + 4 * d4] = o2;
+            part[5 + 4 * d4] = o3;
+        }
+        if (lane == 0) {
             part[0] = stat[hh][0];
             part[1] = stat[hh][1];
         }

@@ -32,6 +32,14 @@ __device__ __forceinline__ float wave_sum(float v)
     return lane63(v);
 }
 
+// Sum over each group of four lanes, in all four lanes.
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v += dpp_mov<0xb1>(v, 0.f); // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4e>(v, 0.f); // quad_perm [2,3,0,1]
+    return v;
+}
+
 // Sums over each half of the wave: lanes 0..31 in lane 31, lanes 32..63 in
 // lane 63 (the first five steps of wave_sum).
 __device__ __forceinline__ float half_wave_sum(float v)
