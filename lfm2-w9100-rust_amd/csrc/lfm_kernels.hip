@@ -959,8 +959,10 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
                 rsum[ROUTE_EXPERTS] = h;
         }
         __syncthreads();
-        rin.lg = rsum[min(lane, (uint32_t)ROUTE_EXPERTS - 1)] /
-                 sqrtf(rsum[ROUTE_EXPERTS] / (float)n + a.src.eps);
+        // logit = dot / sqrt(sum x^2 / n + eps), with the hardware reciprocal
+        // square root (n is a power of two, so the scaling by 1/n is exact)
+        rin.lg = rsum[min(lane, (uint32_t)ROUTE_EXPERTS - 1)] *
+                 __builtin_amdgcn_rsqf(rsum[ROUTE_EXPERTS] * __builtin_amdgcn_rcpf((float)n) + a.src.eps);
     }
     Routed rt = {0, 0, 0, 0, 0.f, 0.f, 0.f, 0.f};
     auto load = [&](uint32_t it, Item<2> &buf) {
@@ -971,11 +973,15 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     };
     Item<2> buf[G];
     if (routed)
-        rt = wave_route(a.route, rin);
+        rt = wave_route_ids(a.route, rin);
     fill_items(buf, first, W, total, load);
-    if (routed && blockIdx.x == 0 && wave == 0 && lane < 8 && a.route.sel_out) {
-        a.route.sel_out[lane] = lane < 4 ? rt.id(lane) : 0u;
-        a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rt.w(lane)) : 0u;
+    if (routed && blockIdx.x == 0 && wave == 0 && a.route.sel_out) {
+        Routed rw = rt;
+        route_normalize(rw, a.route.n_used);
+        if (lane < 8) {
+            a.route.sel_out[lane] = lane < 4 ? rw.id(lane) : 0u;
+            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rw.w(lane)) : 0u;
+        }
     }
     keep_issued();
     if (halted)

@@ -68,7 +68,7 @@ __device__ __forceinline__ float wave_max(float v)
 // Round k takes the largest remaining score, the lowest expert id among equal
 // scores (the order of a stable descending sort); the n_used picks are
 // weighted p / max(sum in rank order, 2^-14).  NaN scores are never picked
-// while a finite one remains; the ids are always valid experts.  Results are
+// while a number remains; the ids are always valid experts.  Results are
 // wave-uniform scalars (small arrays would be placed in memory).
 struct Routed {
     uint32_t id0, id1, id2, id3;
@@ -116,14 +116,47 @@ __device__ __forceinline__ RouteIn route_load_all(const Route &r, const float *a
     return RouteIn{lg[j], bs[j]};
 }
 
-__device__ __forceinline__ Routed wave_route(const Route &r, const RouteIn in)
+// Order-preserving integer key of a float: for numbers, a < b exactly when
+// key(a) < key(b) (+0 and -0 are made equal first).  Integer maxima need no
+// NaN handling and fold into single DPP instructions.
+__device__ __forceinline__ int float_key(float v)
+{
+    const int b = __float_as_int(v + 0.0f);
+    return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+
+template <int CTRL> __device__ __forceinline__ int dpp_imax(int v)
+{
+    const int o = __builtin_amdgcn_update_dpp((int)0x80000000, v, CTRL, 0xf, 0xf, false);
+    return max(v, o);
+}
+
+__device__ __forceinline__ int wave_max_i(int v)
+{
+    v = dpp_imax<0xb1>(v);
+    v = dpp_imax<0x4e>(v);
+    v = dpp_imax<0x114>(v);
+    v = dpp_imax<0x118>(v);
+    v = dpp_imax<0x142>(v);
+    v = dpp_imax<0x143>(v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// The ids of the n_used picks and their probabilities (weights before the
+// normalization of route_normalize).  Selection on integer keys of the
+// scores: removed experts and lanes past n_expert take the lowest key, NaN
+// scores the next (below every number), so numbers rank exactly as floats.
+__device__ __forceinline__ Routed wave_route_ids(const Route &r, const RouteIn in)
 {
     const uint32_t lane = threadIdx.x & 63;
     const bool valid = lane < r.n_expert;
-    float prob = 0.f, score = -INFINITY;
+    float prob = 0.f;
+    int key = (int)0x80000000;
     if (valid) {
-        prob = 1.0f / (1.0f + expf(-in.lg));
-        score = prob + in.bias;
+        // sigmoid with the hardware exp2 / reciprocal (a few ulp)
+        prob = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(in.lg * -1.44269504088896341f));
+        const float score = prob + in.bias;
+        key = score == score ? float_key(score) : (int)0x80000001;
     }
     uint32_t id[4];
     float p[4];
@@ -132,25 +165,41 @@ __device__ __forceinline__ Routed wave_route(const Route &r, const RouteIn in)
         id[k] = 0;
         p[k] = 0.f;
         if ((uint32_t)k < r.n_used) {
-            const float best = wave_max(score);
-            const uint64_t m = __ballot(valid && score == best);
+            const int best = wave_max_i(key);
+            const uint64_t m = __ballot(valid && key == best);
             const uint32_t e = m ? (uint32_t)__ffsll((long long)m) - 1u : 0u;
             id[k] = e;
             p[k] = lane_f32(prob, e);
             if (lane == e)
-                score = -INFINITY;
+                key = (int)0x80000000;
         }
     }
-    float wsum = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        if ((uint32_t)k < r.n_used)
-            wsum = wsum + p[k];
-    if (wsum < 6.103515625e-5f)
-        wsum = 6.103515625e-5f;
     Routed o;
     o.id0 = id[0], o.id1 = id[1], o.id2 = id[2], o.id3 = id[3];
-    o.w0 = p[0] / wsum, o.w1 = p[1] / wsum, o.w2 = p[2] / wsum, o.w3 = p[3] / wsum;
+    o.w0 = p[0], o.w1 = p[1], o.w2 = p[2], o.w3 = p[3];
+    return o;
+}
+
+// Weights p / max(sum of the picks' p in rank order, 2^-14).
+__device__ __forceinline__ void route_normalize(Routed &o, uint32_t n_used)
+{
+    float wsum = 0.f;
+    wsum = wsum + o.w0;
+    if (n_used > 1)
+        wsum = wsum + o.w1;
+    if (n_used > 2)
+        wsum = wsum + o.w2;
+    if (n_used > 3)
+        wsum = wsum + o.w3;
+    if (wsum < 6.103515625e-5f)
+        wsum = 6.103515625e-5f;
+    o.w0 = o.w0 / wsum, o.w1 = o.w1 / wsum, o.w2 = o.w2 / wsum, o.w3 = o.w3 / wsum;
+}
+
+__device__ __forceinline__ Routed wave_route(const Route &r, const RouteIn in)
+{
+    Routed o = wave_route_ids(r, in);
+    route_normalize(o, r.n_used);
     return o;
 }
 
