@@ -823,8 +823,8 @@ static XSrc xsrc(const float *x, const float *norm, float eps)
 static bool fused_router(const lfm_engine *e, uint32_t l)
 {
     const lfm_hparams &hp = e->hp;
-    return l >= hp.dense_lead && hp.n_expert == ROUTE_EXPERTS &&
-           hp.dim == ROUTE_ROWS * ROUTE_PARTS && e->K->gateup.nw == 4;
+    return l >= hp.dense_lead && hp.n_expert == ROUTE_EXPERTS && hp.dim == ROUTE_WIDTH &&
+           e->K->gateup.nw == 4;
 }
 
 // Output projection of layer l's mixer (y += W x); with the fused router it
@@ -835,7 +835,7 @@ static int launch_out_proj(lfm_engine *e, uint32_t l, MatvecArgs &m, bool fuse)
 {
     if (!fuse || !fused_router(e, l))
         return launch_matvec(e->K, m, e->stream);
-    if (m.w.rows != ROUTE_ROWS * ROUTE_PARTS || m.w.nb > 8 || m.mode != 1)
+    if (m.w.rows != ROUTE_WIDTH || m.w.nb > 8 || m.mode != 1)
         return fail(LFM_EINTERNAL, "fused router: unexpected output projection shape");
     MatvecRouteArgs ra;
     ra.m = m;

@@ -113,8 +113,11 @@ struct Route {
 // the partial dots sum_r R[e][r] * (x_new[r] * w_norm[r]) and sum_r x_new[r]^2
 // of its rows, which the gate/up kernel adds up.
 #define ROUTE_EXPERTS 32
-#define ROUTE_ROWS 16
-#define ROUTE_PARTS 128
+#ifndef ROUTE_ROWS
+#define ROUTE_ROWS 8
+#endif
+#define ROUTE_WIDTH 2048
+#define ROUTE_PARTS (ROUTE_WIDTH / ROUTE_ROWS)
 
 struct MatvecRouteArgs { // y += W x (mode 1) and the router partial sums of the new y
     MatvecArgs m;

@@ -275,9 +275,7 @@ __device__ __forceinline__ Lane load_lane_c(const Q6T &t, uint32_t row, uint32_t
 // Wave sum of N per-lane values at once (results in every lane).
 template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
 {
-#pragma unroll
-    for (int i = 0; i < N; ++i)
-        v[i] = wave_sum(v[i]);
+    wave_sums<N>(v);
 }
 
 // Old values y[it0 + g*W] of the rows a wave updates in place (lanes with
@@ -353,12 +351,12 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArg
 // its y[r] is known, lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32
 // y[r]^2, and wave 0 adds the workgroup's rows in order, leaving the partials
 // column-major in rpart for k_gateup4f.  The grid is exactly rows / ROUTE_ROWS.
-extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_route(const MatvecRouteArgs ra)
+extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(const MatvecRouteArgs ra)
 {
     const MatvecArgs &a = ra.m;
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
-    __shared__ float red[16];
+    __shared__ float red[ROUTE_ROWS];
     __shared__ float part[ROUTE_ROWS][ROUTE_EXPERTS + 1];
     const uint32_t lane = threadIdx.x & 63, wave = wave_index();
     const uint32_t b = lane >> 3, c = lane & 7;
@@ -374,7 +372,7 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_route(const Matve
     keep_issued();
     if (halted)
         return;
-    const float inv = x_stage<16>(a.src, a.in_dim, a.st, raw, xs, red);
+    const float inv = x_stage<ROUTE_ROWS>(a.src, a.in_dim, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     const float p = wave_sum(active ? lane_dot(w, X) : 0.f);
@@ -938,25 +936,45 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     const uint32_t n = a.wg.nb * 256;
     const uint32_t ff = a.ff, total = (routed ? a.route.n_used : 1u) * ff;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
-    float4 pv[5];
+    // router partial sums: column e (ROUTE_PARTS floats) holds QC float4; thread
+    // t loads float4 t + 256k of the 32 expert columns and float4 t % QC of the
+    // x^2 column
+    constexpr int QC = ROUTE_PARTS / 4, NK = ROUTE_EXPERTS * QC / 256;
+    static_assert(QC == 32 || QC == 64, "a column is a half wave or a wave of float4");
+    float4 pv[NK + 1];
     if constexpr (FUSED) {
         const float4 *pp = reinterpret_cast<const float4 *>(a.route.rpart);
 #pragma unroll
-        for (int k = 0; k < 4; ++k)
+        for (int k = 0; k < NK; ++k)
             pv[k] = pp[threadIdx.x + 256 * k];
-        pv[4] = pp[ROUTE_EXPERTS * ROUTE_PARTS / 4 + (threadIdx.x & 31)];
+        pv[NK] = pp[ROUTE_EXPERTS * QC + (threadIdx.x & (QC - 1))];
     }
     RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
     XRaw raw;
     x_issue(a.src, n, raw);
     if constexpr (FUSED) {
+        float f[NK + 1];
 #pragma unroll
-        for (int k = 0; k < 5; ++k) {
-            const float h = half_wave_sum((pv[k].x + pv[k].y) + (pv[k].z + pv[k].w));
-            if (k < 4 && (lane & 31) == 31)
-                rsum[wave * 2 + (lane >> 5) + 8 * k] = h;
-            if (k == 4 && threadIdx.x == 31)
-                rsum[ROUTE_EXPERTS] = h;
+        for (int k = 0; k <= NK; ++k)
+            f[k] = (pv[k].x + pv[k].y) + (pv[k].z + pv[k].w);
+        if constexpr (QC == 32) { // two columns per wave (one per half)
+            half_wave_sums<NK + 1>(f);
+            if ((lane & 31) == 31) {
+#pragma unroll
+                for (int k = 0; k < NK; ++k)
+                    rsum[wave * 2 + (lane >> 5) + 8 * k] = f[k];
+                if (threadIdx.x == 31)
+                    rsum[ROUTE_EXPERTS] = f[NK];
+            }
+        } else { // one column per wave
+            wave_sums<NK + 1>(f);
+            if (lane == 0) {
+#pragma unroll
+                for (int k = 0; k < NK; ++k)
+                    rsum[wave + 4 * k] = f[k];
+                if (threadIdx.x == 0)
+                    rsum[ROUTE_EXPERTS] = f[NK];
+            }
         }
         __syncthreads();
         // logit = dot / sqrt(sum x^2 / n + eps), with the hardware reciprocal

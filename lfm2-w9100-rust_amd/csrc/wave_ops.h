@@ -52,6 +52,53 @@ __device__ __forceinline__ float half_wave_sum(float v)
     return v;
 }
 
+// N independent wave sums, their DPP steps interleaved so that each step's
+// wait states are filled by the other sums (results in every lane).
+template <int N> __device__ __forceinline__ void wave_sums(float *v)
+{
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0xb1>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x4e>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x114>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x118>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x142>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x143>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] = lane63(v[i]);
+}
+
+// Half-wave form of wave_sums: lanes 0..31 summed in lane 31, 32..63 in 63.
+template <int N> __device__ __forceinline__ void half_wave_sums(float *v)
+{
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0xb1>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x4e>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x114>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x118>(v[i], 0.f);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += dpp_mov<0x142>(v[i], 0.f);
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
     v = fmaxf(v, dpp_mov<0xb1>(v, -INFINITY));
