@@ -990,21 +990,32 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
         buf.l[1] = load_lane_c(a.wu, row, b, c);
     };
     Item<2> buf[G];
-    if (routed)
+    float inv;
+    if (routed) {
+        // The input (loaded with the router partials) has arrived by the time
+        // the routing is known: stage it first, then issue the weights.  A
+        // wave stalls while the CU's load queue is full, so staging after a
+        // deep weight issue would hold back every dot product.
         rt = wave_route_ids(a.route, rin);
-    fill_items(buf, first, W, total, load);
-    if (routed && blockIdx.x == 0 && wave == 0 && a.route.sel_out) {
-        Routed rw = rt;
-        route_normalize(rw, a.route.n_used);
-        if (lane < 8) {
-            a.route.sel_out[lane] = lane < 4 ? rw.id(lane) : 0u;
-            a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rw.w(lane)) : 0u;
+        if (blockIdx.x == 0 && wave == 0 && a.route.sel_out) {
+            Routed rw = rt;
+            route_normalize(rw, a.route.n_used);
+            if (lane < 8) {
+                a.route.sel_out[lane] = lane < 4 ? rw.id(lane) : 0u;
+                a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rw.w(lane)) : 0u;
+            }
         }
+        if (halted)
+            return;
+        inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
+        fill_items(buf, first, W, total, load);
+    } else {
+        fill_items(buf, first, W, total, load);
+        keep_issued();
+        if (halted)
+            return;
+        inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     }
-    keep_issued();
-    if (halted)
-        return;
-    const float inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     LaneX X;
     lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < total; it0 += G * W) {
