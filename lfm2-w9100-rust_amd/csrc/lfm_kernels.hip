@@ -1094,10 +1094,11 @@ extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs 
     const float4 sv1 = *reinterpret_cast<const float4 *>(a.sw + min(i1, nsw - 4));
     const uint32_t wbits = a.route.sel_out[8 + (tid & 3)];
     const float xold = a.x[min(k0 + (tid & (DOWN_ROWS - 1)), dim - 1)];
+    // First row's weights, then the staging of sw, then the second row: with
+    // both rows issued first, the CU's full load queue stalls the waves before
+    // they reach the staging barrier.
     Item<1> buf[2];
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-        buf[g].l[0] = load_lane_c(a.wd, e * dim + min(k0 + slot + 4 * g, dim - 1), b, c);
+    buf[0].l[0] = load_lane_c(a.wd, e * dim + min(k0 + slot, dim - 1), b, c);
     keep_issued();
     if (halted)
         return;
@@ -1108,6 +1109,7 @@ extern "C" __global__ __launch_bounds__(1024) void k_moe_down(const MoeDownArgs 
     if (i1 < nsw)
         *reinterpret_cast<float4 *>(xs + i1) = sv1;
     __syncthreads();
+    buf[1].l[0] = load_lane_c(a.wd, e * dim + min(k0 + slot + 4, dim - 1), b, c);
     LaneX X;
     lanex_lds(X, xs + rank * ff, b, c, active);
     float p[2];
