@@ -29,9 +29,9 @@ import lfm_hip  # noqa: E402
 METRIC = "decode tok/s (bs=1, ctx 4096) + Q6_K matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
-# HBM bytes per k_gateup launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
+# HBM bytes per k_gateup4f launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
 # WRITE_SIZE x 1.0, scales from a plain 512 MiB copy), profiles/k_gateup_traffic.md
-GATEUP_TRAFFIC_BYTES = 24656588
+GATEUP_TRAFFIC_BYTES = 24929364
 SEED = 0x9E3779B97F4A7C15
 
 
@@ -95,7 +95,7 @@ def matvec_roofline(iters=200):
     return algo, ms_hbm, ms_mall
 
 
-def cpu_baseline(hp, snapshot, start_pos, gpu_tokens, first, budget_s=20.0, max_steps=48):
+def cpu_baseline(hp, snapshot, start_pos, gpu_tokens, first, budget_s=15.0, max_steps=128):
     """The oracle (C restatement of the reference CPU path) on the host cores:
     resident state restored from the GPU at the end of the prompt, then greedy
     decode steps teacher-forced with the GPU's tokens until ~budget_s."""
@@ -193,15 +193,28 @@ def main():
     roof = None
     extra = {}
     if not args.no_roofline:
-        # dominant kernel of the decode step: routed MoE gate/up (k_gateup), timed with
-        # HIP events over a graph of its launches across all 22 MoE layers' experts
+        # dominant kernel of the decode step: routed MoE gate/up (k_gateup4f, router
+        # fused), timed with HIP events over a graph of its launches across all 22
+        # MoE layers' experts
         us, nbytes = eng.time_moe_gateup(reps=10)
         gbs = nbytes / (us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                "kernel": "k_gateup (MoE routed gate+up+SwiGLU, 4 experts x 2 x 1792x2048 Q6_K)",
-                "algorithmic_bytes": nbytes, "us_per_launch": round(us, 3)}
-        log(f"[bench] k_gateup (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
+                "kernel": "k_gateup4f (MoE router total + top-4 + routed gate+up+SwiGLU, "
+                          "4 experts x 2 x 1792x2048 Q6_K)",
+                "algorithmic_bytes": nbytes, "us_per_launch": round(us, 3),
+                "timing": "HIP events over a graph of 220 launches (launch gaps included)"}
+        log(f"[bench] k_gateup4f (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
+        # largest single Q6_K matvec of a step: final norm + tied head (vocab x 2048),
+        # over 3 rotating copies of the embedding planes (beyond the Infinity Cache)
+        hus, hbytes = eng.time_head(ncopies=3, reps=5)
+        hgbs = hbytes / (hus * 1e-6) / 1e9
+        extra["q6k_head"] = {
+            "kernel": "k_head4 (final RMSNorm + %dx%d tied head + argmax partials)" % (hp.vocab, hp.dim),
+            "algorithmic_bytes": hbytes, "us_per_launch": round(hus, 3), "hbm_gbs": round(hgbs, 1),
+            "frac_of_peak": round(hgbs / HBM_PEAK_GBS, 4),
+            "timing": "HIP events over a graph of 15 launches rotating 3 weight copies (gaps included)"}
+        log(f"[bench] k_head4: {hus:.2f} us/launch = {hgbs:.0f} GB/s ({hgbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
         algo, ms_hbm, ms_mall = matvec_roofline()
         extra["q6k_matvec_cfg0"] = {
             "shape": "6144x2048", "algorithmic_bytes": algo,

@@ -146,6 +146,15 @@ int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *weights, uint32_t
 int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *us_per_launch,
                                uint64_t *bytes_per_launch);
 
+/* Mean duration of the final-norm + tied-head kernel (vocab x dim Q6_K, the
+ * largest single matvec of a step), timed with HIP events over one graph of
+ * `reps` rounds rotating `ncopies` (1..8) copies of the embedding planes (the
+ * library allocates the extra copies and frees them before returning);
+ * *bytes_per_launch = its algorithmic HBM bytes.  No reference counterpart:
+ * measurement only. */
+int lfm_engine_time_head(lfm_engine *e, uint32_t ncopies, uint32_t reps, float *us_per_launch,
+                         uint64_t *bytes_per_launch);
+
 /* ---- device buffers (op-level tests and measurement) --------------------- */
 int lfm_dev_alloc(size_t nbytes, void **ptr);
 int lfm_dev_free(void *ptr);

@@ -1601,8 +1601,9 @@ extern "C" int lfm_device_name(const lfm_engine *e, char *buf, size_t cap)
 // Average duration of the routed gate/up kernel (the largest share of a decode
 // step): one graph of `reps` rounds over every MoE layer's weights (their 4
 // routed experts, > 256 MB in total, so the Infinity Cache cannot hold them),
-// timed with HIP events on the engine stream.  Routing uses the router logits
-// of the last decode step.
+// timed with HIP events on the engine stream.  The kernel is the one the
+// decode step runs (with the fused router, k_gateup4f over the router partial
+// sums of the last step; else k_gateup4 over the last router logits).
 extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *us_per_launch,
                                           uint64_t *bytes_per_launch)
 {
@@ -1620,10 +1621,19 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
     hipGraphExec_t ge = nullptr;
     HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
     int rc = LFM_OK;
+    const bool fused = fused_router(e, hp.dense_lead);
     for (uint32_t r = 0; r < reps && rc == LFM_OK; ++r)
         for (uint32_t l = hp.dense_lead; l < hp.n_layers && rc == LFM_OK; ++l) {
             GateUpArgs a = moe_gateup_args(e, l);
-            rc = launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, a);
+            if (fused) {
+                a.route.logits = nullptr;
+                a.route.rpart = e->rpart;
+                const Shape &sh = e->K->gateup;
+                rc = launch_t(e->K->gateup_f, dim3(sh.grid(hp.n_used * hp.expert_ff)), sh.threads(),
+                              0, e->stream, a);
+            } else {
+                rc = launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, a);
+            }
         }
     hipError_t ce = hipStreamEndCapture(e->stream, &g);
     if (rc != LFM_OK || ce != hipSuccess) {
@@ -1650,9 +1660,88 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
     (void)hipGraphExecDestroy(ge);
     e->dispatches += 2ull * reps * nmoe;
     *us_per_launch = ms * 1e3f / (float)(reps * nmoe);
+    // weights + input and norm weight + router inputs (partial sums, or logits)
+    // and bias + output
     const uint64_t wbytes = 2ull * hp.n_used * hp.expert_ff * (hp.dim / 256) * 210;
-    *bytes_per_launch = wbytes + 2ull * hp.dim * 4 + 2ull * hp.n_expert * 4 +
+    const uint64_t rbytes = fused ? (uint64_t)(ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4 : hp.n_expert * 4ull;
+    *bytes_per_launch = wbytes + 2ull * hp.dim * 4 + rbytes + hp.n_expert * 4ull +
                         (uint64_t)hp.n_used * hp.expert_ff * 4;
+    return LFM_OK;
+}
+
+// Average duration of the final-norm + tied-head kernel (k_head*, the largest
+// single matvec of a step: vocab x dim Q6_K) over one graph of `reps` rounds
+// that rotate `ncopies` copies of the embedding planes (ncopies x 110 MB at the
+// model's shape, beyond the 256 MB Infinity Cache from 3 copies on).
+extern "C" int lfm_engine_time_head(lfm_engine *e, uint32_t ncopies, uint32_t reps,
+                                    float *us_per_launch, uint64_t *bytes_per_launch)
+{
+    RC(need_final(e));
+    if (!us_per_launch || !bytes_per_launch || reps == 0 || ncopies == 0 || ncopies > 8)
+        return fail(LFM_EINVAL, "bad arguments");
+    const Q6T emb = q6(e, "token_embd.weight");
+    const size_t nbytes = (size_t)emb.rows * emb.nb * 210;
+    std::vector<uint8_t *> copies(ncopies, nullptr);
+    copies[0] = const_cast<uint8_t *>(emb.base);
+    int rc = LFM_OK;
+    for (uint32_t i = 1; i < ncopies && rc == LFM_OK; ++i) {
+        if (hipMalloc(&copies[i], nbytes) != hipSuccess ||
+            hipMemcpyAsync(copies[i], emb.base, nbytes, hipMemcpyDeviceToDevice, e->stream) != hipSuccess)
+            rc = fail(LFM_EDEVICE, "head copies: %zu bytes", nbytes);
+    }
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    float ms = 0.f;
+    if (rc == LFM_OK) {
+        rc = set_state(e, 0, 0, 0, 0xFFFFFFFFu);
+        if (rc == LFM_OK && hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+            rc = fail(LFM_EDEVICE, "capture begin");
+        if (rc == LFM_OK) {
+            for (uint32_t r = 0; r < reps && rc == LFM_OK; ++r)
+                for (uint32_t i = 0; i < ncopies && rc == LFM_OK; ++i) {
+                    HeadArgs h;
+                    h.emb = emb;
+                    h.emb.base = copies[i];
+                    h.src = xsrc(e->x, f32(e, "token_embd_norm.weight"), e->hp.eps);
+                    h.logits = e->logits;
+                    h.partial = e->hpart;
+                    h.vocab = e->hp.vocab;
+                    h.st = e->st;
+                    rc = launch_t(e->K->head.fn(), dim3(e->head_grid), e->K->head.threads(), 0,
+                                  e->stream, h);
+                }
+            hipError_t ce = hipStreamEndCapture(e->stream, &g);
+            if (rc == LFM_OK && ce != hipSuccess)
+                rc = fail(LFM_EDEVICE, "capture: %s", hipGetErrorString(ce));
+        }
+        if (rc == LFM_OK && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess)
+            rc = fail(LFM_EDEVICE, "hipGraphInstantiate");
+        if (g)
+            (void)hipGraphDestroy(g);
+        if (rc == LFM_OK) {
+            hipEvent_t e0 = nullptr, e1 = nullptr;
+            if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
+                hipGraphLaunch(ge, e->stream) != hipSuccess || hipEventRecord(e0, e->stream) != hipSuccess ||
+                hipGraphLaunch(ge, e->stream) != hipSuccess || hipEventRecord(e1, e->stream) != hipSuccess ||
+                hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+                rc = fail(LFM_EDEVICE, "head timing");
+            if (e0)
+                (void)hipEventDestroy(e0);
+            if (e1)
+                (void)hipEventDestroy(e1);
+        }
+        if (ge)
+            (void)hipGraphExecDestroy(ge);
+    }
+    (void)hipStreamSynchronize(e->stream);
+    for (uint32_t i = 1; i < ncopies; ++i)
+        if (copies[i])
+            (void)hipFree(copies[i]);
+    RC(rc);
+    e->dispatches += 2ull * reps * ncopies;
+    *us_per_launch = ms * 1e3f / (float)(reps * ncopies);
+    // weights + input vector + norm weight + logits + partials
+    *bytes_per_launch = nbytes + 2ull * e->hp.dim * 4 + (uint64_t)e->hp.vocab * 4 + e->head_grid * 8ull;
     return LFM_OK;
 }
 

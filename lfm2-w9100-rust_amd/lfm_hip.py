@@ -124,6 +124,7 @@ def lib():
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
         "lfm_engine_time_moe_gateup": (i32, [P, u32, pf32, C.POINTER(u64)]),
+        "lfm_engine_time_head": (i32, [P, u32, u32, pf32, C.POINTER(u64)]),
         "lfm_dev_alloc": (i32, [sz, C.POINTER(P)]), "lfm_dev_free": (i32, [P]),
         "lfm_memcpy_htod": (i32, [P, P, sz]), "lfm_memcpy_dtoh": (i32, [P, P, sz]),
         "lfm_dev_synchronize": (i32, []),
@@ -474,6 +475,13 @@ class GpuEngine:
         _check(lib().lfm_engine_time_moe_gateup(self._e, reps, C.byref(us), C.byref(nb)))
         return us.value, nb.value
 
+
+    def time_head(self, ncopies: int = 3, reps: int = 5):
+        """Mean k_head duration (us) and its algorithmic bytes, over `ncopies`
+        rotating copies of the embedding planes."""
+        us, nb = C.c_float(0), C.c_uint64(0)
+        _check(lib().lfm_engine_time_head(self._e, ncopies, reps, C.byref(us), C.byref(nb)))
+        return us.value, nb.value
     def close(self):
         if self._e:
             lib().lfm_engine_destroy(self._e)
