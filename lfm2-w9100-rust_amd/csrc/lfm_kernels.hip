@@ -139,6 +139,7 @@ __device__ __forceinline__ void keep_issued() { asm volatile("" ::: "memory"); }
 
 struct XRaw {
     float4 x0, x1, w0, w1;
+    uint32_t tok; // embedding input: DevState::tok, loaded first
 };
 
 // Issues the loads of this thread's 8 values (positions 8t .. 8t+7).  The
@@ -147,8 +148,11 @@ struct XRaw {
 // compiler's wait counts unknown at the join, after which waiting for one
 // early load also waits for every load issued after it.  Threads past n and
 // the embedding case (x_out is then the residual buffer) load stand-ins.
-__device__ __forceinline__ void x_issue(const XSrc &s, uint32_t n, XRaw &r)
+template <bool EMB = false>
+__device__ __forceinline__ void x_issue(const XSrc &s, uint32_t n, const DevState *st, XRaw &r)
 {
+    if constexpr (EMB)
+        r.tok = __hip_atomic_load(&st->tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t k = min(threadIdx.x * 8, n - 8);
     const float *xp = s.embed ? s.x_out : s.x;
     const float *wp = s.norm_w ? s.norm_w : xp;
@@ -170,44 +174,53 @@ __device__ __forceinline__ float x_stage(const XSrc &s, uint32_t n, const DevSta
 {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float ss = 0.f;
-    if (EMB && s.embed) {
-        const uint32_t b = lane >> 3, c = lane & 7;
-        if (wave == 0 && b < n / 256) {
-            float v[32];
-            lane_dequant(load_lane(s.emb, st->tok, b, c), v);
-            const bool writer = blockIdx.x == 0 && s.x_out != nullptr;
+    const uint32_t k = tid * 8;
+    float v[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+    if constexpr (EMB) {
+        // The step's input is the embedding row of DevState::tok (lfm.rs:310-320):
+        // wave 0 dequantizes it into xs, then every thread takes its 8 values
+        // from there as in the plain case (workgroup 0 also stores the residual).
+        if (wave == 0) {
+            const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane((int)r.tok);
+            const uint32_t b = lane >> 3, c = lane & 7;
+            if (b < n / 256) {
+                float e32[32];
+                lane_dequant(load_lane(s.emb, row, b, c), e32);
 #pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4)
+                for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t pos = lane_pos(b, c, s4, i);
-                    const float val = v[s4 * 8 + i];
-                    if (writer)
-                        s.x_out[pos] = val;
-                    ss += val * val;
-                    xs[pos] = s.norm_w ? val * s.norm_w[pos] : val;
-                }
-        }
-    } else {
-        const uint32_t k = tid * 8;
-        if (k < n) {
-            const float v[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
-            float o[8];
-            if (s.norm_w) {
-                const float w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    ss += v[i] * v[i];
-                    o[i] = v[i] * w[i];
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    o[i] = v[i];
+                    for (int i = 0; i < 8; ++i)
+                        xs[lane_pos(b, c, s4, i)] = e32[s4 * 8 + i];
             }
-            *reinterpret_cast<float4 *>(xs + k) = make_float4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<float4 *>(xs + k + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
+        __syncthreads();
+        if (k < n) {
+            const float4 a = *reinterpret_cast<const float4 *>(xs + k);
+            const float4 bb = *reinterpret_cast<const float4 *>(xs + k + 4);
+            v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+            v[4] = bb.x, v[5] = bb.y, v[6] = bb.z, v[7] = bb.w;
+            if (blockIdx.x == 0 && s.x_out != nullptr) {
+                *reinterpret_cast<float4 *>(s.x_out + k) = a;
+                *reinterpret_cast<float4 *>(s.x_out + k + 4) = bb;
+            }
+        }
+    }
+    if (k < n) {
+        float o[8];
+        if (s.norm_w) {
+            const float w[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ss += v[i] * v[i];
+                o[i] = v[i] * w[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                o[i] = v[i];
+        }
+        *reinterpret_cast<float4 *>(xs + k) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4 *>(xs + k + 4) = make_float4(o[4], o[5], o[6], o[7]);
     }
     if (s.norm_w) {
         ss = wave_sum(ss);
@@ -304,7 +317,7 @@ __device__ __forceinline__ void q6_matvec_body(const MatvecArgs &a)
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave, rows = a.w.rows;
     auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c(a.w, r, b, c); };
     XRaw raw;
-    x_issue(a.src, a.in_dim, raw);
+    x_issue(a.src, a.in_dim, a.st, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
     // mode 1: the rows' old values are loaded with the weights, not after the dot
@@ -363,7 +376,7 @@ extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(
     const bool active = b < a.w.nb;
     const uint32_t r = blockIdx.x * ROUTE_ROWS + wave;
     XRaw raw;
-    x_issue(a.src, a.in_dim, raw);
+    x_issue(a.src, a.in_dim, a.st, raw);
     ISSUE_ORDER();
     const Lane w = load_lane_c(a.w, r, b, c);
     const float yold = a.y[r + vzero()];
@@ -495,7 +508,7 @@ __device__ __forceinline__ void conv_inproj_body(const ConvInprojArgs &a)
         it.l[2] = load_lane_c(a.w, 2 * dim + ch, b, c);
     };
     XRaw raw;
-    x_issue(a.src, dim, raw);
+    x_issue<EMB>(a.src, dim, a.st, raw);
     Item<3> buf[G];
     fill_items(buf, first, W, dim, load);
     ConvCh cv[G];
@@ -577,7 +590,7 @@ __device__ __forceinline__ void qkv_body(const QkvArgs &a)
     const uint32_t rows = a.dim + 2 * a.hdkv, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = qkv_lane(a, r, b, c); };
     XRaw raw;
-    x_issue(a.src, a.dim, raw);
+    x_issue<EMB>(a.src, a.dim, a.st, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
     keep_issued();
@@ -951,7 +964,7 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     }
     RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
     XRaw raw;
-    x_issue(a.src, n, raw);
+    x_issue(a.src, n, a.st, raw);
     if constexpr (FUSED) {
         float f[NK + 1];
 #pragma unroll
@@ -1179,7 +1192,7 @@ __device__ __forceinline__ void head_body(const HeadArgs &a)
     const uint32_t rows = a.vocab, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c(a.emb, r, b, c); };
     XRaw raw;
-    x_issue(a.src, a.emb.nb * 256, raw);
+    x_issue(a.src, a.emb.nb * 256, a.st, raw);
     Item<1> buf[G];
     fill_items(buf, first, W, rows, load);
     keep_issued();
