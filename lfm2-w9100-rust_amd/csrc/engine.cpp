@@ -92,7 +92,7 @@ struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
         swiglu_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
-    hipFunction_t matvec_ks, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
+    hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
@@ -183,7 +183,7 @@ static int get_kernels(Kernels **out)
         hipFunction_t *f;
         const char *name;
     } fns[] = {{&k->matvec.f4, "k_q6_matvec4"},   {&k->matvec.f16, "k_q6_matvec16"},
-               {&k->matvec_ks, "k_q6_matvec_ks"}, {&k->conv.f4, "k_conv_inproj4"},
+               {&k->matvec_long, "k_q6_matvec_long"}, {&k->conv.f4, "k_conv_inproj4"},
                {&k->conv.f16, "k_conv_inproj16"}, {&k->qkv.f4, "k_qkv4"},
                {&k->qkv.f16, "k_qkv16"},          {&k->attn, "k_attn"},
                {&k->conv.f4e, "k_conv_inproj4e"}, {&k->conv.f16e, "k_conv_inproj16e"},
@@ -359,36 +359,27 @@ extern "C" int lfm_dev_synchronize(void)
     return LFM_OK;
 }
 
-// Matvec launch geometry: ksplit waves per row (1, 2 or 4), nbw blocks per wave.
-static int matvec_geometry(uint32_t nb, uint32_t *ks, uint32_t *nbw)
+// Matvec input widths: 1..32 blocks (256..8192 inputs).
+static int matvec_check(uint32_t nb)
 {
     if (nb == 0 || nb > 32)
         return fail(LFM_EINVAL, "Q6_K matvec supports 256..8192 inputs (got %u blocks)", nb);
-    uint32_t k = (nb + 7) / 8;
-    if (k == 3)
-        k = 4;
-    *ks = k;
-    *nbw = (nb + k - 1) / k;
     return LFM_OK;
 }
 
-static uint32_t matvec_grid(uint32_t rows, uint32_t ks)
-{
-    const uint32_t rpi = 4 / ks;
-    const uint32_t groups = (rows + rpi - 1) / rpi;
-    return std::max(1u, std::min(groups, 65535u));
-}
-
 // Launches y = W x (mode 0) or y += W x (mode 1): the one-wave-per-row kernel for
-// rows of up to 8 blocks, the split-row kernel for longer rows.
+// rows of up to 8 blocks, the 16-wave split-row kernel for longer rows.
 static int launch_matvec(Kernels *K, MatvecArgs &m, hipStream_t s)
 {
     if (!m.st)
         m.st = K->idle_st;
+    RC(matvec_check(m.w.nb));
     if (m.w.nb <= 8)
         return launch_shape(K->matvec, m.w.rows, s, m);
-    RC(matvec_geometry(m.w.nb, &m.ksplit, &m.nbw));
-    return launch(K->matvec_ks, dim3(matvec_grid(m.w.rows, m.ksplit)), (m.in_dim + 16) * 4, s, m);
+    const uint32_t grid = (m.w.rows + LONG_ROWS - 1) / LONG_ROWS;
+    if (grid > 0x7FFFFFFFu)
+        return fail(LFM_EINVAL, "too many rows");
+    return launch_t(K->matvec_long, dim3(grid), 1024, 0, s, m);
 }
 
 static Q6T q6view(const void *dev, uint64_t rows, uint64_t in_dim)
@@ -425,7 +416,7 @@ extern "C" int lfm_q6k_dequant(const void *packed, uint64_t rows, uint64_t in_di
 }
 
 static int matvec_args(const void *packed, uint64_t rows, uint64_t in_dim, const float *x, float *y,
-                       MatvecArgs *a, uint32_t *grid)
+                       MatvecArgs *a)
 {
     RC(check_q6_args(packed, rows, in_dim));
     memset(a, 0, sizeof(*a));
@@ -434,17 +425,14 @@ static int matvec_args(const void *packed, uint64_t rows, uint64_t in_dim, const
     a->y = y;
     a->in_dim = (uint32_t)in_dim;
     a->mode = 0;
-    RC(matvec_geometry(a->w.nb, &a->ksplit, &a->nbw));
-    *grid = matvec_grid(a->w.rows, a->ksplit);
-    return LFM_OK;
+    return matvec_check(a->w.nb);
 }
 
 extern "C" int lfm_q6k_matvec(const void *packed, uint64_t rows, uint64_t in_dim, const float *x,
                               float *y, void *stream)
 {
     MatvecArgs a;
-    uint32_t grid;
-    RC(matvec_args(packed, rows, in_dim, x, y, &a, &grid));
+    RC(matvec_args(packed, rows, in_dim, x, y, &a));
     Kernels *K;
     RC(get_kernels(&K));
     RC(launch_matvec(K, a, (hipStream_t)stream));
@@ -502,8 +490,7 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
     if (ncopies == 0 || iters == 0 || !ms)
         return fail(LFM_EINVAL, "ncopies, iters must be positive and ms non-null");
     MatvecArgs a;
-    uint32_t grid;
-    RC(matvec_args(packed, rows, in_dim, x, y, &a, &grid));
+    RC(matvec_args(packed, rows, in_dim, x, y, &a));
     Kernels *K;
     RC(get_kernels(&K));
     hipStream_t s;

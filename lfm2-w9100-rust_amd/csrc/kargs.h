@@ -43,14 +43,15 @@ struct XSrc {
     float *x_out;        // embed: workgroup 0 writes x here (the residual)
 };
 
+// Rows per workgroup of the long-row matvec (k_q6_matvec_long).
+#define LONG_ROWS 8
+
 struct MatvecArgs {      // y = W x  (mode 0)  or  y += W x  (mode 1)
     Q6T w;
     XSrc src;
     float *y;
     uint32_t in_dim;
     uint32_t mode;
-    uint32_t ksplit;     // k_q6_matvec_ks: waves per row (1, 2 or 4)
-    uint32_t nbw;        // k_q6_matvec_ks: blocks per wave
     DevState *st;        // nullable
 };
 

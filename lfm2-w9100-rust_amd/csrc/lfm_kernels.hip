@@ -408,56 +408,57 @@ extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(
 // Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
 // `ksplit` waves share a row (nbw blocks each); x staged in LDS; partials
 // combined in wave order.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_q6_matvec_ks(const MatvecArgs a)
+// Q6_K matvec for rows of 9..32 blocks (2304..8192 inputs): a workgroup of 16
+// waves owns LONG_ROWS rows; wave w takes K-chunk kc = w % 4 (blocks
+// kc*nbw .. +nbw, nbw = ceil(nb / 4) <= 8) of rows r0 + w/4 and r0 + w/4 + 4.
+// The input is staged once per workgroup; the first row's weights are issued
+// before the staging and the second row's after it (a full load queue would
+// otherwise stall the waves before the staging barrier).  Per row
+//   y = ((p0 + p1) + p2) + p3   (mode 0)   or   y += that   (mode 1).
+extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec_long(const MatvecArgs a)
 {
-    if (a.st && a.st->halt)
+    const uint32_t halted = load_halt(a.st);
+    __shared__ __attribute__((aligned(16))) float xs[4 * XS_MAX];
+    __shared__ float psh[LONG_ROWS][4];
+    const uint32_t tid = threadIdx.x, wave = wave_index(), lane = tid & 63;
+    const uint32_t kc = wave & 3, slot = wave >> 2;
+    const uint32_t bl = lane >> 3, c = lane & 7;
+    const uint32_t nbw = (a.w.nb + 3) / 4, b = kc * nbw + bl;
+    const bool active = bl < nbw && b < a.w.nb;
+    const uint32_t rows = a.w.rows, r0 = blockIdx.x * LONG_ROWS;
+    const uint32_t n = a.in_dim; // = nb * 256 <= 4 * XS_MAX
+    const uint32_t i0 = tid * 4, i1 = i0 + 1024 * 4;
+    const float4 xv0 = *reinterpret_cast<const float4 *>(a.src.x + min(i0, n - 4));
+    const float4 xv1 = *reinterpret_cast<const float4 *>(a.src.x + min(i1, n - 4));
+    const uint32_t ry = min(r0 + (tid & (LONG_ROWS - 1)), rows - 1);
+    const float yold = a.y[ry];
+    const uint32_t bb = min(b, a.w.nb - 1);
+    Item<1> buf[2];
+    buf[0].l[0] = load_lane(a.w, min(r0 + slot, rows - 1), bb, c);
+    keep_issued();
+    if (halted)
         return;
-    extern __shared__ float smem[];
-    float *xs = smem;
-    float *red = smem + a.in_dim;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t ks = a.ksplit, rpi = 4 / ks;
-    const uint32_t slot = wave / ks, kp = wave % ks;
-    const uint32_t bslot = lane >> 3, c = lane & 7;
-    const uint32_t b = kp * a.nbw + bslot;
-    const bool active = bslot < a.nbw && b < a.w.nb;
-    const uint32_t rows = a.w.rows;
-    const uint32_t ngroups = (rows + rpi - 1) / rpi;
-    uint32_t g = blockIdx.x;
-    Lane cur;
-    if (active && g < ngroups && g * rpi + slot < rows)
-        cur = load_lane(a.w, g * rpi + slot, b, c);
-    const bool owner = kp == 0 && lane == 0 && a.mode;
-    float yold = (owner && g < ngroups && g * rpi + slot < rows) ? a.y[g * rpi + slot] : 0.f;
-    for (uint32_t i = tid * 4; i < a.in_dim; i += WG_THREADS * 4)
-        *reinterpret_cast<float4 *>(xs + i) = *reinterpret_cast<const float4 *>(a.src.x + i);
+    if (i0 < n)
+        *reinterpret_cast<float4 *>(xs + i0) = xv0;
+    if (i1 < n)
+        *reinterpret_cast<float4 *>(xs + i1) = xv1;
     __syncthreads();
+    buf[1].l[0] = load_lane(a.w, min(r0 + slot + 4, rows - 1), bb, c);
     LaneX X;
-    if (active)
-        load_lanex(X, xs, b, c);
-    else
-        zero_lanex(X);
-    for (; g < ngroups; g += gridDim.x) {
-        const uint32_t row = g * rpi + slot;
-        const uint32_t gn = g + gridDim.x, rown = gn * rpi + slot;
-        Lane nxt;
-        if (active && gn < ngroups && rown < rows)
-            nxt = load_lane(a.w, rown, b, c);
-        const float ynxt = (owner && gn < ngroups && rown < rows) ? a.y[rown] : 0.f;
-        float p = (active && row < rows) ? lane_dot(cur, X) : 0.f;
-        p = wave_sum(p);
-        if (lane == 0)
-            red[wave] = p;
-        __syncthreads();
-        if (kp == 0 && lane == 0 && row < rows) {
-            float s = 0.f;
-            for (uint32_t k = 0; k < ks; ++k)
-                s += red[slot * ks + k];
-            a.y[row] = a.mode ? yold + s : s;
-        }
-        __syncthreads();
-        cur = nxt;
-        yold = ynxt;
+    lanex_lds(X, xs, b, c, active);
+    float p[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+        p[g] = active ? lane_dot(buf[g].l[0], X) : 0.f;
+    wave_sum_n<2>(p);
+    if (lane == 0) {
+        psh[slot][kc] = p[0];
+        psh[slot + 4][kc] = p[1];
+    }
+    __syncthreads();
+    if (tid < LONG_ROWS && r0 + tid < rows) {
+        const float s = ((psh[tid][0] + psh[tid][1]) + psh[tid][2]) + psh[tid][3];
+        a.y[r0 + tid] = a.mode ? yold + s : s;
     }
 }
 
