@@ -29,7 +29,7 @@ import lfm_hip  # noqa: E402
 METRIC = "decode tok/s (bs=1, ctx 4096) + Q6_K matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
-# HBM bytes per k_gateup4f launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
+# HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
 # WRITE_SIZE x 1.0, scales from a plain 512 MiB copy), profiles/k_gateup_traffic.md
 GATEUP_TRAFFIC_BYTES = 24929364
 SEED = 0x9E3779B97F4A7C15
@@ -193,18 +193,18 @@ def main():
     roof = None
     extra = {}
     if not args.no_roofline:
-        # dominant kernel of the decode step: routed MoE gate/up (k_gateup4f, router
+        # dominant kernel of the decode step: routed MoE gate/up (k_gateup8f, router
         # fused), timed with HIP events over a graph of its launches across all 22
         # MoE layers' experts
         us, nbytes = eng.time_moe_gateup(reps=10)
         gbs = nbytes / (us * 1e-6) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
-                "kernel": "k_gateup4f (MoE router total + top-4 + routed gate+up+SwiGLU, "
+                "kernel": "k_gateup8f (MoE router total + top-4 + routed gate+up+SwiGLU, "
                           "4 experts x 2 x 1792x2048 Q6_K)",
                 "algorithmic_bytes": nbytes, "us_per_launch": round(us, 3),
                 "timing": "HIP events over a graph of 220 launches (launch gaps included)"}
-        log(f"[bench] k_gateup4f (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
+        log(f"[bench] k_gateup8f (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
         # largest single Q6_K matvec of a step: final norm + tied head (vocab x 2048),
         # over 3 rotating copies of the embedding planes (beyond the Infinity Cache)
         hus, hbytes = eng.time_head(ncopies=3, reps=5)

@@ -194,7 +194,7 @@ static int get_kernels(Kernels **out)
                {&k->head.f16, "k_head16"},        {&k->argmax, "k_argmax"},
                {&k->argmax_final, "k_argmax_final"}, {&k->advance, "k_advance"},
                {&k->dequant, "k_q6_dequant"},    {&k->copy, "k_copy"},
-               {&k->matvec_route, "k_q6_matvec_route"}, {&k->gateup_f, "k_gateup4f"}};
+               {&k->matvec_route, "k_q6_matvec_route"}, {&k->gateup_f, "k_gateup8f"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -805,13 +805,12 @@ static XSrc xsrc(const float *x, const float *norm, float eps)
 }
 
 // The router of MoE layer l is fused into the output projection before it and
-// the gate/up kernel (k_q6_matvec_route + k_gateup4f) at the model's shape:
-// 32 experts, width ROUTE_ROWS * ROUTE_PARTS, 4-wave gate/up workgroups.
+// the gate/up kernel (k_q6_matvec_route + k_gateup8f) at the model's shape:
+// 32 experts, width ROUTE_WIDTH.
 static bool fused_router(const lfm_engine *e, uint32_t l)
 {
     const lfm_hparams &hp = e->hp;
-    return l >= hp.dense_lead && hp.n_expert == ROUTE_EXPERTS && hp.dim == ROUTE_WIDTH &&
-           e->K->gateup.nw == 4;
+    return l >= hp.dense_lead && hp.n_expert == ROUTE_EXPERTS && hp.dim == ROUTE_WIDTH;
 }
 
 // Output projection of layer l's mixer (y += W x); with the fused router it
@@ -830,6 +829,13 @@ static int launch_out_proj(lfm_engine *e, uint32_t l, MatvecArgs &m, bool fuse)
     ra.rnorm = f32(e, "blk.%u.ffn_norm.weight", l);
     ra.rpart = e->rpart;
     return launch_t(e->K->matvec_route, dim3(ROUTE_PARTS), 64 * ROUTE_ROWS, 0, e->stream, ra);
+}
+
+// Fused-router gate/up (k_gateup8f): 8-wave workgroups, 2 (rank, row) items per wave.
+static int launch_gateup_fused(lfm_engine *e, const GateUpArgs &g)
+{
+    const uint32_t items = e->hp.n_used * e->hp.expert_ff;
+    return launch_t(e->K->gateup_f, dim3((items + 15) / 16), 512, 0, e->stream, g);
 }
 
 static int enq_mixer(lfm_engine *e, uint32_t l, bool embed, bool fuse)
@@ -960,9 +966,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
     if (fused) {
         g.route.logits = nullptr;
         g.route.rpart = e->rpart;
-        const Shape &sh = e->K->gateup;
-        RC(launch_t(e->K->gateup_f, dim3(sh.grid(hp.n_used * hp.expert_ff)), sh.threads(), 0,
-                    e->stream, g));
+        RC(launch_gateup_fused(e, g));
     } else {
         RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));
     }
@@ -1589,7 +1593,7 @@ extern "C" int lfm_device_name(const lfm_engine *e, char *buf, size_t cap)
 // step): one graph of `reps` rounds over every MoE layer's weights (their 4
 // routed experts, > 256 MB in total, so the Infinity Cache cannot hold them),
 // timed with HIP events on the engine stream.  The kernel is the one the
-// decode step runs (with the fused router, k_gateup4f over the router partial
+// decode step runs (with the fused router, k_gateup8f over the router partial
 // sums of the last step; else k_gateup4 over the last router logits).
 extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *us_per_launch,
                                           uint64_t *bytes_per_launch)
@@ -1615,9 +1619,7 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
             if (fused) {
                 a.route.logits = nullptr;
                 a.route.rpart = e->rpart;
-                const Shape &sh = e->K->gateup;
-                rc = launch_t(e->K->gateup_f, dim3(sh.grid(hp.n_used * hp.expert_ff)), sh.threads(),
-                              0, e->stream, a);
+                rc = launch_gateup_fused(e, a);
             } else {
                 rc = launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, a);
             }

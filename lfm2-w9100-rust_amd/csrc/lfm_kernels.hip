@@ -363,7 +363,7 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArg
 // (row r) loads R[e][r] for e = lane % 32 and w_norm[r] with its weights; once
 // its y[r] is known, lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32
 // y[r]^2, and wave 0 adds the workgroup's rows in order, leaving the partials
-// column-major in rpart for k_gateup4f.  The grid is exactly rows / ROUTE_ROWS.
+// column-major in rpart for k_gateup8f.  The grid is exactly rows / ROUTE_ROWS.
 extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(const MatvecRouteArgs ra)
 {
     const MatvecArgs &a = ra.m;
@@ -938,7 +938,7 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 template <int NW, int G, bool FUSED>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
-    static_assert(!FUSED || NW == 4, "the fused router reduction assumes 256 threads");
+    static_assert(!FUSED || NW == 4 || NW == 8 || NW == 16, "fused router: 4, 8 or 16 waves");
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
@@ -951,16 +951,16 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     const uint32_t ff = a.ff, total = (routed ? a.route.n_used : 1u) * ff;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
     // router partial sums: column e (ROUTE_PARTS floats) holds QC float4; thread
-    // t loads float4 t + 256k of the 32 expert columns and float4 t % QC of the
-    // x^2 column
-    constexpr int QC = ROUTE_PARTS / 4, NK = ROUTE_EXPERTS * QC / 256;
+    // t loads float4 t + 64*NW*k of the 32 expert columns and float4 t % QC of
+    // the x^2 column
+    constexpr int QC = ROUTE_PARTS / 4, NK = ROUTE_EXPERTS * QC / (64 * NW);
     static_assert(QC == 32 || QC == 64, "a column is a half wave or a wave of float4");
     float4 pv[NK + 1];
     if constexpr (FUSED) {
         const float4 *pp = reinterpret_cast<const float4 *>(a.route.rpart);
 #pragma unroll
         for (int k = 0; k < NK; ++k)
-            pv[k] = pp[threadIdx.x + 256 * k];
+            pv[k] = pp[threadIdx.x + 64 * NW * k];
         pv[NK] = pp[ROUTE_EXPERTS * QC + (threadIdx.x & (QC - 1))];
     }
     RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
@@ -976,7 +976,7 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
             if ((lane & 31) == 31) {
 #pragma unroll
                 for (int k = 0; k < NK; ++k)
-                    rsum[wave * 2 + (lane >> 5) + 8 * k] = f[k];
+                    rsum[wave * 2 + (lane >> 5) + 2 * NW * k] = f[k];
                 if (threadIdx.x == 31)
                     rsum[ROUTE_EXPERTS] = f[NK];
             }
@@ -985,7 +985,7 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
             if (lane == 0) {
 #pragma unroll
                 for (int k = 0; k < NK; ++k)
-                    rsum[wave + 4 * k] = f[k];
+                    rsum[wave + NW * k] = f[k];
                 if (threadIdx.x == 0)
                     rsum[ROUTE_EXPERTS] = f[NK];
             }
@@ -1061,9 +1061,11 @@ extern "C" __global__ __launch_bounds__(1024) void k_gateup16(const GateUpArgs a
 {
     gateup_body<16, 2, false>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void k_gateup4f(const GateUpArgs a)
+// Fused router: 8-wave workgroups (measured best against 4 and 16: half the
+// per-workgroup partial-sum and input reads of 4 waves, while 16 leave CUs idle).
+extern "C" __global__ __launch_bounds__(512) void k_gateup8f(const GateUpArgs a)
 {
-    gateup_body<4, 2, true>(a);
+    gateup_body<8, 2, true>(a);
 }
 
 // Routed down projections and combine (lfm.rs:660-668, resident.rs:101-117).
