@@ -39,6 +39,7 @@ extern "C" {
 #define LFM_EDEVICE 3   /* HIP runtime or device failure                          */
 #define LFM_ESTATE 4    /* call not valid in the engine's current state           */
 #define LFM_EINTERNAL 5 /* library bug                                            */
+#define LFM_ENOTFOUND 6 /* metadata key or tensor name not present in a GGUF file  */
 
 #define LFM_GGML_TYPE_F32 0u
 #define LFM_GGML_TYPE_Q6_K 14u
@@ -73,6 +74,9 @@ const char *lfm_last_error(void);
 const char *lfm_version(void);
 /* Number of visible HIP devices (0 when none). */
 int lfm_device_count(int *count);
+/* Free and total device memory in bytes; replaces the sysfs mem_info_vram_*
+ * reads of bin/api_stream.rs:43-47 (co-resident headroom check). */
+int lfm_device_mem_info(int device, uint64_t *free_bytes, uint64_t *total_bytes);
 
 /* ---- engine lifecycle ---------------------------------------------------- */
 /* GpuEngine::load (gpu_lfm.rs:51-115) is split into create / upload / finalize
@@ -230,6 +234,111 @@ int lfm_synth_normal_f32(uint64_t seed, const char *stream, uint64_t n, float me
                          float sigma, float *out, int threads);
 /* Generate every tensor of the model and upload it (convenience for benches). */
 int lfm_engine_load_synthetic(lfm_engine *e, const lfm_synth_opts *o, int threads);
+
+/* ---- GGUF v3 model files --------------------------------------------------
+ * Reader: parser/src/gguf.rs:299-440 (parse: header, metadata, tensor infos and
+ * every check it makes) and engine/src/model_file.rs:30-186 (ModelFile: tensor
+ * table with absolute offsets, positioned tensor reads, typed metadata access).
+ * A handle is read-only after open and may be shared between threads. */
+#define LFM_GGUF_TYPE_U8 0u
+#define LFM_GGUF_TYPE_I8 1u
+#define LFM_GGUF_TYPE_U16 2u
+#define LFM_GGUF_TYPE_I16 3u
+#define LFM_GGUF_TYPE_U32 4u
+#define LFM_GGUF_TYPE_I32 5u
+#define LFM_GGUF_TYPE_F32 6u
+#define LFM_GGUF_TYPE_BOOL 7u
+#define LFM_GGUF_TYPE_STRING 8u
+#define LFM_GGUF_TYPE_ARRAY 9u
+#define LFM_GGUF_TYPE_U64 10u
+#define LFM_GGUF_TYPE_I64 11u
+#define LFM_GGUF_TYPE_F64 12u
+#define LFM_GGUF_MAX_DIMS 8
+
+typedef struct lfm_gguf lfm_gguf;
+/* parser::gguf::TensorInfo (gguf.rs:58-70) + model_file::TensorInfo (model_file.rs:7-14). */
+typedef struct lfm_gguf_tensor {
+    const char *name;     /* valid until lfm_gguf_close                          */
+    uint32_t ggml_type;   /* 0 = F32, 14 = Q6_K, ...                             */
+    uint32_t n_dims;
+    uint64_t ne[LFM_GGUF_MAX_DIMS]; /* GGUF order: ne[0] is the row length       */
+    uint64_t offset;      /* as stored: relative to the data section             */
+    uint64_t file_offset; /* absolute: data_offset + offset                      */
+    uint64_t nbytes;
+} lfm_gguf_tensor;
+/* One metadata value (parser::gguf::Value, gguf.rs:40-55). */
+typedef struct lfm_gguf_value {
+    uint32_t type;      /* LFM_GGUF_TYPE_*                                        */
+    uint32_t elem_type; /* ARRAY: type of every element                           */
+    uint64_t u64;       /* U8, U16, U32, U64, BOOL                                */
+    int64_t i64;        /* I8, I16, I32, I64                                      */
+    double f64;         /* F32, F64                                               */
+    const char *str;    /* STRING: UTF-8 bytes, NUL-terminated, valid until close */
+    uint64_t len;       /* STRING: byte length; ARRAY: element count              */
+} lfm_gguf_value;
+
+int lfm_gguf_open(const char *path, lfm_gguf **out);               /* ModelFile::open     */
+int lfm_gguf_parse_memory(const void *data, size_t len, lfm_gguf **out); /* gguf::parse  */
+void lfm_gguf_close(lfm_gguf *g);
+int lfm_gguf_header(const lfm_gguf *g, uint32_t *version, uint32_t *alignment,
+                    uint64_t *data_offset, uint64_t *n_kv, uint64_t *n_tensors);
+/* Keys in byte-wise order (the reference's BTreeMap); index < n_kv. */
+int lfm_gguf_meta_key(const lfm_gguf *g, uint64_t index, const char **key);
+int lfm_gguf_meta_get(const lfm_gguf *g, const char *key, lfm_gguf_value *out);
+int lfm_gguf_meta_array_get(const lfm_gguf *g, const char *key, uint64_t index,
+                            lfm_gguf_value *out);
+/* Typed accessors with the reference's conversions (model_file.rs:131-182). */
+int lfm_gguf_meta_u32(const lfm_gguf *g, const char *key, uint32_t *out);
+int lfm_gguf_meta_f32(const lfm_gguf *g, const char *key, float *out);
+int lfm_gguf_meta_str(const lfm_gguf *g, const char *key, char *buf, size_t cap, size_t *len);
+int lfm_gguf_meta_u32_array(const lfm_gguf *g, const char *key, uint32_t *out, size_t cap,
+                            size_t *len);
+int lfm_gguf_tensor_info(const lfm_gguf *g, uint64_t index, lfm_gguf_tensor *out);
+int lfm_gguf_find_tensor(const lfm_gguf *g, const char *name, uint64_t *index); /* tensor() */
+/* read_tensor_into (model_file.rs:100-109): len must equal the tensor's nbytes. */
+int lfm_gguf_read_tensor(const lfm_gguf *g, const char *name, void *dst, size_t len);
+int lfm_gguf_read_tensor_range(const lfm_gguf *g, const char *name, uint64_t byte_off,
+                               void *dst, uint64_t len); /* model_file.rs:111-122 */
+/* load_hyperparams (engine/src/lfm.rs:102-145).  strict != 0 also requires the
+ * reference's fixed geometry (dim 2048, 32 heads, 24 layers, vocab 128000,
+ * 32 experts, top-4, expert_ff 1792), as the reference always does. */
+int lfm_gguf_hparams(const lfm_gguf *g, int strict, lfm_hparams *out);
+/* GpuEngine::load's staging loop (gpu_lfm.rs:64-97): uploads every F32 and Q6_K
+ * tensor of the file; call before lfm_engine_finalize. */
+int lfm_engine_load_gguf(lfm_engine *e, const lfm_gguf *g);
+/* ModelFile::open + GpuEngine::load + set_ctx (gpu_lfm.rs:51-120): a finalized
+ * engine; ctx 0 keeps the default 4096. */
+int lfm_engine_open_gguf(const char *path, int device, uint32_t ctx, int strict,
+                         lfm_engine **out);
+
+/* Writer (no counterpart in the reference, whose tests build GGUF bytes by hand,
+ * gguf.rs:450-553): metadata and tensor table first, then begin() writes the
+ * header, then each tensor's bytes, then finish().  Key "general.alignment" (U32,
+ * a power of two) sets the data alignment, default 32. */
+typedef struct lfm_gguf_writer lfm_gguf_writer;
+int lfm_gguf_writer_create(lfm_gguf_writer **out);
+void lfm_gguf_writer_free(lfm_gguf_writer *w);
+/* Scalar types only; value points to the little-endian value (BOOL: one byte 0/1). */
+int lfm_gguf_writer_set_scalar(lfm_gguf_writer *w, const char *key, uint32_t type,
+                               const void *value);
+int lfm_gguf_writer_set_string(lfm_gguf_writer *w, const char *key, const char *s, uint64_t len);
+int lfm_gguf_writer_set_array(lfm_gguf_writer *w, const char *key, uint32_t elem_type,
+                              const void *values, uint64_t count);
+/* lens may be NULL for NUL-terminated strings. */
+int lfm_gguf_writer_set_string_array(lfm_gguf_writer *w, const char *key,
+                                     const char *const *strs, const uint64_t *lens,
+                                     uint64_t count);
+/* The lfm2moe.* keys load_hyperparams reads, plus general.architecture. */
+int lfm_gguf_writer_set_hparams(lfm_gguf_writer *w, const lfm_hparams *hp);
+int lfm_gguf_writer_add_tensor(lfm_gguf_writer *w, const char *name, uint32_t ggml_type,
+                               uint32_t n_dims, const uint64_t *ne, uint64_t *index);
+int lfm_gguf_writer_begin(lfm_gguf_writer *w, const char *path);
+int lfm_gguf_writer_write_tensor(lfm_gguf_writer *w, uint64_t index, const void *data,
+                                 uint64_t nbytes);
+int lfm_gguf_writer_finish(lfm_gguf_writer *w);
+/* The seeded synthetic model as a GGUF file (o NULL = default options). */
+int lfm_gguf_write_synthetic(const char *path, const lfm_hparams *hp, const lfm_synth_opts *o,
+                             int threads);
 
 /* ---- binary16 helpers (IEEE RNE) ------------------------------------------ */
 uint16_t lfm_f32_to_f16(float f);

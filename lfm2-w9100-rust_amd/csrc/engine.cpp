@@ -24,18 +24,16 @@
 #include <vector>
 
 #include "../../include/lfm_hip.h"
+#include "host_err.h"
 #include "kargs.h"
 
 // ------------------------------------------------------------------ errors
 static thread_local std::string g_err;
 
-static int fail(int code, const char *fmt, ...)
+int lfm_vfail(int code, const char *fmt, va_list ap)
 {
     char buf[1024];
-    va_list ap;
-    va_start(ap, fmt);
     vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
     g_err = buf;
     return code;
 }
@@ -65,6 +63,23 @@ extern "C" int lfm_device_count(int *count)
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
     *count = e == hipSuccess ? n : 0;
+    return LFM_OK;
+}
+
+extern "C" int lfm_device_mem_info(int device, uint64_t *free_bytes, uint64_t *total_bytes)
+{
+    if (!free_bytes || !total_bytes)
+        return fail(LFM_EINVAL, "null argument");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(LFM_EDEVICE, "no HIP device available");
+    if (device < 0 || device >= n)
+        return fail(LFM_EINVAL, "device %d out of range (%d devices)", device, n);
+    HIPCHK(hipSetDevice(device));
+    size_t free_b = 0, total_b = 0;
+    HIPCHK(hipMemGetInfo(&free_b, &total_b));
+    *free_bytes = free_b;
+    *total_bytes = total_b;
     return LFM_OK;
 }
 

@@ -20,7 +20,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblfm_hip.so")
 CODE_OBJECT_PATH = os.path.join(_HERE, "lfm_kernels.hsaco")
 
-LFM_OK, LFM_EINVAL, LFM_ERANGE, LFM_EDEVICE, LFM_ESTATE, LFM_EINTERNAL = range(6)
+LFM_OK, LFM_EINVAL, LFM_ERANGE, LFM_EDEVICE, LFM_ESTATE, LFM_EINTERNAL, LFM_ENOTFOUND = range(7)
 GGML_TYPE_F32 = 0
 GGML_TYPE_Q6_K = 14
 MAX_LAYERS = 64
@@ -68,6 +68,33 @@ class SynthOpts(C.Structure):
     _fields_ = [
         ("seed", C.c_uint64), ("d_sigma", C.c_float), ("norm_sigma", C.c_float),
         ("router_sigma", C.c_float), ("bias_sigma", C.c_float), ("conv_sigma", C.c_float),
+    ]
+
+
+(GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL, GGUF_STRING,
+ GGUF_ARRAY, GGUF_U64, GGUF_I64, GGUF_F64) = range(13)
+GGUF_MAX_DIMS = 8
+
+
+class GgufTensorInfo(C.Structure):
+    """``lfm_gguf_tensor``: parser::gguf::TensorInfo (gguf.rs:58-70) with the
+    absolute offset of model_file::TensorInfo (model_file.rs:7-14)."""
+
+    _fields_ = [
+        ("name", C.c_char_p), ("ggml_type", C.c_uint32), ("n_dims", C.c_uint32),
+        ("ne", C.c_uint64 * GGUF_MAX_DIMS), ("offset", C.c_uint64), ("file_offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+    ]
+
+    @property
+    def shape(self):
+        return tuple(int(self.ne[i]) for i in range(self.n_dims))
+
+
+class GgufValue(C.Structure):
+    _fields_ = [
+        ("type", C.c_uint32), ("elem_type", C.c_uint32), ("u64", C.c_uint64), ("i64", C.c_int64),
+        ("f64", C.c_double), ("str", C.c_void_p), ("len", C.c_uint64),
     ]
 
 
@@ -145,6 +172,39 @@ def lib():
         "lfm_synth_normal_f32": (i32, [u64, C.c_char_p, u64, f32, f32, P, i32]),
         "lfm_engine_load_synthetic": (i32, [P, C.POINTER(SynthOpts), i32]),
         "lfm_f32_to_f16": (C.c_uint16, [f32]), "lfm_f16_to_f32": (f32, [C.c_uint16]),
+        "lfm_gguf_open": (i32, [C.c_char_p, C.POINTER(P)]),
+        "lfm_gguf_parse_memory": (i32, [P, sz, C.POINTER(P)]),
+        "lfm_gguf_close": (None, [P]),
+        "lfm_gguf_header": (i32, [P, pu32, pu32, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+        "lfm_gguf_meta_key": (i32, [P, u64, C.POINTER(C.c_char_p)]),
+        "lfm_gguf_meta_get": (i32, [P, C.c_char_p, C.POINTER(GgufValue)]),
+        "lfm_gguf_meta_array_get": (i32, [P, C.c_char_p, u64, C.POINTER(GgufValue)]),
+        "lfm_gguf_meta_u32": (i32, [P, C.c_char_p, pu32]),
+        "lfm_gguf_meta_f32": (i32, [P, C.c_char_p, pf32]),
+        "lfm_gguf_meta_str": (i32, [P, C.c_char_p, C.c_char_p, sz, C.POINTER(sz)]),
+        "lfm_gguf_meta_u32_array": (i32, [P, C.c_char_p, pu32, sz, C.POINTER(sz)]),
+        "lfm_gguf_tensor_info": (i32, [P, u64, C.POINTER(GgufTensorInfo)]),
+        "lfm_gguf_find_tensor": (i32, [P, C.c_char_p, C.POINTER(u64)]),
+        "lfm_gguf_read_tensor": (i32, [P, C.c_char_p, P, sz]),
+        "lfm_gguf_read_tensor_range": (i32, [P, C.c_char_p, u64, P, u64]),
+        "lfm_gguf_hparams": (i32, [P, i32, C.POINTER(Hparams)]),
+        "lfm_engine_load_gguf": (i32, [P, P]),
+        "lfm_engine_open_gguf": (i32, [C.c_char_p, i32, u32, i32, C.POINTER(P)]),
+        "lfm_gguf_writer_create": (i32, [C.POINTER(P)]),
+        "lfm_gguf_writer_free": (None, [P]),
+        "lfm_gguf_writer_set_scalar": (i32, [P, C.c_char_p, u32, P]),
+        "lfm_gguf_writer_set_string": (i32, [P, C.c_char_p, C.c_char_p, u64]),
+        "lfm_gguf_writer_set_array": (i32, [P, C.c_char_p, u32, P, u64]),
+        "lfm_gguf_writer_set_string_array": (i32, [P, C.c_char_p, C.POINTER(C.c_char_p),
+                                                   C.POINTER(u64), u64]),
+        "lfm_gguf_writer_set_hparams": (i32, [P, C.POINTER(Hparams)]),
+        "lfm_gguf_writer_add_tensor": (i32, [P, C.c_char_p, u32, u32, C.POINTER(u64),
+                                             C.POINTER(u64)]),
+        "lfm_gguf_writer_begin": (i32, [P, C.c_char_p]),
+        "lfm_gguf_writer_write_tensor": (i32, [P, u64, P, u64]),
+        "lfm_gguf_writer_finish": (i32, [P]),
+        "lfm_gguf_write_synthetic": (i32, [C.c_char_p, C.POINTER(Hparams), C.POINTER(SynthOpts),
+                                           i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -223,6 +283,237 @@ def synth_normal(seed: int, stream: str, n: int, mean: float = 0.0, sigma: float
 
 def f32_to_f16_bits(x: float) -> int:
     return int(lib().lfm_f32_to_f16(x))
+
+
+# ------------------------------------------------------------------ GGUF files
+_GGUF_SCALAR = {GGUF_U8: np.uint8, GGUF_I8: np.int8, GGUF_U16: np.uint16, GGUF_I16: np.int16,
+                GGUF_U32: np.uint32, GGUF_I32: np.int32, GGUF_F32: np.float32,
+                GGUF_BOOL: np.uint8, GGUF_U64: np.uint64, GGUF_I64: np.int64,
+                GGUF_F64: np.float64}
+_GGUF_UNSIGNED = (GGUF_U8, GGUF_U16, GGUF_U32, GGUF_U64)
+_GGUF_SIGNED = (GGUF_I8, GGUF_I16, GGUF_I32, GGUF_I64)
+
+
+def _gguf_scalar(v: GgufValue):
+    if v.type in _GGUF_UNSIGNED:
+        return int(v.u64)
+    if v.type in _GGUF_SIGNED:
+        return int(v.i64)
+    if v.type == GGUF_BOOL:
+        return bool(v.u64)
+    if v.type in (GGUF_F32, GGUF_F64):
+        return float(v.f64)
+    if v.type == GGUF_STRING:
+        return C.string_at(v.str, v.len).decode()
+    raise LfmError(LFM_EINTERNAL, f"unexpected GGUF value type {v.type}")
+
+
+class GgufFile:
+    """A parsed GGUF v3 file: the reference's ModelFile (engine/src/model_file.rs:30-186)
+    over parser::gguf::parse (parser/src/gguf.rs:299-440), parsed by the C++ reader."""
+
+    def __init__(self, handle: C.c_void_p):
+        self._g = handle
+        ver, al = C.c_uint32(), C.c_uint32()
+        off, nkv, nt = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        _check(lib().lfm_gguf_header(self._g, C.byref(ver), C.byref(al), C.byref(off),
+                                     C.byref(nkv), C.byref(nt)))
+        self.version, self.alignment, self.data_offset = ver.value, al.value, off.value
+        self.n_kv, self.n_tensors = nkv.value, nt.value
+
+    @classmethod
+    def open(cls, path: str) -> "GgufFile":
+        g = C.c_void_p()
+        _check(lib().lfm_gguf_open(os.fsencode(path), C.byref(g)))
+        return cls(g)
+
+    @classmethod
+    def parse(cls, data: bytes) -> "GgufFile":
+        g = C.c_void_p()
+        buf = C.create_string_buffer(bytes(data), len(data)) if data else None
+        _check(lib().lfm_gguf_parse_memory(buf, len(data), C.byref(g)))
+        return cls(g)
+
+    def keys(self) -> List[str]:
+        k = C.c_char_p()
+        out = []
+        for i in range(self.n_kv):
+            _check(lib().lfm_gguf_meta_key(self._g, i, C.byref(k)))
+            out.append(k.value.decode())
+        return out
+
+    def value_type(self, key: str) -> int:
+        v = GgufValue()
+        _check(lib().lfm_gguf_meta_get(self._g, key.encode(), C.byref(v)))
+        return int(v.type)
+
+    def get(self, key: str):
+        """A metadata value as Python: int, float, bool, str or a list of those."""
+        v = GgufValue()
+        _check(lib().lfm_gguf_meta_get(self._g, key.encode(), C.byref(v)))
+        if v.type != GGUF_ARRAY:
+            return _gguf_scalar(v)
+        return [self._element(key, i) for i in range(v.len)]
+
+    def _element(self, key: str, i: int):
+        e = GgufValue()
+        _check(lib().lfm_gguf_meta_array_get(self._g, key.encode(), i, C.byref(e)))
+        if e.type == GGUF_ARRAY:
+            raise LfmError(LFM_EINVAL, f"{key}[{i}]: nested arrays are read with the C API")
+        return _gguf_scalar(e)
+
+    @property
+    def metadata(self) -> dict:
+        return {k: self.get(k) for k in self.keys()}
+
+    def meta_u32(self, key: str) -> int:
+        out = C.c_uint32()
+        _check(lib().lfm_gguf_meta_u32(self._g, key.encode(), C.byref(out)))
+        return out.value
+
+    def meta_f32(self, key: str) -> float:
+        out = C.c_float()
+        _check(lib().lfm_gguf_meta_f32(self._g, key.encode(), C.byref(out)))
+        return out.value
+
+    def meta_str(self, key: str) -> str:
+        n = C.c_size_t()
+        rc = lib().lfm_gguf_meta_str(self._g, key.encode(), None, 0, C.byref(n))
+        if rc not in (LFM_OK, LFM_ERANGE):
+            _check(rc)
+        buf = C.create_string_buffer(n.value + 1)
+        _check(lib().lfm_gguf_meta_str(self._g, key.encode(), buf, n.value + 1, C.byref(n)))
+        return buf.raw[:n.value].decode()
+
+    def meta_u32_array(self, key: str) -> List[int]:
+        n = C.c_size_t()
+        rc = lib().lfm_gguf_meta_u32_array(self._g, key.encode(), None, 0, C.byref(n))
+        if rc not in (LFM_OK, LFM_ERANGE):
+            _check(rc)
+        out = np.zeros(max(n.value, 1), dtype=np.uint32)
+        _check(lib().lfm_gguf_meta_u32_array(self._g, key.encode(), _u32p(out), n.value,
+                                             C.byref(n)))
+        return [int(x) for x in out[:n.value]]
+
+    def tensor_info(self, index: int) -> GgufTensorInfo:
+        t = GgufTensorInfo()
+        _check(lib().lfm_gguf_tensor_info(self._g, index, C.byref(t)))
+        return t
+
+    @property
+    def tensors(self) -> List[GgufTensorInfo]:
+        return [self.tensor_info(i) for i in range(self.n_tensors)]
+
+    def tensor(self, name: str) -> GgufTensorInfo:
+        i = C.c_uint64()
+        _check(lib().lfm_gguf_find_tensor(self._g, name.encode(), C.byref(i)))
+        return self.tensor_info(i.value)
+
+    def has_tensor(self, name: str) -> bool:
+        i = C.c_uint64()
+        return lib().lfm_gguf_find_tensor(self._g, name.encode(), C.byref(i)) == LFM_OK
+
+    def read_tensor(self, name: str) -> np.ndarray:
+        """The tensor's raw bytes (read_tensor_into)."""
+        out = np.empty(self.tensor(name).nbytes, dtype=np.uint8)
+        _check(lib().lfm_gguf_read_tensor(self._g, name.encode(), out.ctypes.data, out.nbytes))
+        return out
+
+    def read_tensor_range(self, name: str, byte_off: int, length: int) -> np.ndarray:
+        out = np.empty(length, dtype=np.uint8)
+        _check(lib().lfm_gguf_read_tensor_range(self._g, name.encode(), byte_off,
+                                                out.ctypes.data, length))
+        return out
+
+    def hparams(self, strict: bool = True) -> Hparams:
+        """load_hyperparams (engine/src/lfm.rs:102-145)."""
+        hp = Hparams()
+        _check(lib().lfm_gguf_hparams(self._g, int(strict), C.byref(hp)))
+        return hp
+
+    def close(self):
+        if self._g:
+            lib().lfm_gguf_close(self._g)
+            self._g = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GgufWriter:
+    """Streaming GGUF v3 writer: metadata and tensor table, then ``begin(path)``,
+    each tensor's bytes, then ``finish()``."""
+
+    def __init__(self):
+        self._w = C.c_void_p()
+        _check(lib().lfm_gguf_writer_create(C.byref(self._w)))
+
+    def set_scalar(self, key: str, type_: int, value):
+        a = np.array([value], dtype=_GGUF_SCALAR[type_])
+        _check(lib().lfm_gguf_writer_set_scalar(self._w, key.encode(), type_, a.ctypes.data))
+
+    def set_string(self, key: str, value: str):
+        b = value.encode()
+        _check(lib().lfm_gguf_writer_set_string(self._w, key.encode(), b, len(b)))
+
+    def set_array(self, key: str, elem_type: int, values):
+        if elem_type == GGUF_STRING:
+            bs = [v.encode() for v in values]
+            arr = (C.c_char_p * max(len(bs), 1))(*bs)
+            lens = (C.c_uint64 * max(len(bs), 1))(*[len(b) for b in bs])
+            _check(lib().lfm_gguf_writer_set_string_array(self._w, key.encode(), arr, lens,
+                                                          len(bs)))
+            return
+        a = np.ascontiguousarray(np.array(values, dtype=_GGUF_SCALAR[elem_type]))
+        _check(lib().lfm_gguf_writer_set_array(self._w, key.encode(), elem_type, a.ctypes.data,
+                                               a.size))
+
+    def set_hparams(self, hp: Hparams):
+        _check(lib().lfm_gguf_writer_set_hparams(self._w, C.byref(hp)))
+
+    def add_tensor(self, name: str, ggml_type: int, shape: Sequence[int]) -> int:
+        ne = (C.c_uint64 * GGUF_MAX_DIMS)(*[int(x) for x in shape])
+        idx = C.c_uint64()
+        _check(lib().lfm_gguf_writer_add_tensor(self._w, name.encode(), ggml_type, len(shape), ne,
+                                                C.byref(idx)))
+        return idx.value
+
+    def begin(self, path: str):
+        _check(lib().lfm_gguf_writer_begin(self._w, os.fsencode(path)))
+
+    def write_tensor(self, index: int, data: np.ndarray):
+        data = np.ascontiguousarray(data)
+        _check(lib().lfm_gguf_writer_write_tensor(self._w, index, data.ctypes.data, data.nbytes))
+
+    def finish(self):
+        _check(lib().lfm_gguf_writer_finish(self._w))
+
+    def close(self):
+        if self._w:
+            lib().lfm_gguf_writer_free(self._w)
+            self._w = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def write_synthetic_gguf(path: str, hp: Hparams, opts: Optional[SynthOpts] = None,
+                         threads: int = 8):
+    """The seeded synthetic model as a GGUF file."""
+    _check(lib().lfm_gguf_write_synthetic(os.fsencode(path), C.byref(hp),
+                                          C.byref(opts) if opts else None, threads))
 
 
 # ------------------------------------------------------------------ device buffers
@@ -376,6 +667,25 @@ class GpuEngine:
         _check(lib().lfm_engine_load_synthetic(e._e, C.byref(o), threads))
         e.finalize()
         return e
+
+    @classmethod
+    def from_gguf(cls, path: str, device: int = 0, ctx: int = MAX_CTX,
+                  strict: bool = True) -> "GpuEngine":
+        """ModelFile::open + GpuEngine::load (gpu_lfm.rs:51-120) in one call."""
+        h = C.c_void_p()
+        _check(lib().lfm_engine_open_gguf(os.fsencode(path), device, ctx, int(strict),
+                                          C.byref(h)))
+        e = cls.__new__(cls)
+        e._e = h
+        e.hp = Hparams()
+        _check(lib().lfm_engine_hparams(h, C.byref(e.hp)))
+        e.ctx = ctx
+        e._finalized = True
+        return e
+
+    def load_gguf(self, f: GgufFile):
+        """Upload every F32 and Q6_K tensor of an open file (before finalize)."""
+        _check(lib().lfm_engine_load_gguf(self._e, f._g))
 
     def upload_tensor(self, name: str, ggml_type: int, shape: Sequence[int], data: np.ndarray):
         data = np.ascontiguousarray(data)

@@ -145,6 +145,50 @@ def test_cfg4_reduced_token_loop(gpu, oracle, reduced_model):
     assert g2.forward_token([first], len(prompt)) == toks[0]
 
 
+def test_real_vocab_head_and_chunked_prefill(gpu, oracle):
+    """The real model's vocabulary (V = 128000, lfm.rs:117-125) through the tied
+    head and argmax, and a prompt prefilled in 64-token chunks (api_stream.rs:57-63,
+    work_bound.rs PREFILL_CHUNK) against the whole-prompt forward and the oracle."""
+    hp = gpu.make_hparams(dim=2048, heads=32, n_layers=2, attention_layers=(1,), kv=8,
+                          vocab=128000, eos=1 << 30, n_expert=32, n_used=4, expert_ff=1792,
+                          n_ff=7168, dense_lead=1)
+    tensors = model_tensors(hp, gpu.synth_opts(SEED, bias_sigma=0.1))
+    g = gpu_engine(hp, tensors, ctx=160)
+    o = oracle_engine(oracle, hp, tensors, ctx=160)
+    prompt = [int(t) for t in np.random.default_rng(9).integers(0, hp.vocab, 80)]
+    prompt[-1] = hp.vocab - 1
+    lg, lo = g.forward(prompt, 0), o.forward(prompt, 0)
+    assert lg.shape == (128000,)
+    err = rel_l2(lg, lo)
+    print(f"V=128000 prompt logits rel-L2 {err:.3e}")
+    assert err <= 1e-3
+    first = int(oracle.argmax(lg))
+    tol = 1e-3 * float(np.abs(lo).max())
+    if top2_margin(lo) > tol:
+        assert first == oracle.argmax(lo)
+    toks = g.decode_run(first, len(prompt), 6)
+    feed, clear = first, []
+    for s, t in enumerate(toks):
+        lo = o.forward([feed], len(prompt) + s)
+        clear.append(top2_margin(lo) > tol)
+        if clear[-1]:
+            assert t == oracle.argmax(lo), (s, t, oracle.argmax(lo))
+        feed = t
+    assert sum(clear) >= 3
+    # the same prompt in chunks of 64 and 16 tokens, then the same greedy tokens
+    g2 = gpu_engine(hp, tensors, ctx=160)
+    g2.forward_token(prompt[:64], 0)
+    nxt = g2.forward_token(prompt[64:], 64)
+    if top2_margin(lg) > tol:
+        assert nxt == first
+    feed = first
+    for s in range(len(toks)):
+        nxt = g2.forward_token([feed], len(prompt) + s)
+        if clear[s]:
+            assert nxt == toks[s], s
+        feed = toks[s]
+
+
 def test_engine_preconditions(gpu, reduced_model):
     hp, tensors = reduced_model
     g = gpu_engine(hp, tensors, ctx=64)
