@@ -29,9 +29,10 @@ import lfm_hip  # noqa: E402
 METRIC = "decode tok/s (bs=1, ctx 4096) + Q6_K matvec HBM GB/s vs ~8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
-# HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes (FETCH_SIZE x 2.0 +
-# WRITE_SIZE x 1.0, scales from a plain 512 MiB copy), profiles/k_gateup_traffic.md
-GATEUP_TRAFFIC_BYTES = 24929364
+# HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes over this bench
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the scales are what the two
+# counters read for a plain 512 MiB copy): 1.02 x the algorithmic 24 163 456 bytes.
+GATEUP_TRAFFIC_BYTES = 24659689
 SEED = 0x9E3779B97F4A7C15
 
 
