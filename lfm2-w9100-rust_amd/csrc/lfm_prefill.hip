@@ -589,17 +589,38 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_swiglu_split(const Sw
 }
 
 // Router logits for T tokens (lfm.rs:599-607): a workgroup takes 16 tokens.
-// Each wave first finds the RMSNorm scale of 4 of them; then 256-wide slices of
-// x . w and of the f32 router rows are staged in LDS and thread (token, e)
-// accumulates its dot products in k order; logits = inv * sum.
+// Each wave first finds the RMSNorm scale of 4 of them; then 128-wide slices of
+// x . w and of the f32 router rows are staged in LDS (rows padded by 4 floats,
+// so the 16-byte reads below are conflict-free) and thread (token tid / 16,
+// experts tid % 16 + 16 j) accumulates its dot products in k order, reading
+// four k at a time; logits = inv * sum.  NE = 2 covers up to 32 experts, 4 up
+// to 64.
 #define RT_TOK 16
-#define RT_K 256
+#define RT_K 128
+#define RT_PAD (RT_K + 4)
 #define RT_EMAX 64
+template <int NE>
+__device__ __forceinline__ void router_dots(const float *xr, const float *ws, uint32_t eg, float (&acc)[4])
+{
+#pragma unroll 4
+    for (uint32_t kk = 0; kk < RT_K; kk += 4) {
+        const float4 x4 = *reinterpret_cast<const float4 *>(xr + kk);
+#pragma unroll
+        for (int j = 0; j < NE; ++j) {
+            const float4 w4 = *reinterpret_cast<const float4 *>(ws + (eg + 16 * j) * RT_PAD + kk);
+            acc[j] = fmaf(x4.x, w4.x, acc[j]);
+            acc[j] = fmaf(x4.y, w4.y, acc[j]);
+            acc[j] = fmaf(x4.z, w4.z, acc[j]);
+            acc[j] = fmaf(x4.w, w4.w, acc[j]);
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const RouterPrefillArgs a)
 {
     __shared__ float inv[RT_TOK];
-    __shared__ float xs[RT_TOK][RT_K + 1];
-    __shared__ float ws[RT_EMAX][RT_K + 1];
+    __shared__ __attribute__((aligned(16))) float xs[RT_TOK * RT_PAD];
+    __shared__ __attribute__((aligned(16))) float ws[RT_EMAX * RT_PAD];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t t0 = blockIdx.x * RT_TOK;
     for (uint32_t j = 0; j < RT_TOK / 4; ++j) {
@@ -615,36 +636,42 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const 
         }
     }
     const uint32_t tt = tid / 16, eg = tid % 16;
-    float acc[RT_EMAX / 16];
-#pragma unroll
-    for (int j = 0; j < RT_EMAX / 16; ++j)
-        acc[j] = 0.f;
+    const bool wide = a.n_expert > 32;                     // uniform
+    const uint32_t wrows = wide ? RT_EMAX : 32;             // staged expert rows
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t k0 = 0; k0 < a.dim; k0 += RT_K) {
         __syncthreads();
-        for (uint32_t u = tid; u < RT_TOK * RT_K; u += WG_THREADS) {
-            const uint32_t r = u / RT_K, kk = u % RT_K, t = t0 + r;
-            xs[r][kk] = t < a.T ? a.x[(size_t)t * a.dim + k0 + kk] * a.norm_w[k0 + kk] : 0.f;
+        // 16 tokens x 128 floats of x . w: two float4 per thread
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint32_t u = tid + WG_THREADS * v, r = u / (RT_K / 4), kk = (u % (RT_K / 4)) * 4;
+            const uint32_t t = t0 + r;
+            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < a.T) {
+                const float4 x4 = *reinterpret_cast<const float4 *>(a.x + (size_t)t * a.dim + k0 + kk);
+                const float4 n4 = *reinterpret_cast<const float4 *>(a.norm_w + k0 + kk);
+                xv = make_float4(x4.x * n4.x, x4.y * n4.y, x4.z * n4.z, x4.w * n4.w);
+            }
+            *reinterpret_cast<float4 *>(&xs[r * RT_PAD + kk]) = xv;
         }
-        for (uint32_t u = tid; u < a.n_expert * RT_K; u += WG_THREADS) {
-            const uint32_t e = u / RT_K, kk = u % RT_K;
-            ws[e][kk] = a.w[(size_t)e * a.dim + k0 + kk];
+        // wrows x 128 floats of the router rows (rows past n_expert are zero)
+        for (uint32_t u = tid; u < wrows * (RT_K / 4); u += WG_THREADS) {
+            const uint32_t e = u / (RT_K / 4), kk = (u % (RT_K / 4)) * 4;
+            float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (e < a.n_expert)
+                wv = *reinterpret_cast<const float4 *>(a.w + (size_t)e * a.dim + k0 + kk);
+            *reinterpret_cast<float4 *>(&ws[e * RT_PAD + kk]) = wv;
         }
         __syncthreads();
-#pragma unroll
-        for (int j = 0; j < RT_EMAX / 16; ++j) {
-            const uint32_t e = eg + 16 * j;
-            if (e < a.n_expert) {
-                float s = acc[j];
-                for (uint32_t kk = 0; kk < RT_K; ++kk)
-                    s += xs[tt][kk] * ws[e][kk];
-                acc[j] = s;
-            }
-        }
+        if (wide)
+            router_dots<4>(xs + tt * RT_PAD, ws, eg, acc);
+        else
+            router_dots<2>(xs + tt * RT_PAD, ws, eg, acc);
     }
     const uint32_t t = t0 + tt;
     if (t < a.T)
 #pragma unroll
-        for (int j = 0; j < RT_EMAX / 16; ++j) {
+        for (int j = 0; j < 4; ++j) {
             const uint32_t e = eg + 16 * j;
             if (e < a.n_expert)
                 a.logits[(size_t)t * a.n_expert + e] = inv[tt] * acc[j];
