@@ -783,13 +783,19 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     }
     HIPCHK(hipMalloc(&t.dev, want));
     t.nbytes = want;
+    hipError_t ce;
     if (type == LFM_GGML_TYPE_Q6_K) {
         std::vector<uint8_t> packed(want);
         pack_blocks((const uint8_t *)host, n / 256, packed.data());
-        HIPCHK(hipMemcpy(t.dev, packed.data(), want, hipMemcpyHostToDevice));
+        ce = hipMemcpy(t.dev, packed.data(), want, hipMemcpyHostToDevice);
         t.q6 = q6view(t.dev, n / ne[0], ne[0]);
     } else {
-        HIPCHK(hipMemcpy(t.dev, host, want, hipMemcpyHostToDevice));
+        ce = hipMemcpy(t.dev, host, want, hipMemcpyHostToDevice);
+    }
+    if (ce != hipSuccess) {
+        (void)hipFree(t.dev);
+        return fail(LFM_EDEVICE, "%s: upload of %zu bytes failed: %s", name, want,
+                    hipGetErrorString(ce));
     }
     e->tensors[name] = t;
     return LFM_OK;

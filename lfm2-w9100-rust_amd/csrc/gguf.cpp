@@ -12,6 +12,8 @@
 //   zero padding up to `alignment` = metadata "general.alignment" when it is a U32
 //   (a power of two), else 32; tensor data follows, tensor i at data_offset + offset_i,
 //   and every tensor must end inside the file.
+// Keys and tensor names are looked up through C strings, so one containing a NUL
+// byte is rejected (the reference accepts it; no real model file has one).
 // A string is a u64 byte length (<= 1 GiB) and UTF-8 bytes; an array is a u32
 // element type, a u64 count (<= 10 000 000) and the elements' payloads.
 #include <errno.h>
@@ -302,6 +304,14 @@ int read_value(Cursor &c, uint32_t type, Value *v, int depth)
     RC(c.u64(&n));
     if (n > kMaxArray)
         return fail(LFM_EINVAL, "array length %llu exceeds maximum (10 M)", (unsigned long long)n);
+    // Elements of a known type take at least `least` bytes each: a count the rest
+    // of the file cannot hold is the truncation it would end in, found before
+    // building n values.
+    size_t least = 0;
+    if (!scalar_size(v->elem, &least))
+        least = v->elem == LFM_GGUF_TYPE_STRING ? 8 : v->elem == LFM_GGUF_TYPE_ARRAY ? 12 : 0;
+    if (least && n > c.left() / least)
+        return fail(LFM_EINVAL, "unexpected end of file (truncated input)");
     v->a.reserve((size_t)std::min<uint64_t>(n, 4096));
     for (uint64_t k = 0; k < n; ++k) {
         v->a.emplace_back();
@@ -438,6 +448,8 @@ static int parse(lfm_gguf *g)
         uint32_t type;
         Value v;
         RC(c.string(&key));
+        if (key.find('\0') != std::string::npos)
+            return fail(LFM_EINVAL, "metadata key contains a NUL byte (not addressable by name)");
         RC(c.u32(&type));
         RC(read_value(c, type, &v, 0));
         if (!g->meta.emplace(key, std::move(v)).second)
@@ -455,6 +467,8 @@ static int parse(lfm_gguf *g)
         TensorEntry t;
         uint32_t nd;
         RC(c.string(&t.name));
+        if (t.name.find('\0') != std::string::npos)
+            return fail(LFM_EINVAL, "tensor name contains a NUL byte (not addressable by name)");
         RC(c.u32(&nd));
         if (nd > kMaxDims)
             return fail(LFM_EINVAL, "too many dimensions: %u (max 8)", nd);

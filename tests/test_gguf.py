@@ -180,6 +180,8 @@ def test_bad_metadata_values():
     parse_err(build(meta=[("k", 8, b"\xc0\x80")]), "UTF-8")          # overlong NUL
     parse_err(build(meta=[("k", 8, b"\xed\xa0\x80")]), "UTF-8")      # surrogate
     parse_err(build(tensors=[("t", [1] * 9, 0, 0)]), "dimensions")
+    parse_err(build(meta=[("a\0b", 4, 1)]), "NUL")
+    parse_err(build(tensors=[("t\0", [4], 0, 0)]), "NUL")
     big_str = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", (1 << 30) + 1)
     parse_err(big_str, "1 GiB")
     big_arr = (b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + enc_str("k") +
