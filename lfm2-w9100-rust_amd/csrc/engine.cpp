@@ -537,7 +537,7 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
 // ------------------------------------------------------------------ MFMA GEMM
 #define GEMM_ROWS 256   // weight rows per GEMM workgroup
 #define GEMM_TOKENS 128 // token columns per GEMM workgroup
-#define GEMM_THREADS 512
+#define GEMM_THREADS 256 // 4 waves of 64 weight rows each
 static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz)
 {
     return dim3((rows + GEMM_ROWS - 1) / GEMM_ROWS, (ntok + GEMM_TOKENS - 1) / GEMM_TOKENS, nz);

@@ -3,10 +3,11 @@
 // Prefill is the one place the LFM2 token loop is a dense contraction: every
 // projection multiplies a Q6_K weight by T activation columns.  The GEMM here
 // runs on the matrix cores (v_mfma_f32_32x32x16_f16):
-//   * the weight tile is decoded in LDS to binary16 values sc * (q - 32), which
-//     are exact whenever |sc * (q - 32)| <= 2048 (and within 1/2 ulp otherwise);
-//   * the super-block scale d multiplies each 256-wide block's partial product
-//     in fp32 (one FMA per accumulator per block);
+//   * each wave decodes its weight rows in registers to binary16 values
+//     sc * (q - 32), which are exact whenever |sc * (q - 32)| <= 2048 (and within
+//     1/2 ulp otherwise), straight into the MFMA A operand;
+//   * the super-block scale d is applied in fp32 by rescaling the accumulators
+//     once per 256-wide block;
 //   * activations are split into binary16 hi + lo (x = hi + lo to ~22 bits), and
 //     both halves go through the matrix cores, so results are close to an fp32
 //     matvec (the reference's prefill is its f32 q6k_prompt path,
@@ -72,25 +73,15 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     }
 }
 
-#define TM 256 // weight rows per workgroup (8 waves: 4 along rows x 2 along tokens)
-#define TN 128 // token columns per workgroup
+#define TM 256 // weight rows per workgroup (4 waves of 64 rows)
+#define TN 128 // token columns per workgroup (each wave covers all of them)
 #define TK 64  // K elements per stage (a quarter Q6_K block)
+#define GEMM_NTH 256
 
-// LDS tiles are [row][64 halves] = 8 pieces of 16 B per row; piece p of row r
-// holds k-piece p ^ ((r >> 1) & 7), so the 16-B fragment reads of 16
-// consecutive rows fall in distinct banks.
+// Activation tiles are [token][64 halves] = 8 pieces of 16 B per token; piece p
+// of token row r holds k-piece p ^ ((r >> 1) & 7), so the 16-B fragment reads of
+// 16 consecutive tokens fall in distinct banks.
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kp) { return r * TK + ((kp ^ ((r >> 1) & 7)) << 3); }
-
-// Raw Q6_K bytes of a thread's two (row, l0 group) units for one half block,
-// and its B pieces (hi, lo) of one stage.
-struct ARaw {
-    uint4 ql0, ql1;
-    uint2 qh0, qh1;
-    uint32_t sc0, sc1;
-};
-struct BRaw {
-    uint4 h0, h1, l0, l1;
-};
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // Two codes c0, c1 (bytes 0, 1 or 2, 3 of `c`) -> half2 (c - 32) exactly: the
@@ -106,49 +97,72 @@ __device__ __forceinline__ half2v codes_hi(uint32_t c)
     return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1056.0f, (_Float16)1056.0f};
 }
 
-// 16 weights of one (row, l0 group) for quarter q of a half block, as binary16
-// sc * (q6 - 32) (exact while |sc * (q6 - 32)| <= 2048): positions j*32 + l0 + i
-// for j = 0, 1 (s = 2q + j), i.e. k-pieces 4j + cq of the stage.
-__device__ __forceinline__ void decode_unit(uint4 ql, uint2 qh, uint32_t sc, uint32_t q, uint32_t r,
-                                            uint32_t cq, _Float16 *A)
+// A lane's Q6_K bytes for one half block (128 weights) of one row: the chunks of
+// its two l0 groups (chunk c of the half block covers l0 in [8c', 8c' + 8) of
+// the ql / qh planes): 16 B of low bits, 8 B of high bits and the 4 scales.
+struct AChunk {
+    uint4 ql;
+    uint2 qh;
+    uint32_t sc;
+};
+
+// The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in
+// MFMA A-operand order, or zeros when the block scale d is zero.  Exact while
+// |sc * (q6 - 32)| <= 2048, within 1/2 ulp otherwise.
+__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool zero)
 {
+    const _Float16 scf = zero ? (_Float16)0.0f : (_Float16)(float)(int)(int8_t)(c.sc >> (8 * s));
+    const half2v sc2 = {scf, scf};
+    half2v o[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t s = 2 * q + j;
-        const _Float16 scf = (_Float16)(float)(int)(int8_t)(sc >> (8 * s));
-        const half2v sc2 = {scf, scf};
-        half2v o[4];
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const uint32_t Aw = w ? ql.y : ql.x, Bw = w ? ql.w : ql.z, H = w ? qh.y : qh.x;
-            uint32_t c;
-            if (q == 0)
-                c = j == 0 ? ((Aw & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u))
-                           : ((Bw & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u));
-            else
-                c = j == 0 ? (((Aw >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u))
-                           : (((Bw >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u));
-            o[2 * w] = codes_lo(c) * sc2;
-            o[2 * w + 1] = codes_hi(c) * sc2;
+    for (int w = 0; w < 2; ++w) {
+        const uint32_t Aw = w ? c.ql.y : c.ql.x, Bw = w ? c.ql.w : c.ql.z, H = w ? c.qh.y : c.qh.x;
+        uint32_t cc;
+        switch (s) {
+        case 0: cc = (Aw & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u); break;
+        case 1: cc = (Bw & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u); break;
+        case 2: cc = ((Aw >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u); break;
+        default: cc = ((Bw >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u); break;
         }
-        half8 v = {o[0][0], o[0][1], o[1][0], o[1][1], o[2][0], o[2][1], o[3][0], o[3][1]};
-        *reinterpret_cast<half8 *>(A + swz(r, 4 * j + cq)) = v;
+        o[2 * w] = codes_lo(cc) * sc2;
+        o[2 * w + 1] = codes_hi(cc) * sc2;
     }
+    return (half8){o[0][0], o[0][1], o[1][0], o[1][1], o[2][0], o[2][1], o[3][0], o[3][1]};
 }
 
 // C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, zrows) of group
 // z and token columns n < ntok.  Column n reads activation row (tok ? tok[n] :
-// n) and writes output row (slot ? slot[n] : n).  A workgroup computes 256 rows
-// x 128 tokens; each wave 64 x 64 with v_mfma_f32_32x32x16_f16 on the decoded
-// weights and the hi / lo activation halves.  K advances in 64-wide stages
-// through double-buffered LDS: while the matrix cores work on stage s, the
-// wave decodes stage s+1's weights and stores its activations, and the loads
-// for the stage after that are in flight (one barrier per stage).  Each Q6_K
-// block's partial product is scaled by its d in fp32.
-extern "C" __global__ __launch_bounds__(512) void k_gemm_q6(const GemmArgs a)
+// n) and writes output row (slot ? slot[n] : n).
+//
+// A workgroup computes 256 rows x 128 tokens; wave w owns rows 64w..64w+63 for
+// all 128 tokens (2 x 4 tiles of v_mfma_f32_32x32x16_f16, hi and lo activation
+// halves).  K advances in 64-wide stages:
+//   * weights never touch LDS: each lane loads its rows' Q6_K bytes one half
+//     block ahead into registers and decodes the MFMA A fragments itself, the
+//     next k-step's fragments while the current k-step's MFMAs run;
+//   * activation tiles go global -> LDS directly (global_load_lds_dwordx4),
+//     double-buffered, one barrier per stage;
+//   * the super-block scale d is folded into the accumulators: they hold
+//     sum_b d_b P_b / u with u the last nonzero d seen, so entering block b
+//     multiplies them by u / d_b (blocks with d = 0 contribute zero weights),
+//     and the epilogue multiplies by the final u.
+// Workgroup i runs on XCD i % 8; tiles are handed out so that each XCD takes a
+// contiguous run with the weight rows fastest, and the workgroups resident on
+// one XCD share activation tiles in its L2.
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6(const GemmArgs a)
 {
-    const uint32_t z = blockIdx.z;
-    const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TN;
+    uint32_t z, mx, ny;
+    {
+        const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+        const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+        const uint32_t q = total / 8, r = total % 8, xcd = L % 8, idx = L / 8;
+        const uint32_t V = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+        mx = V % gx;
+        ny = (V / gx) % gy;
+        z = V / (gx * gy);
+    }
+    const uint32_t m0 = mx * TM, n0 = ny * TN;
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
@@ -157,166 +171,164 @@ extern "C" __global__ __launch_bounds__(512) void k_gemm_q6(const GemmArgs a)
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
     const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][TM * TK];
     __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TN * TK];
     __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TN * TK];
-    __shared__ float dsh[2][TM];
+    __shared__ float dsh[2][TM], rsh[2][TM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t wm = (wave & 3) * 64, wn = (wave >> 2) * 64;
+    const uint32_t wm = wave * 64, p = lane >> 5, lr = lane & 31;
     const uint32_t nb = a.w.nb, K = nb * 256;
     const size_t nblk = (size_t)a.w.rows * nb;
-    // A units: unit u = tid + 512 v -> row u >> 2, l0 group u & 3
-    const uint32_t ar0 = tid >> 2, ar1 = (tid + 512) >> 2, acq = tid & 3;
-    const uint32_t arow0 = rbase + min(m0 + ar0, a.zrows - 1), arow1 = rbase + min(m0 + ar1, a.zrows - 1);
-    // B pieces: piece u = tid + 512 v -> token row u >> 3, k-piece u & 7
-    const uint32_t bkp = tid & 7, bn0 = tid >> 3, bn1 = (tid + 512) >> 3;
-    uint32_t bsrc0, bsrc1;
-    {
-        uint32_t col;
-        col = min(n0 + bn0, ntok - 1); bsrc0 = tokl ? tokl[col] : col;
-        col = min(n0 + bn1, ntok - 1); bsrc1 = tokl ? tokl[col] : col;
+    uint32_t arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        arow[i] = rbase + min(m0 + wm + i * 32 + lr, a.zrows - 1);
+    // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
+    // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
+    // k-piece j ^ ((t >> 1) & 7)
+    uint32_t bsrc[4], bkq[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const uint32_t t = (tid + GEMM_NTH * v) >> 3, col = min(n0 + t, ntok - 1);
+        bsrc[v] = tokl ? tokl[col] : col;
+        bkq[v] = ((tid & 7) ^ ((t >> 1) & 7)) * 8;
     }
-    auto loadA = [=](uint32_t half) -> ARaw {
-        ARaw R;
-        const uint32_t kb = half >> 1, c = (half & 1) * 4 + acq;
-        const size_t b0 = (size_t)arow0 * nb + kb, b1 = (size_t)arow1 * nb + kb;
-        R.ql0 = *reinterpret_cast<const uint4 *>(a.w.base + b0 * 128 + c * 16);
-        R.ql1 = *reinterpret_cast<const uint4 *>(a.w.base + b1 * 128 + c * 16);
-        R.qh0 = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + b0 * 64 + c * 8);
-        R.qh1 = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + b1 * 64 + c * 8);
-        R.sc0 = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + b0 * 16 + (c >> 1) * 4);
-        R.sc1 = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + b1 * 16 + (c >> 1) * 4);
-        return R;
+    auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) {
+        const uint32_t kb = half >> 1, h = half & 1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const size_t blk = (size_t)arow[i] * nb + kb;
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                const uint32_t c = 4 * h + 2 * ch + p;
+                A[i][ch].ql = *reinterpret_cast<const uint4 *>(a.w.base + blk * 128 + c * 16);
+                A[i][ch].qh = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + blk * 64 + c * 8);
+                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + blk * 16 + (c >> 1) * 4);
+            }
+        }
     };
-    auto loadB = [=](uint32_t st) -> BRaw {
-        BRaw R;
-        const size_t k = (size_t)st * TK + bkp * 8;
-        R.h0 = *reinterpret_cast<const uint4 *>(xh + (size_t)bsrc0 * K + k);
-        R.h1 = *reinterpret_cast<const uint4 *>(xh + (size_t)bsrc1 * K + k);
-        R.l0 = *reinterpret_cast<const uint4 *>(xl + (size_t)bsrc0 * K + k);
-        R.l1 = *reinterpret_cast<const uint4 *>(xl + (size_t)bsrc1 * K + k);
-        return R;
-    };
-    auto storeB = [&](const BRaw R, uint32_t buf) {
-        *reinterpret_cast<uint4 *>(&Bh[buf][swz(bn0, bkp)]) = R.h0;
-        *reinterpret_cast<uint4 *>(&Bh[buf][swz(bn1, bkp)]) = R.h1;
-        *reinterpret_cast<uint4 *>(&Bl[buf][swz(bn0, bkp)]) = R.l0;
-        *reinterpret_cast<uint4 *>(&Bl[buf][swz(bn1, bkp)]) = R.l1;
+    auto loadB = [&](uint32_t st) {
+        const uint32_t buf = st & 1;
+        const size_t k = (size_t)st * TK;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t u0 = (GEMM_NTH * v + 64 * wave) * 8;
+            __builtin_amdgcn_global_load_lds((const void *)(xh + (size_t)bsrc[v] * K + k + bkq[v]),
+                                             (__attribute__((address_space(3))) void *)&Bh[buf][u0], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(xl + (size_t)bsrc[v] * K + k + bkq[v]),
+                                             (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
+        }
     };
     auto loadD = [=](uint32_t kb) -> float {
-        if (tid >= TM)
-            return 0.f;
         const uint32_t row = rbase + min(m0 + tid, a.zrows - 1);
         return half_bits_to_float(reinterpret_cast<const uint16_t *>(a.w.base + nblk * 208)[(size_t)row * nb + kb]);
     };
-    auto decodeA = [&](const ARaw R, uint32_t q, uint32_t buf) {
-        decode_unit(R.ql0, R.qh0, R.sc0, q, ar0, acq, As[buf]);
-        decode_unit(R.ql1, R.qh1, R.sc1, q, ar1, acq, As[buf]);
-    };
-    floatx16 acc[2][2], tmp[2][2];
+    floatx16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-                acc[i][j][e] = 0.f, tmp[i][j][e] = 0.f;
-    auto mfma_half = [&](uint32_t buf, int ks0) {
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t kp = (ks0 + kk) * 2 + (lane >> 5);
-            half8 af[2], bfh[2], bfl[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(&As[buf][swz(wm + i * 32 + (lane & 31), kp)]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bfh[j] = *reinterpret_cast<const half8 *>(&Bh[buf][swz(wn + j * 32 + (lane & 31), kp)]);
-                bfl[j] = *reinterpret_cast<const half8 *>(&Bl[buf][swz(wn + j * 32 + (lane & 31), kp)]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfh[j], tmp[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], tmp[i][j], 0, 0, 0);
-        }
-    };
-    auto apply_d = [&](uint32_t db) {
+                acc[i][j][e] = 0.f;
+    auto rescale = [&](uint32_t rb) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t r = wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                const float d = dsh[db][r];
+                const float r = rsh[rb][wm + i * 32 + 8 * (e / 4) + 4 * p + (e % 4)];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[i][j][e] += d * tmp[i][j][e];
-                    tmp[i][j][e] = 0.f;
-                }
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j][e] *= r;
             }
     };
-    const uint32_t nstage = nb * 4;
-    ARaw R = loadA(0);
-    BRaw RB = loadB(0);
-    float dreg = loadD(0);
-    decodeA(R, 0, 0);
-    storeB(RB, 0);
-    if (tid < TM)
-        dsh[0][tid] = dreg;
+    // thread tid keeps row tid's running scale u (TM == GEMM_NTH)
+    float u = 1.0f;
+    auto set_d = [&](uint32_t slot, float d) {
+        dsh[slot][tid] = d;
+        const bool nz = d != 0.f;
+        rsh[slot][tid] = nz ? u / d : 1.0f;
+        u = nz ? d : u;
+    };
+    const uint32_t nst = nb * 4, nhb = nb * 2; // stages; half block hb = stages 2hb, 2hb + 1
+    AChunk A[2][2], An[2][2];
+    loadA(0, A);
+    loadB(0);
+    set_d(0, loadD(0));
+    __builtin_amdgcn_s_waitcnt(0);
+    loadB(1);
+    loadA(1, An);
+    float dnext = 0.f;
     __syncthreads();
-    RB = loadB(1);
-    for (uint32_t kb = 0; kb < nb; ++kb) {
-        const uint32_t s0 = kb * 4;
-        const bool more = kb + 1 < nb;
-        // t = 0: MFMA s0 (buf 0); next = half 2kb q1 -> buf 1 (R holds half 2kb)
-        mfma_half(0, 0);
-        decodeA(R, 1, 1);
-        storeB(RB, 1);
-        mfma_half(0, 2);
-        __syncthreads();
-        if (s0 + 2 < nstage)
-            RB = loadB(s0 + 2);
-        R = loadA(2 * kb + 1);
-        if (more)
-            dreg = loadD(kb + 1);
-        // t = 1: MFMA s0+1 (buf 1); next = half 2kb+1 q0 -> buf 0
-        mfma_half(1, 0);
-        decodeA(R, 0, 0);
-        storeB(RB, 0);
-        mfma_half(1, 2);
-        __syncthreads();
-        if (s0 + 3 < nstage)
-            RB = loadB(s0 + 3);
-        // t = 2: MFMA s0+2 (buf 0); next = half 2kb+1 q1 -> buf 1
-        mfma_half(0, 0);
-        decodeA(R, 1, 1);
-        storeB(RB, 1);
-        mfma_half(0, 2);
-        __syncthreads();
-        if (s0 + 4 < nstage)
-            RB = loadB(s0 + 4);
-        if (more)
-            R = loadA(2 * kb + 2);
-        // t = 3: MFMA s0+3 (buf 1); next = half 2kb+2 q0 -> buf 0 (unused after the last block)
-        mfma_half(1, 0);
-        decodeA(R, 0, 0);
-        storeB(RB, 0);
-        if (tid < TM)
-            dsh[(kb + 1) & 1][tid] = dreg;
-        mfma_half(1, 2);
-        apply_d(kb & 1);
-        __syncthreads();
-        if (s0 + 5 < nstage)
-            RB = loadB(s0 + 5);
-    }
+    for (uint32_t hb = 0; hb < nhb; ++hb) {
+        const uint32_t db = (hb >> 1) & 1;
+        if ((hb & 1) == 0 && hb > 0)
+            rescale(db);
+        if ((hb & 1) == 0 && hb + 2 < nhb)
+            dnext = loadD((hb >> 1) + 1);
+        bool zero[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t n = n0 + wn + j * 32 + (lane & 31);
+        for (int i = 0; i < 2; ++i)
+            zero[i] = dsh[db][wm + i * 32 + lr] == 0.f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) { // stage st = 2hb + q reads buffer q
+            const uint32_t st = hb * 2 + q;
+            half8 afc[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
+                const uint32_t kp = ks * 2 + p;
+                half8 afn[2], bfh[4], bfl[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    bfh[j] = *reinterpret_cast<const half8 *>(&Bh[q][swz(j * 32 + lr, kp)]);
+                    bfl[j] = *reinterpret_cast<const half8 *>(&Bl[q][swz(j * 32 + lr, kp)]);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j], acc[i][j], 0, 0, 0);
+                if (ks < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j], acc[i][j], 0, 0, 0);
+                if (ks < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        afc[i] = afn[i];
+                }
+            }
+            if (q == 0 && (hb & 1) && hb + 1 < nhb) // stage 4kb + 2: publish block kb + 1's scale
+                set_d(((hb >> 1) + 1) & 1, dnext);
+            __builtin_amdgcn_s_waitcnt(0); // this wave's pieces of stage st + 1 have landed
+            __syncthreads();
+            if (st + 2 < nst)
+                loadB(st + 2); // into the buffer every wave has just finished reading
+        }
+        if (hb + 1 < nhb) { // the half block is done: take the next, prefetch the one after
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch)
+                    A[i][ch] = An[i][ch];
+            if (hb + 2 < nhb)
+                loadA(hb + 2, An);
+        }
+    }
+    rsh[0][tid] = u;
+    __syncthreads();
+    rescale(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t n = n0 + j * 32 + lr;
         if (n >= ntok)
             continue;
         const uint32_t orow = slotl ? slotl[n] : n;
@@ -326,7 +338,7 @@ extern "C" __global__ __launch_bounds__(512) void k_gemm_q6(const GemmArgs a)
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t r = m0 + wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                const uint32_t r = m0 + wm + i * 32 + 8 * (e / 4) + 4 * p + (e % 4);
                 const float v = acc[i][j][e] * xs;
                 if (r < a.zrows)
                     out[r] = a.mode ? out[r] + v : v;

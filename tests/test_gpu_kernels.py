@@ -106,3 +106,36 @@ def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
         ref = oracle.q6k_matvec(raw, in_dim, rows, x[t])
         err = rel_l2(y[t], ref)
         assert err <= 1e-5, (t, err)
+
+
+def test_gemm_prefill_block_scale_edges(gpu, oracle):
+    """Super-block scales d that are zero (first, last, every other or every
+    block of a row), -0.0, subnormal, or spread over eleven decades within one
+    row: the GEMM folds d into its accumulators block by block, so every row
+    is checked on its own against the f64 oracle (rel-L2 over tokens <= 1e-5;
+    rows whose blocks all have d = 0 give exactly 0)."""
+    rows, in_dim, T = 300, 2048, 130
+    nb = in_dim // 256
+    raw = blocks(rows * nb, 77).reshape(rows, nb, 210)
+    rng = np.random.default_rng(5)
+    d = (rng.standard_normal((rows, nb)) * 1e-3).astype(np.float16)
+    kind = np.arange(rows) % 8
+    d[kind == 0] = 0
+    d[kind == 1, 0] = 0
+    d[kind == 2, nb - 1] = 0
+    d[kind == 3, ::2] = 0
+    spread = kind == 4
+    mag = 10.0 ** rng.uniform(-7, 4.5, size=(int(spread.sum()), nb))
+    d[spread] = (mag * rng.choice([-1.0, 1.0], size=mag.shape)).astype(np.float16)
+    d[kind == 5, 1::3] = np.float16(-0.0)
+    raw[:, :, 208:210] = d.view(np.uint8).reshape(rows, nb, 2)
+    raw = raw.reshape(-1)
+    x = rng.standard_normal((T, in_dim)).astype(np.float32)
+    y = gpu.q6k_gemm(gpu.Q6Weight(raw, rows, in_dim), x)
+    toks = [0, 64, 127, T - 1]
+    ref = np.stack([oracle.q6k_matvec(raw, in_dim, rows, x[t]) for t in toks])
+    got = y[toks]
+    assert np.all(got[:, kind == 0] == 0)
+    for r in np.flatnonzero(kind != 0):
+        err = rel_l2(got[:, r], ref[:, r])
+        assert err <= 1e-5, (r, kind[r], err)
