@@ -32,7 +32,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
 # HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes over this bench
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the scales are what the two
 # counters read for a plain 512 MiB copy): 1.02 x the algorithmic 24 163 456 bytes.
-GATEUP_TRAFFIC_BYTES = 24659689
+GATEUP_TRAFFIC_BYTES = 24660865
 SEED = 0x9E3779B97F4A7C15
 
 
@@ -208,13 +208,13 @@ def main():
         log(f"[bench] k_gateup8f (MoE): {us:.2f} us/launch = {gbs:.0f} GB/s")
         # largest single Q6_K matvec of a step: final norm + tied head (vocab x 2048),
         # over 3 rotating copies of the embedding planes (beyond the Infinity Cache)
-        hus, hbytes = eng.time_head(ncopies=3, reps=5)
+        hus, hbytes = eng.time_head(ncopies=3, reps=15)
         hgbs = hbytes / (hus * 1e-6) / 1e9
         extra["q6k_head"] = {
             "kernel": "k_head4 (final RMSNorm + %dx%d tied head + argmax partials)" % (hp.vocab, hp.dim),
             "algorithmic_bytes": hbytes, "us_per_launch": round(hus, 3), "hbm_gbs": round(hgbs, 1),
             "frac_of_peak": round(hgbs / HBM_PEAK_GBS, 4),
-            "timing": "HIP events over a graph of 15 launches rotating 3 weight copies (gaps included)"}
+            "timing": "HIP events over a graph of 45 launches rotating 3 weight copies (gaps included)"}
         log(f"[bench] k_head4: {hus:.2f} us/launch = {hgbs:.0f} GB/s ({hgbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
         algo, ms_hbm, ms_mall = matvec_roofline()
         extra["q6k_matvec_cfg0"] = {

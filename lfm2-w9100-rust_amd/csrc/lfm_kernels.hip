@@ -281,9 +281,10 @@ __device__ __forceinline__ void fill_items(Item<NR> (&buf)[G], uint32_t it0, uin
 // A lane's share of a row with the block index clamped into the row: lanes
 // past the row's blocks (b >= nb) re-read its last block, which the dot
 // products then leave out.
+template <bool StreamAll = false>
 __device__ __forceinline__ Lane load_lane_c(const Q6T &t, uint32_t row, uint32_t b, uint32_t c)
 {
-    return load_lane(t, row, min(b, t.nb - 1), c);
+    return load_lane<StreamAll>(t, row, min(b, t.nb - 1), c);
 }
 // Wave sum of N per-lane values at once (results in every lane).
 template <int N> __device__ __forceinline__ void wave_sum_n(float *v)
@@ -1193,7 +1194,7 @@ __device__ __forceinline__ void head_body(const HeadArgs &a)
     const uint32_t b = lane >> 3, c = lane & 7;
     const bool active = b < a.emb.nb;
     const uint32_t rows = a.vocab, W = gridDim.x * NW, first = blockIdx.x * NW + wave;
-    auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c(a.emb, r, b, c); };
+    auto load = [&](uint32_t r, Item<1> &it) { it.l[0] = load_lane_c<true>(a.emb, r, b, c); };
     XRaw raw;
     x_issue(a.src, a.emb.nb * 256, a.st, raw);
     Item<1> buf[G];
