@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        swiglu_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -231,7 +231,7 @@ static int get_kernels(Kernels **out)
     } pfns[] = {{&k->split_rows, "k_split_rows"},       {&k->gemm_q6, "k_gemm_q6"},
                 {&k->conv_prefill, "k_conv_prefill"},   {&k->conv_state, "k_conv_state"},
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
-                {&k->swiglu_split, "k_swiglu_split"},   {&k->router_prefill, "k_router_prefill"},
+                {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_prefill, "k_router_prefill"},
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"},
                 {&k->embed_rows, "k_embed_rows"}};
@@ -538,9 +538,9 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
 #define GEMM_ROWS 256   // weight rows per GEMM workgroup
 #define GEMM_TOKENS 128 // token columns per GEMM workgroup
 #define GEMM_THREADS 256 // 4 waves of 64 weight rows each
-static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz)
+static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_per_wg = GEMM_ROWS)
 {
-    return dim3((rows + GEMM_ROWS - 1) / GEMM_ROWS, (ntok + GEMM_TOKENS - 1) / GEMM_TOKENS, nz);
+    return dim3((rows + rows_per_wg - 1) / rows_per_wg, (ntok + GEMM_TOKENS - 1) / GEMM_TOKENS, nz);
 }
 
 // Y[t][r] = sum_k W[r][k] X[t][k] for T token rows (prefill GEMM, op level).
@@ -646,7 +646,7 @@ struct lfm_engine {
     DevState *host_st = nullptr;    // pinned staging for state copies
     // batched prefill buffers (capacity: ctx tokens per call)
     struct {
-        float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *u = nullptr, *d = nullptr;
+        float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr;
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
         uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr;
@@ -1162,7 +1162,6 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.bcx, TC * bcxw * 4));
         HIPCHK(hipMalloc(&e->pf.y, TC * dim * 4));
         HIPCHK(hipMalloc(&e->pf.g, TC * wide * 4));
-        HIPCHK(hipMalloc(&e->pf.u, TC * wide * 4));
         HIPCHK(hipMalloc(&e->pf.d, TC * 4 * dim * 4));
         HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
@@ -1196,7 +1195,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->logits, e->hpart, e->apart, e->rope,
-                    e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.u, e->pf.d, e->pf.hi, e->pf.lo,
+                    e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot};
     for (void *p : bufs)
@@ -1249,6 +1248,37 @@ static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t l
     g.col0 = col0;
     g.mode = mode;
     RC(launch_t(e->K->gemm_q6, gemm_grid(w.rows, T, 1), GEMM_THREADS, 0, e->stream, g));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
+// Gate and up projections of a SwiGLU FFN in one launch: c = silu(Wg x) * (Wu x)
+// for `zrows` rows per weight (128 of each per workgroup).  Dense (tok null): the
+// T tokens of the call; grouped: z = expert over the per-expert token lists, as
+// pf_gemm_grouped.
+static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t zrows, uint32_t T,
+                          const uint32_t *tok, float *c, uint32_t ldc)
+{
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.w = wg;
+    g.w2 = wu;
+    g.x_hi = e->pf.hi;
+    g.x_lo = e->pf.lo;
+    g.xscale = e->pf.scale;
+    g.ntok = T;
+    g.zrows = zrows;
+    g.c = c;
+    g.ldc = ldc;
+    uint32_t nz = 1;
+    if (tok) {
+        g.tok = tok;
+        g.slot = e->pf.slot;
+        g.counts = e->pf.counts;
+        g.list_stride = e->ctx;
+        nz = e->hp.n_expert;
+    }
+    RC(launch_t(e->K->gemm_swiglu, gemm_grid(zrows, T, nz, GEMM_ROWS / 2), GEMM_THREADS, 0, e->stream, g));
     e->dispatches += 1;
     return LFM_OK;
 }
@@ -1318,12 +1348,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     if (l < hp.dense_lead) {
         const uint32_t ff = hp.n_ff;
         RC(pf_split(e, x, norm, T, dim));
-        RC(pf_gemm(e, q6(e, "blk.%u.ffn_gate.weight", l), T, e->pf.g, ff, 0, 0));
-        RC(pf_gemm(e, q6(e, "blk.%u.ffn_up.weight", l), T, e->pf.u, ff, 0, 0));
-        SwigluSplitArgs sw{e->pf.g, e->pf.u, e->pf.hi, e->pf.lo, e->pf.scale, T, ff};
-        RC(launch(e->K->swiglu_split, dim3(T), 0, e->stream, sw));
+        RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate.weight", l), q6(e, "blk.%u.ffn_up.weight", l), ff, T,
+                          nullptr, e->pf.g, ff));
+        RC(pf_split(e, e->pf.g, nullptr, T, ff));
         RC(pf_gemm(e, q6(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
-        e->dispatches += 1;
         return LFM_OK;
     }
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
@@ -1335,14 +1363,13 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
     RC(pf_split(e, x, norm, T, dim));
-    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), eff, T, e->pf.tok, e->pf.g, eff));
-    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_up_exps.weight", l), eff, T, e->pf.tok, e->pf.u, eff));
-    SwigluSplitArgs sw{e->pf.g, e->pf.u, e->pf.hi, e->pf.lo, e->pf.scale, 4 * T, eff};
-    RC(launch(e->K->swiglu_split, dim3(4 * T), 0, e->stream, sw));
+    RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), q6(e, "blk.%u.ffn_up_exps.weight", l), eff,
+                      T, e->pf.tok, e->pf.g, eff));
+    RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff)); // slots are token * 4 + rank
     RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim));
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
     RC(launch(e->K->combine_prefill, dim3((dim + 255) / 256, T), 0, e->stream, cb));
-    e->dispatches += 5;
+    e->dispatches += 4;
     return LFM_OK;
 }
 

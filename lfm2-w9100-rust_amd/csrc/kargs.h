@@ -203,6 +203,7 @@ struct SplitArgs {
 // its token list (grouped GEMM).  Plain GEMM: zrows = w.rows, lists null.
 struct GemmArgs {
     Q6T w;
+    Q6T w2;                 // pair kernel: the up weight (gate in w), same shape
     const uint16_t *x_hi, *x_lo;
     const float *xscale;
     const uint32_t *tok;    // [z][list_stride] activation rows, nullable
@@ -235,13 +236,6 @@ struct AttnPrefillArgs {  // causal GQA attention of T queries at positions star
     float *out;           // [T][dim]
     float scale;
     uint32_t T, start, heads, kv, ctx;
-};
-
-struct SwigluSplitArgs {  // sw = silu(g) * u, then binary16 hi/lo split with row scale
-    const float *g, *u;   // [T][ff]
-    uint16_t *hi, *lo;
-    float *scale;
-    uint32_t T, ff;
 };
 
 struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)

@@ -132,11 +132,15 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 
 // C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, zrows) of group
 // z and token columns n < ntok.  Column n reads activation row (tok ? tok[n] :
-// n) and writes output row (slot ? slot[n] : n).
+// n) and writes output row (slot ? slot[n] : n).  The pair form (k_gemm_q6_swiglu)
+// multiplies the gate weight w and the up weight w2 by the same activations and
+// writes silu(gate) * up (lfm.rs:578-582 SwiGLU, g / (1 + e^-g) * u).
 //
-// A workgroup computes 256 rows x 128 tokens; wave w owns rows 64w..64w+63 for
-// all 128 tokens (2 x 4 tiles of v_mfma_f32_32x32x16_f16, hi and lo activation
-// halves).  K advances in 64-wide stages:
+// A workgroup computes 256 weight rows x 128 tokens: wave w owns rows 64w..64w+63
+// for all 128 tokens (2 x 4 tiles of v_mfma_f32_32x32x16_f16, hi and lo
+// activation halves); in the pair form its two row tiles are the same 32 rows of
+// the gate and of the up weight (128 rows of each per workgroup), so a lane holds
+// a row's gate and up sums side by side.  K advances in 64-wide stages:
 //   * weights never touch LDS: each lane loads its rows' Q6_K bytes one half
 //     block ahead into registers and decodes the MFMA A fragments itself, the
 //     next k-step's fragments while the current k-step's MFMAs run;
@@ -149,9 +153,12 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 // Workgroup i runs on XCD i % 8; tiles are handed out so that each XCD takes a
 // contiguous run with the weight rows fastest, and the workgroups resident on
 // one XCD share activation tiles in its L2.
-extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-k_gemm_q6(const GemmArgs a)
+template <bool PAIR>
+__device__ __forceinline__ void gemm_body(const GemmArgs &a)
 {
+    // rows of each weight per workgroup; the workgroup's 256 "tile rows" v are
+    // rows m0 + v (single) or rows m0 + (v & 127) of weight v >> 7 (pair)
+    constexpr uint32_t TMW = PAIR ? TM / 2 : TM;
     uint32_t z, mx, ny;
     {
         const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
@@ -162,7 +169,7 @@ k_gemm_q6(const GemmArgs a)
         ny = (V / gx) % gy;
         z = V / (gx * gy);
     }
-    const uint32_t m0 = mx * TM, n0 = ny * TN;
+    const uint32_t m0 = mx * TMW, n0 = ny * TN;
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
@@ -175,13 +182,17 @@ k_gemm_q6(const GemmArgs a)
     __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TN * TK];
     __shared__ float dsh[2][TM], rsh[2][TM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint32_t wm = wave * 64, p = lane >> 5, lr = lane & 31;
+    const uint32_t p = lane >> 5, lr = lane & 31;
     const uint32_t nb = a.w.nb, K = nb * 256;
     const size_t nblk = (size_t)a.w.rows * nb;
-    uint32_t arow[2];
+    // row tile i of the wave: tile rows vb[i] .. vb[i] + 31, rows lb[i] .. of weight i (pair)
+    uint32_t vb[2], lb[2], arow[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        arow[i] = rbase + min(m0 + wm + i * 32 + lr, a.zrows - 1);
+    for (int i = 0; i < 2; ++i) {
+        vb[i] = PAIR ? i * 128 + wave * 32 : wave * 64 + i * 32;
+        lb[i] = PAIR ? wave * 32 : vb[i];
+        arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
+    }
     // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
     // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
     // k-piece j ^ ((t >> 1) & 7)
@@ -196,13 +207,14 @@ k_gemm_q6(const GemmArgs a)
         const uint32_t kb = half >> 1, h = half & 1;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
             const size_t blk = (size_t)arow[i] * nb + kb;
 #pragma unroll
             for (int ch = 0; ch < 2; ++ch) {
                 const uint32_t c = 4 * h + 2 * ch + p;
-                A[i][ch].ql = *reinterpret_cast<const uint4 *>(a.w.base + blk * 128 + c * 16);
-                A[i][ch].qh = *reinterpret_cast<const uint2 *>(a.w.base + nblk * 128 + blk * 64 + c * 8);
-                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(a.w.base + nblk * 192 + blk * 16 + (c >> 1) * 4);
+                A[i][ch].ql = *reinterpret_cast<const uint4 *>(wb + blk * 128 + c * 16);
+                A[i][ch].qh = *reinterpret_cast<const uint2 *>(wb + nblk * 128 + blk * 64 + c * 8);
+                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(wb + nblk * 192 + blk * 16 + (c >> 1) * 4);
             }
         }
     };
@@ -218,9 +230,10 @@ k_gemm_q6(const GemmArgs a)
                                              (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
         }
     };
-    auto loadD = [=](uint32_t kb) -> float {
-        const uint32_t row = rbase + min(m0 + tid, a.zrows - 1);
-        return half_bits_to_float(reinterpret_cast<const uint16_t *>(a.w.base + nblk * 208)[(size_t)row * nb + kb]);
+    auto loadD = [=](uint32_t kb) -> float { // d of tile row tid
+        const uint8_t *wb = PAIR && tid >= 128 ? a.w2.base : a.w.base;
+        const uint32_t row = rbase + min(m0 + (PAIR ? tid & 127 : tid), a.zrows - 1);
+        return half_bits_to_float(reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)row * nb + kb]);
     };
     floatx16 acc[2][4];
 #pragma unroll
@@ -235,13 +248,13 @@ k_gemm_q6(const GemmArgs a)
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float r = rsh[rb][wm + i * 32 + 8 * (e / 4) + 4 * p + (e % 4)];
+                const float r = rsh[rb][vb[i] + 8 * (e / 4) + 4 * p + (e % 4)];
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j][e] *= r;
             }
     };
-    // thread tid keeps row tid's running scale u (TM == GEMM_NTH)
+    // thread tid keeps tile row tid's running scale u (TM == GEMM_NTH)
     float u = 1.0f;
     auto set_d = [&](uint32_t slot, float d) {
         dsh[slot][tid] = d;
@@ -268,7 +281,7 @@ k_gemm_q6(const GemmArgs a)
         bool zero[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            zero[i] = dsh[db][wm + i * 32 + lr] == 0.f;
+            zero[i] = dsh[db][vb[i] + lr] == 0.f;
 #pragma unroll
         for (int q = 0; q < 2; ++q) { // stage st = 2hb + q reads buffer q
             const uint32_t st = hb * 2 + q;
@@ -334,16 +347,38 @@ k_gemm_q6(const GemmArgs a)
         const uint32_t orow = slotl ? slotl[n] : n;
         const float xs = a.xscale[tokl ? tokl[n] : n];
         float *out = a.c + (size_t)orow * a.ldc + a.col0;
+        if (PAIR) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t r = m0 + lb[0] + 8 * (e / 4) + 4 * p + (e % 4);
+                const float g = acc[0][j][e] * xs, u = acc[1][j][e] * xs;
+                if (r < a.zrows)
+                    out[r] = g / (1.0f + expf(-g)) * u;
+            }
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t r = m0 + wm + i * 32 + 8 * (e / 4) + 4 * p + (e % 4);
+                const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
                 const float v = acc[i][j][e] * xs;
                 if (r < a.zrows)
                     out[r] = a.mode ? out[r] + v : v;
             }
     }
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6(const GemmArgs a)
+{
+    gemm_body<false>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6_swiglu(const GemmArgs a)
+{
+    gemm_body<true>(a);
 }
 // ------------------------------------------------------------------ short conv
 // The LFM2 short conv keeps only the previous two values of bx = B*X, so each
@@ -567,39 +602,6 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
 }
 
 // ------------------------------------------------------------------ FFN pieces
-// sw = g / (1 + exp(-g)) * u (lfm.rs:578-582), then the binary16 hi/lo split for
-// the down projection with a per-row power-of-two scale.
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_swiglu_split(const SwigluSplitArgs a)
-{
-    const uint32_t t = blockIdx.x;
-    if (t >= a.T)
-        return;
-    const float *g = a.g + (size_t)t * a.ff, *u = a.u + (size_t)t * a.ff;
-    __shared__ float redm[4];
-    float amax = 0.f;
-    for (uint32_t k = threadIdx.x; k < a.ff; k += WG_THREADS) {
-        const float gv = g[k];
-        amax = fmaxf(amax, fabsf(gv / (1.0f + expf(-gv)) * u[k]));
-    }
-    amax = wave_max(amax);
-    if ((threadIdx.x & 63) == 0)
-        redm[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
-    int e = 0;
-    if (amax > 0.f && amax <= 3.0e38f)
-        frexpf(amax, &e);
-    const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
-    if (threadIdx.x == 0)
-        a.scale[t] = scale;
-    _Float16 *hi = reinterpret_cast<_Float16 *>(a.hi) + (size_t)t * a.ff;
-    _Float16 *lo = reinterpret_cast<_Float16 *>(a.lo) + (size_t)t * a.ff;
-    for (uint32_t k = threadIdx.x; k < a.ff; k += WG_THREADS) {
-        const float gv = g[k];
-        split_f16(gv / (1.0f + expf(-gv)) * u[k] * rs, hi[k], lo[k]);
-    }
-}
-
 // Router logits for T tokens (lfm.rs:599-607): a workgroup takes 16 tokens.
 // Each wave first finds the RMSNorm scale of 4 of them; then 128-wide slices of
 // x . w and of the f32 router rows are staged in LDS (rows padded by 4 floats,
