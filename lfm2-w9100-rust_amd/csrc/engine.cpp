@@ -640,6 +640,10 @@ struct lfm_engine {
           *logits = nullptr, *hpart = nullptr, *apart = nullptr;
     float *rpart = nullptr; // fused router partial sums [ROUTE_EXPERTS + 1][ROUTE_PARTS]
     std::vector<uint16_t *> kc, vc;
+    // attention layers: attn_q, attn_k and attn_v rows concatenated into one
+    // Q6_K tensor (plane layout), so prefill projects q, k, v in one GEMM
+    std::vector<Q6T> qkvw;
+    std::vector<void *> qkvdev;
     std::vector<float *> conv;
     uint32_t head_grid = 1, nchunk = 1;
     float *rope = nullptr; // [ctx][32] (cos, sin)
@@ -1137,6 +1141,29 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMemset(e->logits, 0, (size_t)hp.vocab * 4));
     HIPCHK(hipMalloc(&e->hpart, e->head_grid * 2 * 4));
     HIPCHK(hipMalloc(&e->apart, (size_t)8 * e->nchunk * 4 * 66 * 4));
+    e->qkvdev.assign(hp.n_layers, nullptr);
+    e->qkvw.assign(hp.n_layers, Q6T{});
+    for (uint32_t l = 0; l < hp.n_layers; ++l) {
+        if (!hp.kv_heads[l])
+            continue;
+        const Q6T parts[3] = {q6(e, "blk.%u.attn_q.weight", l), q6(e, "blk.%u.attn_k.weight", l),
+                              q6(e, "blk.%u.attn_v.weight", l)};
+        const uint32_t rows = parts[0].rows + parts[1].rows + parts[2].rows, nb = parts[0].nb;
+        const size_t nblk = (size_t)rows * nb;
+        HIPCHK(hipMalloc(&e->qkvdev[l], nblk * 210));
+        uint8_t *dst = (uint8_t *)e->qkvdev[l];
+        // planes ql (128 B per block), qh (64), scales (16), d (2), each [rows][nb]
+        const size_t pofs[4] = {0, 128, 192, 208}, psz[4] = {128, 64, 16, 2};
+        for (int pl = 0; pl < 4; ++pl) {
+            size_t at = nblk * pofs[pl];
+            for (const Q6T &t : parts) {
+                const size_t tb = (size_t)t.rows * t.nb;
+                HIPCHK(hipMemcpy(dst + at, t.base + tb * pofs[pl], tb * psz[pl], hipMemcpyDeviceToDevice));
+                at += tb * psz[pl];
+            }
+        }
+        e->qkvw[l] = q6view(dst, rows, (uint64_t)nb * 256);
+    }
     e->kc.assign(hp.n_layers, nullptr);
     e->vc.assign(hp.n_layers, nullptr);
     e->conv.assign(hp.n_layers, nullptr);
@@ -1205,6 +1232,9 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipHostFree(e->host_st);
     if (e->host_ids)
         (void)hipHostFree(e->host_ids);
+    for (auto p : e->qkvdev)
+        if (p)
+            (void)hipFree(p);
     for (auto p : e->kc)
         if (p)
             (void)hipFree(p);
@@ -1323,9 +1353,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         return LFM_OK;
     }
     const uint32_t hdkv = 64 * kv, w = dim + 2 * hdkv;
-    RC(pf_gemm(e, q6(e, "blk.%u.attn_q.weight", l), T, e->pf.bcx, w, 0, 0));
-    RC(pf_gemm(e, q6(e, "blk.%u.attn_k.weight", l), T, e->pf.bcx, w, dim, 0));
-    RC(pf_gemm(e, q6(e, "blk.%u.attn_v.weight", l), T, e->pf.bcx, w, dim + hdkv, 0));
+    RC(pf_gemm(e, e->qkvw[l], T, e->pf.bcx, w, 0, 0)); // rows q | k | v = columns of bcx
     RopeKvArgs r{e->pf.bcx, f32(e, "blk.%u.attn_q_norm.weight", l),
                  f32(e, "blk.%u.attn_k_norm.weight", l), e->rope, hp.eps, e->kc[l], e->vc[l], T,
                  start, hp.heads, kv, e->ctx};
