@@ -1256,6 +1256,8 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
 // residual in e->x (the decode path's residual) for the head.
 static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t T, uint32_t K)
 {
+    if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
+        return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
     SplitArgs a{x, norm, e->hp.eps, e->pf.hi, e->pf.lo, e->pf.scale, T, K};
     RC(launch(e->K->split_rows, dim3(T), 0, e->stream, a));
     e->dispatches += 1;

@@ -32,45 +32,59 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
 
 // RMSNorm (optional) of T rows of x [T][K], then a binary16 hi/lo split of
 // x / scale with scale = 2^(e - 14) for max|x| = m * 2^e (so |x / scale| < 2^14).
-// One workgroup per token row.
+// One workgroup per token row; K is a multiple of 256 up to 8192 (the engine's
+// widths), so thread tid keeps its elements tid + 256 i in registers and the
+// row is read from memory once.
+#define SPLIT_NPT 32
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
 {
     const uint32_t t = blockIdx.x;
     if (t >= a.T)
         return;
+    const uint32_t tid = threadIdx.x, nk = a.K / WG_THREADS;
     const float *x = a.x + (size_t)t * a.K;
     __shared__ float red[4], redm[4];
-    float ss = 0.f;
-    for (uint32_t k = threadIdx.x; k < a.K; k += WG_THREADS)
-        ss += x[k] * x[k];
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-    const float inv = a.norm_w ? 1.0f / sqrtf(tot / (float)a.K + a.eps) : 1.0f;
-    float amax = 0.f;
-    for (uint32_t k = threadIdx.x; k < a.K; k += WG_THREADS) {
-        const float v = a.norm_w ? x[k] * inv * a.norm_w[k] : x[k];
-        amax = fmaxf(amax, fabsf(v));
+    float v[SPLIT_NPT];
+#pragma unroll
+    for (int i = 0; i < SPLIT_NPT; ++i)
+        v[i] = i < (int)nk ? x[i * WG_THREADS + tid] : 0.f;
+    if (a.norm_w) { // uniform
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < SPLIT_NPT; ++i)
+            ss += v[i] * v[i];
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0)
+            red[tid >> 6] = ss;
+        __syncthreads();
+        const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+        const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+        for (int i = 0; i < SPLIT_NPT; ++i)
+            if (i < (int)nk)
+                v[i] = v[i] * inv * a.norm_w[i * WG_THREADS + tid];
     }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < SPLIT_NPT; ++i)
+        amax = fmaxf(amax, fabsf(v[i]));
     amax = wave_max(amax);
-    if ((threadIdx.x & 63) == 0)
-        redm[threadIdx.x >> 6] = amax;
+    if ((tid & 63) == 0)
+        redm[tid >> 6] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     int e = 0;
     if (amax > 0.f && amax <= 3.0e38f)
         frexpf(amax, &e);
     const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
-    if (threadIdx.x == 0)
+    if (tid == 0)
         a.scale[t] = scale;
     _Float16 *hi = reinterpret_cast<_Float16 *>(a.hi) + (size_t)t * a.K;
     _Float16 *lo = reinterpret_cast<_Float16 *>(a.lo) + (size_t)t * a.K;
-    for (uint32_t k = threadIdx.x; k < a.K; k += WG_THREADS) {
-        const float v = (a.norm_w ? x[k] * inv * a.norm_w[k] : x[k]) * rs;
-        split_f16(v, hi[k], lo[k]);
-    }
+#pragma unroll
+    for (int i = 0; i < SPLIT_NPT; ++i)
+        if (i < (int)nk)
+            split_f16(v[i] * rs, hi[i * WG_THREADS + tid], lo[i * WG_THREADS + tid]);
 }
 
 #define TM 256 // weight rows per workgroup (4 waves of 64 rows)
@@ -603,12 +617,12 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
 
 // ------------------------------------------------------------------ FFN pieces
 // Router logits for T tokens (lfm.rs:599-607): a workgroup takes 16 tokens.
-// Each wave first finds the RMSNorm scale of 4 of them; then 128-wide slices of
-// x . w and of the f32 router rows are staged in LDS (rows padded by 4 floats,
-// so the 16-byte reads below are conflict-free) and thread (token tid / 16,
-// experts tid % 16 + 16 j) accumulates its dot products in k order, reading
-// four k at a time; logits = inv * sum.  NE = 2 covers up to 32 experts, 4 up
-// to 64.
+// 128-wide slices of x . w and of the f32 router rows are staged in LDS (rows
+// padded by 4 floats, so the 16-byte reads below are conflict-free), the next
+// slice's loads in flight while thread (token tid / 16, experts tid % 16 + 16 j)
+// accumulates its dot products in k order, four k at a time; the RMSNorm sum of
+// squares is gathered from the same staged loads, and logits = inv * sum.  NE = 2
+// covers up to 32 experts, 4 up to 64.
 #define RT_TOK 16
 #define RT_K 128
 #define RT_PAD (RT_K + 4)
@@ -635,53 +649,71 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const 
     __shared__ float inv[RT_TOK];
     __shared__ __attribute__((aligned(16))) float xs[RT_TOK * RT_PAD];
     __shared__ __attribute__((aligned(16))) float ws[RT_EMAX * RT_PAD];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t t0 = blockIdx.x * RT_TOK;
-    for (uint32_t j = 0; j < RT_TOK / 4; ++j) {
-        const uint32_t tt = wave * (RT_TOK / 4) + j, t = t0 + tt;
-        if (t < a.T) { // uniform across the wave
-            const float *x = a.x + (size_t)t * a.dim;
-            float ss = 0.f;
-            for (uint32_t k = lane; k < a.dim; k += 64)
-                ss += x[k] * x[k];
-            ss = wave_sum(ss);
-            if (lane == 0)
-                inv[tt] = 1.0f / sqrtf(ss / (float)a.dim + a.eps);
-        }
-    }
     const uint32_t tt = tid / 16, eg = tid % 16;
-    const bool wide = a.n_expert > 32;                     // uniform
-    const uint32_t wrows = wide ? RT_EMAX : 32;             // staged expert rows
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k0 = 0; k0 < a.dim; k0 += RT_K) {
-        __syncthreads();
-        // 16 tokens x 128 floats of x . w: two float4 per thread
+    const bool wide = a.n_expert > 32;    // uniform
+    const uint32_t nw4 = wide ? 8 : 4;    // float4 of router rows per thread and slice
+    // staging: x piece v of thread tid is token (tid + 256v) / 32, floats
+    // ((tid + 256v) % 32) * 4 ..; router piece v is row (tid + 256v) / 32 likewise
+    float4 xr[2], nr[2], wr[8];
+    float ss[2] = {0.f, 0.f};
+    auto fetch = [&](uint32_t k0) {
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
-            const uint32_t u = tid + WG_THREADS * v, r = u / (RT_K / 4), kk = (u % (RT_K / 4)) * 4;
-            const uint32_t t = t0 + r;
-            float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t < a.T) {
-                const float4 x4 = *reinterpret_cast<const float4 *>(a.x + (size_t)t * a.dim + k0 + kk);
-                const float4 n4 = *reinterpret_cast<const float4 *>(a.norm_w + k0 + kk);
-                xv = make_float4(x4.x * n4.x, x4.y * n4.y, x4.z * n4.z, x4.w * n4.w);
-            }
-            *reinterpret_cast<float4 *>(&xs[r * RT_PAD + kk]) = xv;
+            const uint32_t u = tid + WG_THREADS * v, t = t0 + u / 32, kk = (u % 32) * 4;
+            xr[v] = t < a.T ? *reinterpret_cast<const float4 *>(a.x + (size_t)t * a.dim + k0 + kk)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            nr[v] = *reinterpret_cast<const float4 *>(a.norm_w + k0 + kk);
         }
-        // wrows x 128 floats of the router rows (rows past n_expert are zero)
-        for (uint32_t u = tid; u < wrows * (RT_K / 4); u += WG_THREADS) {
-            const uint32_t e = u / (RT_K / 4), kk = (u % (RT_K / 4)) * 4;
-            float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (e < a.n_expert)
-                wv = *reinterpret_cast<const float4 *>(a.w + (size_t)e * a.dim + k0 + kk);
-            *reinterpret_cast<float4 *>(&ws[e * RT_PAD + kk]) = wv;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const uint32_t u = tid + WG_THREADS * v, e = u / 32, kk = (u % 32) * 4;
+            if (v < (int)nw4)
+                wr[v] = e < a.n_expert ? *reinterpret_cast<const float4 *>(a.w + (size_t)e * a.dim + k0 + kk)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const uint32_t u = tid + WG_THREADS * v, r = u / 32, kk = (u % 32) * 4;
+            const float4 x4 = xr[v], n4 = nr[v];
+            ss[v] += x4.x * x4.x + x4.y * x4.y + x4.z * x4.z + x4.w * x4.w;
+            *reinterpret_cast<float4 *>(&xs[r * RT_PAD + kk]) =
+                make_float4(x4.x * n4.x, x4.y * n4.y, x4.z * n4.z, x4.w * n4.w);
+        }
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+            const uint32_t u = tid + WG_THREADS * v, e = u / 32, kk = (u % 32) * 4;
+            if (v < (int)nw4)
+                *reinterpret_cast<float4 *>(&ws[e * RT_PAD + kk]) = wr[v];
+        }
+    };
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    for (uint32_t k0 = 0; k0 < a.dim; k0 += RT_K) {
+        __syncthreads(); // the previous slice's dot products are done
+        stage();
+        if (k0 + RT_K < a.dim)
+            fetch(k0 + RT_K); // in flight during this slice's dot products
         __syncthreads();
         if (wide)
             router_dots<4>(xs + tt * RT_PAD, ws, eg, acc);
         else
             router_dots<2>(xs + tt * RT_PAD, ws, eg, acc);
     }
+    // RMSNorm scale: token (tid + 256v) / 32 is shared by the 32 lanes of a wave half
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        float q = ss[v];
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1)
+            q += __shfl_xor(q, off, 64);
+        if ((lane & 31) == 0)
+            inv[(tid + WG_THREADS * v) / 32] = 1.0f / sqrtf(q / (float)a.dim + a.eps);
+    }
+    __syncthreads();
     const uint32_t t = t0 + tt;
     if (t < a.T)
 #pragma unroll
