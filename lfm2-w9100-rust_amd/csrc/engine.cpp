@@ -1398,7 +1398,7 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff)); // slots are token * 4 + rank
     RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim));
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
-    RC(launch(e->K->combine_prefill, dim3((dim + 255) / 256, T), 0, e->stream, cb));
+    RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread
     e->dispatches += 4;
     return LFM_OK;
 }

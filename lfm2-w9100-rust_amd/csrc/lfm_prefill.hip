@@ -487,7 +487,8 @@ typedef float floatx16a __attribute__((ext_vector_type(16)));
 #define FA_VROW 36 // halves per transposed-V row in LDS (32 + 4)
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const AttnPrefillArgs a)
 {
-    const uint32_t kh = blockIdx.y, t0 = blockIdx.x * FA_Q;
+    // the longest (latest) query tiles are dispatched first
+    const uint32_t kh = blockIdx.y, t0 = (gridDim.x - 1 - blockIdx.x) * FA_Q;
     if (t0 >= a.T)
         return;
     const uint32_t G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64, stride = dim + 2 * hdkv;
@@ -496,7 +497,10 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
     __shared__ __attribute__((aligned(16))) _Float16 Vt[2][64 * FA_VROW];
     const bool active = wave < G;
     const uint32_t h = kh * G + (active ? wave : 0);
-    // q fragments (B operand, 16 keys-dims steps): lane holds query lq, dims ks*16 + 8*lh + i
+    // q fragments (B operand, 16 keys-dims steps): lane holds query lq, dims ks*16 + 8*lh + i.
+    // Scores are kept in log2 units (q scaled by scale * log2 e), so the softmax
+    // exponentials are single v_exp_f32 (2^x): 2^(s2 - m2) = e^(s - m).
+    const float qscale = a.scale * 1.4426950408889634f;
     const uint32_t tq = t0 + lq;
     half8 qh[4], ql[4];
     {
@@ -508,7 +512,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
             const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float x = v[i] * a.scale;
+                const float x = v[i] * qscale;
                 qh[ks][i] = (_Float16)x;
                 ql[ks][i] = (_Float16)(x - (float)qh[ks][i]);
             }
@@ -569,12 +573,12 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
             }
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
             const float mn = fmaxf(m, bm);
-            const float r = m > -INFINITY ? expf(m - mn) : 0.f;
+            const float r = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.f;
             float ps = 0.f;
             half4v phi[4], plo[4];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = sacc[e] > -INFINITY ? expf(sacc[e] - mn) : 0.f;
+                const float p = sacc[e] > -INFINITY ? __builtin_amdgcn_exp2f(sacc[e] - mn) : 0.f;
                 ps += p;
                 const _Float16 hi = (_Float16)p;
                 phi[e / 4][e % 4] = hi;
@@ -791,14 +795,31 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const Rou
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_combine_prefill(const CombinePrefillArgs a)
 {
 #pragma clang fp contract(off)
-    const uint32_t k = blockIdx.x * WG_THREADS + threadIdx.x, t = blockIdx.y;
+    // thread: 4 consecutive k of token t; every rank's loads issued together
+    const uint32_t k = (blockIdx.x * WG_THREADS + threadIdx.x) * 4, t = blockIdx.y;
     if (k >= a.dim || t >= a.T)
         return;
-    float s = 0.0f;
-    for (uint32_t r = 0; r < a.n_used; ++r)
-        s = s + a.d[((size_t)t * 4 + r) * a.dim + k] * a.wsel[(size_t)t * 4 + r];
-    float *x = a.x + (size_t)t * a.dim + k;
-    *x = *x + s;
+    float4 dv[4];
+    float wv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bool on = r < (int)a.n_used;
+        dv[r] = on ? *reinterpret_cast<const float4 *>(a.d + ((size_t)t * 4 + r) * a.dim + k)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[r] = on ? a.wsel[(size_t)t * 4 + r] : 0.f;
+    }
+    float4 *xp = reinterpret_cast<float4 *>(a.x + (size_t)t * a.dim + k);
+    const float4 x0 = *xp;
+    float4 sm = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (r < (int)a.n_used) {
+            sm.x = sm.x + dv[r].x * wv[r];
+            sm.y = sm.y + dv[r].y * wv[r];
+            sm.z = sm.z + dv[r].z * wv[r];
+            sm.w = sm.w + dv[r].w * wv[r];
+        }
+    *xp = make_float4(x0.x + sm.x, x0.y + sm.y, x0.z + sm.z, x0.w + sm.w);
 }
 
 // Token embeddings of T ids (lfm.rs:310-320): row ids[t] of the Q6_K table,
