@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -233,7 +233,8 @@ static int get_kernels(Kernels **out)
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
                 {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_prefill, "k_router_prefill"},
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
-                {&k->combine_prefill, "k_combine_prefill"},
+                {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
+                {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
@@ -538,9 +539,50 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
 #define GEMM_ROWS 256   // weight rows per GEMM workgroup
 #define GEMM_TOKENS 128 // token columns per GEMM workgroup
 #define GEMM_THREADS 256 // 4 waves of 64 weight rows each
-static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_per_wg = GEMM_ROWS)
+static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_per_wg = GEMM_ROWS,
+                      uint32_t tokens_per_wg = GEMM_TOKENS)
 {
-    return dim3((rows + rows_per_wg - 1) / rows_per_wg, (ntok + GEMM_TOKENS - 1) / GEMM_TOKENS, nz);
+    return dim3((rows + rows_per_wg - 1) / rows_per_wg, (ntok + tokens_per_wg - 1) / tokens_per_wg, nz);
+}
+
+#define GEMM_PART_BYTES ((size_t)64 << 20) // split-K partial sums (prefill scratch)
+
+// Launches the matrix-core GEMM g (pair: gate + up + SwiGLU) over T tokens and nz
+// groups.  Up to one 128-token tile (T <= 128, as in 64-token chunked prefill,
+// about 8 tokens per expert) the kernels with 32-token tiles run, the grid is
+// then mostly the weight-row tiles and each workgroup's K loop is a chain of
+// dependent stages, so K is split into slices (about 1024 workgroups, each slice
+// at least one Q6_K block, the partials within `part_cap` floats of `part`) and
+// k_gemm_reduce adds the slices in order.  part_rows: output rows the GEMM can
+// write (T, or 4T for expert slots); n_used: ranks per token of the expert slots.
+static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
+                       uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches)
+{
+    const bool small = T <= GEMM_TOKENS;
+    dim3 grid = gemm_grid(g.zrows, T, nz, pair ? GEMM_ROWS / 2 : GEMM_ROWS, small ? 32 : GEMM_TOKENS);
+    uint32_t S = 1;
+    if (part && small) {
+        const uint32_t wgs = grid.x * grid.y * grid.z;
+        const size_t per = (size_t)(pair ? 2 : 1) * part_rows * g.zrows;
+        S = std::min<uint32_t>(std::max<uint32_t>(1, 1024 / wgs), g.w.nb);
+        S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, part_cap / per));
+    }
+    hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : K->gemm_q6_t32) : (pair ? K->gemm_swiglu : K->gemm_q6);
+    if (S == 1) {
+        RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
+        *dispatches += 1;
+        return LFM_OK;
+    }
+    g.part = part;
+    g.ksplit = S;
+    g.nz = nz;
+    g.part_rows = part_rows;
+    grid.z = nz * S;
+    RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
+    GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used};
+    RC(launch(K->gemm_reduce, dim3((g.zrows + 255) / 256, part_rows), 0, s, r));
+    *dispatches += 2;
+    return LFM_OK;
 }
 
 // Y[t][r] = sum_k W[r][k] X[t][k] for T token rows (prefill GEMM, op level).
@@ -572,13 +614,23 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     ga.zrows = (uint32_t)rows;
     ga.c = y;
     ga.ldc = (uint32_t)rows;
+    float *part = nullptr;
+    size_t part_cap = 0;
+    if (rc == LFM_OK && T <= GEMM_TOKENS) {
+        part_cap = std::min<size_t>(GEMM_PART_BYTES / 4, (size_t)T * rows * (in_dim / 256));
+        if (hipMalloc(&part, part_cap * 4) != hipSuccess)
+            rc = fail(LFM_EDEVICE, "lfm_q6k_gemm: scratch allocation failed");
+    }
+    uint64_t nd = 0;
     if (rc == LFM_OK)
-        rc = launch_t(K->gemm_q6, gemm_grid((uint32_t)rows, T, 1), GEMM_THREADS, 0, s, ga);
+        rc = launch_gemm(K, s, ga, false, T, 1, T, 0, part, part_cap, &nd);
     if (rc == LFM_OK && hipStreamSynchronize(s) != hipSuccess)
         rc = fail(LFM_EDEVICE, "lfm_q6k_gemm: synchronize failed");
     (void)hipFree(hi);
     (void)hipFree(lo);
     (void)hipFree(scale);
+    if (part)
+        (void)hipFree(part);
     return rc;
 }
 
@@ -650,7 +702,7 @@ struct lfm_engine {
     DevState *host_st = nullptr;    // pinned staging for state copies
     // batched prefill buffers (capacity: ctx tokens per call)
     struct {
-        float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr;
+        float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr, *part = nullptr;
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
         uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr;
@@ -1190,6 +1242,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.y, TC * dim * 4));
         HIPCHK(hipMalloc(&e->pf.g, TC * wide * 4));
         HIPCHK(hipMalloc(&e->pf.d, TC * 4 * dim * 4));
+        HIPCHK(hipMalloc(&e->pf.part, GEMM_PART_BYTES));
         HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));
@@ -1222,7 +1275,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->logits, e->hpart, e->apart, e->rope,
-                    e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.hi, e->pf.lo,
+                    e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot};
     for (void *p : bufs)
@@ -1279,9 +1332,7 @@ static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t l
     g.ldc = ldc;
     g.col0 = col0;
     g.mode = mode;
-    RC(launch_t(e->K->gemm_q6, gemm_grid(w.rows, T, 1), GEMM_THREADS, 0, e->stream, g));
-    e->dispatches += 1;
-    return LFM_OK;
+    return launch_gemm(e->K, e->stream, g, false, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches);
 }
 
 // Gate and up projections of a SwiGLU FFN in one launch: c = silu(Wg x) * (Wu x)
@@ -1302,17 +1353,14 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t 
     g.zrows = zrows;
     g.c = c;
     g.ldc = ldc;
-    uint32_t nz = 1;
-    if (tok) {
-        g.tok = tok;
-        g.slot = e->pf.slot;
-        g.counts = e->pf.counts;
-        g.list_stride = e->ctx;
-        nz = e->hp.n_expert;
-    }
-    RC(launch_t(e->K->gemm_swiglu, gemm_grid(zrows, T, nz, GEMM_ROWS / 2), GEMM_THREADS, 0, e->stream, g));
-    e->dispatches += 1;
-    return LFM_OK;
+    if (!tok)
+        return launch_gemm(e->K, e->stream, g, true, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches);
+    g.tok = tok;
+    g.slot = e->pf.slot;
+    g.counts = e->pf.counts;
+    g.list_stride = e->ctx;
+    return launch_gemm(e->K, e->stream, g, true, T, e->hp.n_expert, 4 * T, e->hp.n_used, e->pf.part,
+                       GEMM_PART_BYTES / 4, &e->dispatches);
 }
 
 // Grouped expert GEMM: z = expert, rows zrows per expert, activation rows from
@@ -1333,9 +1381,8 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t
     g.zrows = zrows;
     g.c = c;
     g.ldc = ldc;
-    RC(launch_t(e->K->gemm_q6, gemm_grid(zrows, T, e->hp.n_expert), GEMM_THREADS, 0, e->stream, g));
-    e->dispatches += 1;
-    return LFM_OK;
+    return launch_gemm(e->K, e->stream, g, false, T, e->hp.n_expert, 4 * T, e->hp.n_used, e->pf.part,
+                       GEMM_PART_BYTES / 4, &e->dispatches);
 }
 
 static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)

@@ -212,6 +212,18 @@ struct GemmArgs {
     uint32_t ntok, list_stride, zrows;
     float *c;
     uint32_t ldc, col0, mode;
+    // split over K (ksplit > 1): grid z = nz groups x ksplit slices; slice s covers
+    // Q6_K blocks [s nb / ksplit, (s + 1) nb / ksplit) and writes its fp32 sums to
+    // part[((s * (pair ? 2 : 1) + weight) * part_rows + out_row) * zrows + row]
+    float *part;
+    uint32_t ksplit, nz, part_rows;
+};
+
+struct GemmReduceArgs {    // c (+)= sum_s part[s] in slice order; pair: silu(g) * u
+    const float *part;
+    float *c;
+    uint32_t ksplit, pair, part_rows, zrows, ldc, col0, mode;
+    uint32_t n_used;       // grouped: out_row = token * 4 + rank, ranks >= n_used unused; 0 = all
 };
 
 struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t

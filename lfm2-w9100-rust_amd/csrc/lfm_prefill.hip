@@ -167,9 +167,10 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 // Workgroup i runs on XCD i % 8; tiles are handed out so that each XCD takes a
 // contiguous run with the weight rows fastest, and the workgroups resident on
 // one XCD share activation tiles in its L2.
-template <bool PAIR>
+template <bool PAIR, int NJ>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 {
+    constexpr uint32_t TNW = 32 * NJ; // token columns per workgroup (128, or 32 for small calls)
     // rows of each weight per workgroup; the workgroup's 256 "tile rows" v are
     // rows m0 + v (single) or rows m0 + (v & 127) of weight v >> 7 (pair)
     constexpr uint32_t TMW = PAIR ? TM / 2 : TM;
@@ -183,7 +184,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         ny = (V / gx) % gy;
         z = V / (gx * gy);
     }
-    const uint32_t m0 = mx * TMW, n0 = ny * TN;
+    // K slice of this workgroup (the whole row unless split)
+    const uint32_t nb = a.w.nb, K = nb * 256;
+    const uint32_t ks = a.ksplit > 1 ? z / a.nz : 0;
+    if (a.ksplit > 1)
+        z -= ks * a.nz;
+    const uint32_t kb0 = a.ksplit > 1 ? ks * nb / a.ksplit : 0;
+    const uint32_t nbl = a.ksplit > 1 ? (ks + 1) * nb / a.ksplit - kb0 : nb;
+    const uint32_t m0 = mx * TMW, n0 = ny * TNW;
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
@@ -192,12 +200,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
     const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
-    __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TN * TK];
-    __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TN * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TNW * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TNW * TK];
     __shared__ float dsh[2][TM], rsh[2][TM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
-    const uint32_t nb = a.w.nb, K = nb * 256;
     const size_t nblk = (size_t)a.w.rows * nb;
     // row tile i of the wave: tile rows vb[i] .. vb[i] + 31, rows lb[i] .. of weight i (pair)
     uint32_t vb[2], lb[2], arow[2];
@@ -210,15 +217,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
     // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
     // k-piece j ^ ((t >> 1) & 7)
-    uint32_t bsrc[4], bkq[4];
+    uint32_t bsrc[NJ], bkq[NJ];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < NJ; ++v) {
         const uint32_t t = (tid + GEMM_NTH * v) >> 3, col = min(n0 + t, ntok - 1);
         bsrc[v] = tokl ? tokl[col] : col;
         bkq[v] = ((tid & 7) ^ ((t >> 1) & 7)) * 8;
     }
-    auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) {
-        const uint32_t kb = half >> 1, h = half & 1;
+    auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) { // half block of the slice
+        const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
@@ -232,11 +239,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
             }
         }
     };
-    auto loadB = [&](uint32_t st) {
+    auto loadB = [&](uint32_t st) { // stage st of the slice
         const uint32_t buf = st & 1;
-        const size_t k = (size_t)st * TK;
+        const size_t k = ((size_t)kb0 * 4 + st) * TK;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
+        for (int v = 0; v < NJ; ++v) {
             const uint32_t u0 = (GEMM_NTH * v + 64 * wave) * 8;
             __builtin_amdgcn_global_load_lds((const void *)(xh + (size_t)bsrc[v] * K + k + bkq[v]),
                                              (__attribute__((address_space(3))) void *)&Bh[buf][u0], 16, 0, 0);
@@ -244,16 +251,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
                                              (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
         }
     };
-    auto loadD = [=](uint32_t kb) -> float { // d of tile row tid
+    auto loadD = [=](uint32_t kb) -> float { // d of tile row tid, block kb of the slice
         const uint8_t *wb = PAIR && tid >= 128 ? a.w2.base : a.w.base;
         const uint32_t row = rbase + min(m0 + (PAIR ? tid & 127 : tid), a.zrows - 1);
-        return half_bits_to_float(reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)row * nb + kb]);
+        return half_bits_to_float(reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)row * nb + kb0 + kb]);
     };
-    floatx16 acc[2][4];
+    floatx16 acc[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.f;
@@ -264,7 +271,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
             for (int e = 0; e < 16; ++e) {
                 const float r = rsh[rb][vb[i] + 8 * (e / 4) + 4 * p + (e % 4)];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NJ; ++j)
                     acc[i][j][e] *= r;
             }
     };
@@ -276,7 +283,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         rsh[slot][tid] = nz ? u / d : 1.0f;
         u = nz ? d : u;
     };
-    const uint32_t nst = nb * 4, nhb = nb * 2; // stages; half block hb = stages 2hb, 2hb + 1
+    const uint32_t nst = nbl * 4, nhb = nbl * 2; // stages; half block hb = stages 2hb, 2hb + 1
     AChunk A[2][2], An[2][2];
     loadA(0, A);
     loadB(0);
@@ -306,16 +313,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
                 const uint32_t kp = ks * 2 + p;
-                half8 afn[2], bfh[4], bfl[4];
+                half8 afn[2], bfh[NJ], bfl[NJ];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     bfh[j] = *reinterpret_cast<const half8 *>(&Bh[q][swz(j * 32 + lr, kp)]);
                     bfl[j] = *reinterpret_cast<const half8 *>(&Bl[q][swz(j * 32 + lr, kp)]);
                 }
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j], acc[i][j], 0, 0, 0);
                 if (ks < 3) {
 #pragma unroll
@@ -325,7 +332,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j], acc[i][j], 0, 0, 0);
                 if (ks < 3) {
 #pragma unroll
@@ -354,12 +361,27 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     __syncthreads();
     rescale(0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const uint32_t n = n0 + j * 32 + lr;
         if (n >= ntok)
             continue;
         const uint32_t orow = slotl ? slotl[n] : n;
         const float xs = a.xscale[tokl ? tokl[n] : n];
+        if (a.ksplit > 1) { // this slice's sums, reduced by k_gemm_reduce
+            constexpr uint32_t NW = PAIR ? 2 : 1;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t wi = PAIR ? i : 0;
+                float *pp = a.part + ((size_t)(ks * NW + wi) * a.part_rows + orow) * a.zrows;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
+                    if (r < a.zrows)
+                        pp[r] = acc[i][j][e] * xs;
+                }
+            }
+            continue;
+        }
         float *out = a.c + (size_t)orow * a.ldc + a.col0;
         if (PAIR) {
 #pragma unroll
@@ -386,13 +408,267 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 k_gemm_q6(const GemmArgs a)
 {
-    gemm_body<false>(a);
+    gemm_body<false, 4>(a);
 }
 
 extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 k_gemm_q6_swiglu(const GemmArgs a)
 {
-    gemm_body<true>(a);
+    gemm_body<true, 4>(a);
+}
+
+// The same products for calls of up to 128 tokens (chunked prefill: about 8
+// tokens per expert at 64 tokens), 32 tokens per workgroup: a quarter of the
+// padded matrix-core work, and every wave runs on its own.  A lane loads its
+// weight rows' Q6_K bytes a half block ahead and its token column's activation
+// fragments (hi, lo) a stage ahead straight into registers; the block scales
+// are exchanged between lanes by shuffles (lane l holds row l's running scale),
+// so there is no LDS tile and no barrier, and each wave waits only for the
+// loads its next instructions use.  Same arithmetic per (row, token) as
+// gemm_body.
+template <bool PAIR>
+__device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
+{
+    constexpr uint32_t TMW = PAIR ? TM / 2 : TM;
+    uint32_t z, mx, ny;
+    {
+        const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+        const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+        const uint32_t q = total / 8, r = total % 8, xcd = L % 8, idx = L / 8;
+        const uint32_t V = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+        mx = V % gx;
+        ny = (V / gx) % gy;
+        z = V / (gx * gy);
+    }
+    const uint32_t nb = a.w.nb, K = nb * 256;
+    const uint32_t ks = a.ksplit > 1 ? z / a.nz : 0;
+    if (a.ksplit > 1)
+        z -= ks * a.nz;
+    const uint32_t kb0 = a.ksplit > 1 ? ks * nb / a.ksplit : 0;
+    const uint32_t nbl = a.ksplit > 1 ? (ks + 1) * nb / a.ksplit - kb0 : nb;
+    const uint32_t m0 = mx * TMW, n0 = ny * 32;
+    const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
+    if (m0 >= a.zrows || n0 >= ntok)
+        return;
+    const uint32_t rbase = z * a.zrows;
+    const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
+    const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
+    const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
+    const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint32_t p = lane >> 5, lr = lane & 31;
+    const size_t nblk = (size_t)a.w.rows * nb;
+    uint32_t lb[2], arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        lb[i] = PAIR ? wave * 32 : wave * 64 + i * 32;
+        arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
+    }
+    const uint32_t col = min(n0 + lr, ntok - 1);
+    const size_t brow = (size_t)(tokl ? tokl[col] : col) * K;
+    auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) {
+        const uint32_t kb = kb0 + (half >> 1), h = half & 1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
+            const size_t blk = (size_t)arow[i] * nb + kb;
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                const uint32_t c = 4 * h + 2 * ch + p;
+                A[i][ch].ql = *reinterpret_cast<const uint4 *>(wb + blk * 128 + c * 16);
+                A[i][ch].qh = *reinterpret_cast<const uint2 *>(wb + nblk * 128 + blk * 64 + c * 8);
+                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(wb + nblk * 192 + blk * 16 + (c >> 1) * 4);
+            }
+        }
+    };
+    // activation fragments of stage st: k-step ks reads k-piece ks * 2 + p
+    auto loadB = [=](uint32_t st, half8 (&bh)[4], half8 (&bl)[4]) {
+        const size_t k = brow + ((size_t)kb0 * 4 + st) * TK;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            bh[q] = *reinterpret_cast<const half8 *>(xh + k + (q * 2 + p) * 8);
+            bl[q] = *reinterpret_cast<const half8 *>(xl + k + (q * 2 + p) * 8);
+        }
+    };
+    auto loadD = [=](uint32_t kb, float (&d)[2]) { // this lane's A rows, block kb of the slice
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
+            d[i] = half_bits_to_float(
+                reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)arow[i] * nb + kb0 + kb]);
+        }
+    };
+    floatx16 acc[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            acc[i][e] = 0.f;
+    // accumulator element e of a lane is row 8 (e / 4) + 4p + e % 4 of its tile,
+    // whose scale lives in lane (that row)
+    auto by_row = [&](int i, float v) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            acc[i][e] *= __shfl(v, 8 * (e / 4) + 4 * p + (e % 4), 64);
+    };
+    float u[2] = {1.0f, 1.0f}, dcur[2], dnext[2] = {0.f, 0.f};
+    auto enter_block = [&](bool first) { // accumulators: sum_b d_b P_b / u
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const bool nz = dcur[i] != 0.f;
+            const float r = nz ? u[i] / dcur[i] : 1.0f;
+            u[i] = nz ? dcur[i] : u[i];
+            if (!first)
+                by_row(i, r);
+        }
+    };
+    const uint32_t nst = nbl * 4, nhb = nbl * 2;
+    AChunk A[2][2], An[2][2];
+    half8 bch[4], bcl[4], bnh[4], bnl[4];
+    loadA(0, A);
+    loadD(0, dcur);
+    loadB(0, bch, bcl);
+    enter_block(true);
+    for (uint32_t hb = 0; hb < nhb; ++hb) {
+        if ((hb & 1) == 0 && hb > 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                dcur[i] = dnext[i];
+            enter_block(false);
+        }
+        bool zero[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            zero[i] = dcur[i] == 0.f;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t st = hb * 2 + q;
+            // Loads retire in issue order: the next stage's activations go first, so
+            // waiting for them does not wait for the next half block's weights and
+            // scales, issued after them and used two stages later.
+            if (st + 1 < nst)
+                loadB(st + 1, bnh, bnl);
+            if (q == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (hb + 1 < nhb)
+                    loadA(hb + 1, An);
+                if ((hb & 1) == 0 && hb + 2 < nhb)
+                    loadD((hb >> 1) + 1, dnext);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            half8 afc[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) {
+                half8 afn[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bch[kq], acc[i], 0, 0, 0);
+                if (kq < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), zero[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bcl[kq], acc[i], 0, 0, 0);
+                if (kq < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        afc[i] = afn[i];
+                }
+            }
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq)
+                bch[kq] = bnh[kq], bcl[kq] = bnl[kq];
+        }
+        if (hb + 1 < nhb) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch)
+                    A[i][ch] = An[i][ch];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        by_row(i, u[i]);
+    const uint32_t n = n0 + lr;
+    if (n >= ntok)
+        return;
+    const uint32_t orow = slotl ? slotl[n] : n;
+    const float xs = a.xscale[tokl ? tokl[n] : n];
+    if (a.ksplit > 1) {
+        constexpr uint32_t NW = PAIR ? 2 : 1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float *pp = a.part + ((size_t)(ks * NW + (PAIR ? i : 0)) * a.part_rows + orow) * a.zrows;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
+                if (r < a.zrows)
+                    pp[r] = acc[i][e] * xs;
+            }
+        }
+        return;
+    }
+    float *out = a.c + (size_t)orow * a.ldc + a.col0;
+    if (PAIR) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t r = m0 + lb[0] + 8 * (e / 4) + 4 * p + (e % 4);
+            const float g = acc[0][e] * xs, uu = acc[1][e] * xs;
+            if (r < a.zrows)
+                out[r] = g / (1.0f + expf(-g)) * uu;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
+            const float v = acc[i][e] * xs;
+            if (r < a.zrows)
+                out[r] = a.mode ? out[r] + v : v;
+        }
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32(const GemmArgs a)
+{
+    gemm_small_body<false>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32(const GemmArgs a)
+{
+    gemm_small_body<true>(a);
+}
+
+// Sums the K slices of a split GEMM in slice order and applies its epilogue:
+// c = v, c += v (mode 1), or silu(g) * u for the pair form.  One thread per
+// output element (row blockIdx.x * 256 + tid of output row blockIdx.y).
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_reduce(const GemmReduceArgs a)
+{
+    const uint32_t r = blockIdx.x * WG_THREADS + threadIdx.x, orow = blockIdx.y;
+    if (r >= a.zrows || (a.n_used && orow % 4 >= a.n_used))
+        return;
+    const size_t slice = (size_t)a.part_rows * a.zrows, at = (size_t)orow * a.zrows + r;
+    float *out = a.c + (size_t)orow * a.ldc + a.col0 + r;
+    if (a.pair) {
+        float g = a.part[at], u = a.part[slice + at];
+        for (uint32_t s = 1; s < a.ksplit; ++s) {
+            g += a.part[2 * s * slice + at];
+            u += a.part[(2 * s + 1) * slice + at];
+        }
+        *out = g / (1.0f + expf(-g)) * u;
+        return;
+    }
+    float v = a.part[at];
+    for (uint32_t s = 1; s < a.ksplit; ++s)
+        v += a.part[s * slice + at];
+    *out = a.mode ? *out + v : v;
 }
 // ------------------------------------------------------------------ short conv
 // The LFM2 short conv keeps only the previous two values of bx = B*X, so each
