@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, attn_merge_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -235,6 +235,7 @@ static int get_kernels(Kernels **out)
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
+                {&k->attn_merge_split, "k_attn_merge_split"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
@@ -1408,8 +1409,28 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
                  start, hp.heads, kv, e->ctx};
     RC(launch(e->K->rope_kv_prefill, dim3(T), 0, e->stream, r));
     AttnPrefillArgs at{e->pf.bcx, e->kc[l], e->vc[l], e->pf.y, 1.0f / sqrtf((float)hp.head_dim), T,
-                       start, hp.heads, kv, e->ctx};
-    RC(launch(e->K->attn_prefill, dim3((T + 31) / 32, kv), 0, e->stream, at));
+                       start, hp.heads, kv, e->ctx, nullptr, 0};
+    // Few query tiles (small calls, e.g. 64-token chunks late in the context): the
+    // keys are split into ranges (about 256 workgroups, at least 4 blocks of 32
+    // keys each) whose softmax states k_attn_merge_split combines.
+    const uint32_t qtiles = (T + 31) / 32, nblk_max = (start + T - 1) / 32 + 1;
+    uint32_t nsplit = 1, kb_per = 0;
+    if (qtiles * kv < 128 && nblk_max >= 8) {
+        kb_per = std::max<uint32_t>(4, (nblk_max * qtiles * kv + 255) / 256);
+        nsplit = (nblk_max + kb_per - 1) / kb_per;
+        if ((size_t)nsplit * T * hp.heads * 66 * 4 > GEMM_PART_BYTES)
+            nsplit = 1, kb_per = 0;
+    }
+    if (nsplit > 1) {
+        at.part = e->pf.part;
+        at.kb_per = kb_per;
+        RC(launch(e->K->attn_prefill, dim3(qtiles, kv, nsplit), 0, e->stream, at));
+        AttnMergeSplitArgs mg{e->pf.part, e->pf.y, T, hp.heads, nsplit};
+        RC(launch(e->K->attn_merge_split, dim3(T, (hp.heads + 3) / 4), 0, e->stream, mg));
+        e->dispatches += 1;
+    } else {
+        RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
+    }
     RC(pf_split(e, e->pf.y, nullptr, T, dim));
     RC(pf_gemm(e, q6(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
     e->dispatches += 2;

@@ -248,6 +248,16 @@ struct AttnPrefillArgs {  // causal GQA attention of T queries at positions star
     float *out;           // [T][dim]
     float scale;
     uint32_t T, start, heads, kv, ctx;
+    // key split (kb_per > 0): grid z = key ranges of kb_per 32-key blocks; range s
+    // writes (max, sum, o[64]) of each (query, head) to part[((s T + t) heads + h) 66]
+    float *part;
+    uint32_t kb_per;
+};
+
+struct AttnMergeSplitArgs { // out[t][h] = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s
+    const float *part;
+    float *out;
+    uint32_t T, heads, nsplit;
 };
 
 struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)

@@ -796,13 +796,17 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
     }
     const uint32_t qpos = a.start + tq; // causal limit of this lane's query
     const uint32_t tmax = min(t0 + FA_Q, a.T) - 1;
-    const uint32_t nblk = (a.start + tmax) / FA_K + 1;
+    // key blocks [kb_lo, kb_hi) of this workgroup: all the causal ones, or one range
+    const uint32_t nblk_all = (a.start + tmax) / FA_K + 1;
+    const uint32_t kb_lo = a.kb_per ? blockIdx.z * a.kb_per : 0;
+    const uint32_t kb_hi = a.kb_per ? min(nblk_all, kb_lo + a.kb_per) : nblk_all;
+    const uint32_t nblk = kb_hi > kb_lo ? kb_hi - kb_lo : 0;
     // staging: thread -> key row tid / 8, dims (tid % 8) * 8 .. +7
     const uint32_t sr = tid >> 3, sp = (tid & 7) * 8;
     const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
     const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
-    auto load_kv = [&](uint32_t blk, uint4 &kr, uint4 &vr) {
-        const uint32_t pos = min(blk * FA_K + sr, a.ctx - 1);
+    auto load_kv = [&](uint32_t blk, uint4 &kr, uint4 &vr) { // blk counts from kb_lo
+        const uint32_t pos = min((kb_lo + blk) * FA_K + sr, a.ctx - 1);
         kr = *reinterpret_cast<const uint4 *>(kg + (size_t)pos * 64 + sp);
         vr = *reinterpret_cast<const uint4 *>(vg + (size_t)pos * 64 + sp);
     };
@@ -819,8 +823,10 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
         o0[e] = 0.f, o1[e] = 0.f;
     float m = -INFINITY, l = 0.f;
     uint4 kr, vr;
-    load_kv(0, kr, vr);
-    store_kv(0, kr, vr);
+    if (nblk > 0) {
+        load_kv(0, kr, vr);
+        store_kv(0, kr, vr);
+    }
     if (nblk > 1)
         load_kv(1, kr, vr);
     __syncthreads();
@@ -842,7 +848,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
             float bm = -INFINITY;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t kpos = blk * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
+                const uint32_t kpos = (kb_lo + blk) * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
                 if (kpos > qpos)
                     sacc[e] = -INFINITY;
                 bm = fmaxf(bm, sacc[e]);
@@ -885,6 +891,20 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
     }
     if (!active || tq >= a.T)
         return;
+    if (a.kb_per) { // this key range's softmax state, merged by k_attn_merge_split
+        float *pp = a.part + (((size_t)blockIdx.z * a.T + tq) * a.heads + h) * 66;
+        if (lh == 0) {
+            pp[0] = m;
+            pp[1] = l;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
+            pp[2 + d] = o0[e];
+            pp[2 + 32 + d] = o1[e];
+        }
+        return;
+    }
     const float rl = 1.0f / l;
     float *orow = a.out + (size_t)tq * dim + h * 64;
 #pragma unroll
@@ -893,6 +913,29 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
         orow[d] = o0[e] * rl;
         orow[32 + d] = o1[e] * rl;
     }
+}
+
+// Combines the key ranges of a split prefill attention: for (query t, head h),
+// out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s (scores in log2 units).
+// Workgroup: one query, four heads (thread: head tid / 64, dim tid % 64).
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge_split(const AttnMergeSplitArgs a)
+{
+    const uint32_t t = blockIdx.x, h = blockIdx.y * 4 + (threadIdx.x >> 6), d = threadIdx.x & 63;
+    if (t >= a.T || h >= a.heads)
+        return;
+    const size_t stride = (size_t)a.T * a.heads * 66;
+    const float *pb = a.part + ((size_t)t * a.heads + h) * 66;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < a.nsplit; ++s)
+        M = fmaxf(M, pb[s * stride]);
+    float num = 0.f, den = 0.f;
+    for (uint32_t s = 0; s < a.nsplit; ++s) {
+        const float ms = pb[s * stride];
+        const float f = ms > -INFINITY ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+        den += f * pb[s * stride + 1];
+        num += f * pb[s * stride + 2 + d];
+    }
+    a.out[(size_t)t * a.heads * 64 + h * 64 + d] = num / den;
 }
 
 // ------------------------------------------------------------------ FFN pieces

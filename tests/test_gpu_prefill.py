@@ -106,3 +106,31 @@ def test_prefill_chunks_then_decode(gpu, oracle, real_width):
             compared += 1
         feed = toks[s]
     assert compared >= steps // 2
+
+
+def test_prefill_64_token_chunks(gpu, oracle, real_width):
+    """A 448-token prompt in 64-token chunks (api_stream.rs:57-63, work_bound.rs
+    PREFILL_CHUNK): calls of up to 128 tokens take the split-K GEMM with 32-token
+    tiles, and chunks from position 192 on split attention over key ranges.  The
+    last logits and the resident state match the oracle and the engine's own
+    whole-prompt forward."""
+    hp, tensors = real_width
+    n = 448
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, hp.vocab, n)]
+    g = gpu_engine(hp, tensors, ctx=512)
+    for s in range(0, n, 64):
+        lg = g.forward(prompt[s:s + 64], s)
+    o = oracle_engine(oracle, hp, tensors, ctx=512)
+    lo = o.forward(prompt, 0)
+    err = rel_l2(lg, lo)
+    sg = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    so = np.frombuffer(o.snapshot(n), np.float32)
+    serr = rel_l2(sg, so)
+    print(f"64-token chunks: logits rel-L2 {err:.3e}, state rel-L2 {serr:.3e}")
+    assert err <= 1e-3
+    assert serr <= 1e-3
+    w = gpu_engine(hp, tensors, ctx=512)
+    lw = w.forward(prompt, 0)
+    assert rel_l2(lg, lw) <= 1e-3
+    sw = np.frombuffer(w.snapshot_resident_cache(n), np.float32)
+    assert rel_l2(sg, sw) <= 1e-3
