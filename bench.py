@@ -191,6 +191,21 @@ def main():
     log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tok_s:.1f} tok/s, "
         f"{decode_gbs:.0f} GB/s algorithmic")
 
+    chunked = None
+    if not args.synthetic_state:
+        # the same prompt as 64-token lfm_forward_token calls, the chunking the
+        # reference's api_stream uses (work_bound.rs PREFILL_CHUNK)
+        eng.reset_session()
+        lfm_hip.lib().lfm_dev_synchronize()
+        t = time.perf_counter()
+        for s0 in range(0, n_prompt, 64):
+            nxt = eng.forward_token(prompt[s0:s0 + 64], s0)
+        lfm_hip.lib().lfm_dev_synchronize()
+        cs = time.perf_counter() - t
+        chunked = {"tokens": n_prompt, "chunk": 64, "ms": round(cs * 1e3, 1),
+                   "tok_s": round(n_prompt / cs, 1), "next_token_equals_whole_prompt": nxt == first}
+        log(f"[bench] prefill {n_prompt} tokens in 64-token chunks: {cs * 1e3:.1f} ms")
+
     roof = None
     extra = {}
     if not args.no_roofline:
@@ -259,6 +274,7 @@ def main():
             "mfma_frac": round(pf_flops / prefill_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "note": "algorithmic FLOPs (projections, router, causal attention, last-token head); "
                     "each GEMM product runs as two binary16 matrix-core passes (hi, lo)"},
+        "prefill_chunked": chunked,
         **extra,
     }
     print(json.dumps(line), flush=True)

@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, attn_merge_split, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -235,7 +235,7 @@ static int get_kernels(Kernels **out)
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
-                {&k->attn_merge_split, "k_attn_merge_split"},
+                {&k->attn_merge_split, "k_attn_merge_split"}, {&k->router_small, "k_router_prefill_small"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
@@ -1455,7 +1455,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
     RouterPrefillArgs ra{x, norm, f32(e, "blk.%u.ffn_gate_inp.weight", l), hp.eps, e->pf.logits, T,
                          dim, E};
-    RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
+    if (T <= GEMM_TOKENS) // few tokens: one workgroup per (expert, token)
+        RC(launch(e->K->router_small, dim3(E, T), 0, e->stream, ra));
+    else
+        RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
     RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
                       e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx};
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));

@@ -1047,6 +1047,45 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const 
         }
 }
 
+// Router logits for calls of up to 128 tokens: one workgroup per (expert, token)
+// (grid n_expert x T), thread tid covering inputs 8 tid .. 8 tid + 7 of the
+// token's x . w (dim <= 2048), so the workgroup also sums x^2 for the RMSNorm
+// scale; logits = inv * dot.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill_small(const RouterPrefillArgs a)
+{
+    __shared__ float red[2][4];
+    const uint32_t e = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    if (e >= a.n_expert || t >= a.T)
+        return;
+    const float *x = a.x + (size_t)t * a.dim, *w = a.w + (size_t)e * a.dim;
+    float ss = 0.f, dot = 0.f;
+    for (uint32_t k = tid * 8; k < a.dim; k += WG_THREADS * 8) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float4 x4 = *reinterpret_cast<const float4 *>(x + k + 4 * h);
+            const float4 n4 = *reinterpret_cast<const float4 *>(a.norm_w + k + 4 * h);
+            const float4 w4 = *reinterpret_cast<const float4 *>(w + k + 4 * h);
+            ss += x4.x * x4.x + x4.y * x4.y + x4.z * x4.z + x4.w * x4.w;
+            dot = fmaf(x4.x * n4.x, w4.x, dot);
+            dot = fmaf(x4.y * n4.y, w4.y, dot);
+            dot = fmaf(x4.z * n4.z, w4.z, dot);
+            dot = fmaf(x4.w * n4.w, w4.w, dot);
+        }
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = ss;
+        red[1][tid >> 6] = dot;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float tss = ((red[0][0] + red[0][1]) + red[0][2]) + red[0][3];
+        const float td = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+        a.logits[(size_t)t * a.n_expert + e] = td / sqrtf(tss / (float)a.dim + a.eps);
+    }
+}
+
 // Top-k per token (the decode routing rule, wave_route): one wave per token
 // stores the selected ids and weights [t][4] (unused ranks: id 0, weight 0).
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_topk(const RouteGroupArgs a)
