@@ -166,7 +166,9 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 //     and the epilogue multiplies by the final u.
 // Workgroup i runs on XCD i % 8; tiles are handed out so that each XCD takes a
 // contiguous run with the weight rows fastest, and the workgroups resident on
-// one XCD share activation tiles in its L2.
+// one XCD share activation tiles in its L2.  With ksplit > 1 the grid's z also
+// enumerates K slices: a workgroup runs its slice's blocks only and writes its
+// sums to part, which k_gemm_reduce adds up in slice order.
 template <bool PAIR, int NJ>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 {
