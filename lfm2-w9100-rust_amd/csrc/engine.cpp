@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -235,7 +235,7 @@ static int get_kernels(Kernels **out)
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
-                {&k->attn_merge_split, "k_attn_merge_split"}, {&k->router_small, "k_router_prefill_small"},
+                {&k->attn_merge_split, "k_attn_merge_split"}, {&k->reduce_combine, "k_reduce_combine"}, {&k->router_small, "k_router_prefill_small"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
@@ -557,8 +557,11 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 // k_gemm_reduce adds the slices in order.  part_rows: output rows the GEMM can
 // write (T, or 4T for expert slots); n_used: ranks per token of the expert slots.
 static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
-                       uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches)
+                       uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches,
+                       const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr)
 {
+    if (combined)
+        *combined = false;
     const bool small = T <= GEMM_TOKENS;
     dim3 grid = gemm_grid(g.zrows, T, nz, pair ? GEMM_ROWS / 2 : GEMM_ROWS, small ? 32 : GEMM_TOKENS);
     uint32_t S = 1;
@@ -580,8 +583,14 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     g.part_rows = part_rows;
     grid.z = nz * S;
     RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
-    GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used};
-    RC(launch(K->gemm_reduce, dim3((g.zrows + 255) / 256, part_rows), 0, s, r));
+    if (combine) { // grouped down projection: slices and the rank combine in one pass
+        ReduceCombineArgs rc{part, combine->wsel, combine->x, S, combine->T, combine->dim, combine->n_used};
+        RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
+        *combined = true;
+    } else {
+        GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used};
+        RC(launch(K->gemm_reduce, dim3((g.zrows + 255) / 256, part_rows), 0, s, r));
+    }
     *dispatches += 2;
     return LFM_OK;
 }
@@ -1367,7 +1376,8 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t 
 // Grouped expert GEMM: z = expert, rows zrows per expert, activation rows from
 // `tok`, output rows `slot`, counts per expert on the device.
 static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t T,
-                           const uint32_t *tok, float *c, uint32_t ldc)
+                           const uint32_t *tok, float *c, uint32_t ldc,
+                           const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -1383,7 +1393,7 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t
     g.c = c;
     g.ldc = ldc;
     return launch_gemm(e->K, e->stream, g, false, T, e->hp.n_expert, 4 * T, e->hp.n_used, e->pf.part,
-                       GEMM_PART_BYTES / 4, &e->dispatches);
+                       GEMM_PART_BYTES / 4, &e->dispatches, combine, combined);
 }
 
 static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
@@ -1467,10 +1477,13 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), q6(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff)); // slots are token * 4 + rank
-    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim));
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
-    RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread
-    e->dispatches += 4;
+    bool combined = false;
+    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,
+                       &combined));
+    if (!combined)
+        RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread
+    e->dispatches += combined ? 3 : 4;
     return LFM_OK;
 }
 

@@ -226,6 +226,13 @@ struct GemmReduceArgs {    // c (+)= sum_s part[s] in slice order; pair: silu(g)
     uint32_t n_used;       // grouped: out_row = token * 4 + rank, ranks >= n_used unused; 0 = all
 };
 
+struct ReduceCombineArgs { // x[t] += sum_r w[t][r] * (sum_s part[s][t*4 + r]), rank then slice order
+    const float *part;       // [ksplit][T*4][dim]
+    const float *wsel;       // [T][4]
+    float *x;                // [T][dim]
+    uint32_t ksplit, T, dim, n_used;
+};
+
 struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t
     const float *bcx;     // [T][3*dim] in_proj rows B, C, X
     const float *conv_w;  // [dim][3]

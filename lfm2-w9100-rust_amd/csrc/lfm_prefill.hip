@@ -1182,6 +1182,28 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_combine_prefill(const
     *xp = make_float4(x0.x + sm.x, x0.y + sm.y, x0.z + sm.z, x0.w + sm.w);
 }
 
+// The expert down projection's K slices and the combine in one pass (split-K
+// calls): d = sum_s part[s] in slice order, then k_combine_prefill's
+// x += ((0 + d_0 w_0) + d_1 w_1) + ... in rank order, no contraction.
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_reduce_combine(const ReduceCombineArgs a)
+{
+#pragma clang fp contract(off)
+    const uint32_t k = blockIdx.x * WG_THREADS + threadIdx.x, t = blockIdx.y;
+    if (k >= a.dim || t >= a.T)
+        return;
+    const size_t slice = (size_t)a.T * 4 * a.dim;
+    float sm = 0.0f;
+    for (uint32_t r = 0; r < a.n_used; ++r) {
+        const size_t at = ((size_t)t * 4 + r) * a.dim + k;
+        float d = a.part[at];
+        for (uint32_t s = 1; s < a.ksplit; ++s)
+            d += a.part[s * slice + at];
+        sm = sm + d * a.wsel[(size_t)t * 4 + r];
+    }
+    float *x = a.x + (size_t)t * a.dim + k;
+    *x = *x + sm;
+}
+
 // Token embeddings of T ids (lfm.rs:310-320): row ids[t] of the Q6_K table,
 // dequantized exactly; one wave per row (8 lanes per 256-wide block).
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_embed_rows(const EmbedRowsArgs a)
