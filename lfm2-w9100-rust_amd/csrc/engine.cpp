@@ -106,7 +106,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -235,6 +235,7 @@ static int get_kernels(Kernels **out)
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
+                {&k->gemm_q6_t32n1, "k_gemm_q6_t32n1"},
                 {&k->attn_merge_split, "k_attn_merge_split"}, {&k->reduce_combine, "k_reduce_combine"}, {&k->router_small, "k_router_prefill_small"},
                 {&k->embed_rows, "k_embed_rows"}};
     for (auto &f : pfns) {
@@ -563,7 +564,9 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     if (combined)
         *combined = false;
     const bool small = T <= GEMM_TOKENS;
-    dim3 grid = gemm_grid(g.zrows, T, nz, pair ? GEMM_ROWS / 2 : GEMM_ROWS, small ? 32 : GEMM_TOKENS);
+    // small ungrouped projections of up to 2048 rows: one 32-row tile per wave
+    const bool one_tile = small && !pair && nz == 1 && g.zrows <= 2048;
+    dim3 grid = gemm_grid(g.zrows, T, nz, pair || one_tile ? GEMM_ROWS / 2 : GEMM_ROWS, small ? 32 : GEMM_TOKENS);
     uint32_t S = 1;
     if (part && small) {
         const uint32_t wgs = grid.x * grid.y * grid.z;
@@ -571,7 +574,8 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         S = std::min<uint32_t>(std::max<uint32_t>(1, 1024 / wgs), g.w.nb);
         S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, part_cap / per));
     }
-    hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : K->gemm_q6_t32) : (pair ? K->gemm_swiglu : K->gemm_q6);
+    hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
+                            : (pair ? K->gemm_swiglu : K->gemm_q6);
     if (S == 1) {
         RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
         *dispatches += 1;

@@ -427,11 +427,12 @@ k_gemm_q6_swiglu(const GemmArgs a)
 // are exchanged between lanes by shuffles (lane l holds row l's running scale),
 // so there is no LDS tile and no barrier, and each wave waits only for the
 // loads its next instructions use.  Same arithmetic per (row, token) as
-// gemm_body.
-template <bool PAIR>
+// gemm_body.  NI: 32-row tiles per wave (the pair form: its gate and up tile).
+template <bool PAIR, int NI>
 __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 {
-    constexpr uint32_t TMW = PAIR ? TM / 2 : TM;
+    static_assert(!PAIR || NI == 2, "the pair form holds a gate and an up tile per wave");
+    constexpr uint32_t TMW = PAIR ? TM / 2 : 128 * NI; // rows of each weight per workgroup
     uint32_t z, mx, ny;
     {
         const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
@@ -460,18 +461,18 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
     const size_t nblk = (size_t)a.w.rows * nb;
-    uint32_t lb[2], arow[2];
+    uint32_t lb[NI], arow[NI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        lb[i] = PAIR ? wave * 32 : wave * 64 + i * 32;
+    for (int i = 0; i < NI; ++i) {
+        lb[i] = PAIR ? wave * 32 : wave * 32 * NI + i * 32;
         arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
     }
     const uint32_t col = min(n0 + lr, ntok - 1);
     const size_t brow = (size_t)(tokl ? tokl[col] : col) * K;
-    auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) {
+    auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
             const size_t blk = (size_t)arow[i] * nb + kb;
 #pragma unroll
@@ -492,17 +493,17 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             bl[q] = *reinterpret_cast<const half8 *>(xl + k + (q * 2 + p) * 8);
         }
     };
-    auto loadD = [=](uint32_t kb, float (&d)[2]) { // this lane's A rows, block kb of the slice
+    auto loadD = [=](uint32_t kb, float (&d)[NI]) { // this lane's A rows, block kb of the slice
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
             d[i] = half_bits_to_float(
                 reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)arow[i] * nb + kb0 + kb]);
         }
     };
-    floatx16 acc[2];
+    floatx16 acc[NI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
             acc[i][e] = 0.f;
@@ -513,10 +514,13 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         for (int e = 0; e < 16; ++e)
             acc[i][e] *= __shfl(v, 8 * (e / 4) + 4 * p + (e % 4), 64);
     };
-    float u[2] = {1.0f, 1.0f}, dcur[2], dnext[2] = {0.f, 0.f};
+    float u[NI], dcur[NI], dnext[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        u[i] = 1.0f, dnext[i] = 0.f;
     auto enter_block = [&](bool first) { // accumulators: sum_b d_b P_b / u
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const bool nz = dcur[i] != 0.f;
             const float r = nz ? u[i] / dcur[i] : 1.0f;
             u[i] = nz ? dcur[i] : u[i];
@@ -525,7 +529,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         }
     };
     const uint32_t nst = nbl * 4, nhb = nbl * 2;
-    AChunk A[2][2], An[2][2];
+    AChunk A[NI][2], An[NI][2];
     half8 bch[4], bcl[4], bnh[4], bnl[4];
     loadA(0, A);
     loadD(0, dcur);
@@ -534,13 +538,13 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     for (uint32_t hb = 0; hb < nhb; ++hb) {
         if ((hb & 1) == 0 && hb > 0) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NI; ++i)
                 dcur[i] = dnext[i];
             enter_block(false);
         }
-        bool zero[2];
+        bool zero[NI];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NI; ++i)
             zero[i] = dcur[i] == 0.f;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -558,27 +562,27 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                     loadD((hb >> 1) + 1, dnext);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            half8 afc[2];
+            half8 afc[NI];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NI; ++i)
                 afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
 #pragma unroll
             for (int kq = 0; kq < 4; ++kq) {
-                half8 afn[2];
+                half8 afn[NI];
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < NI; ++i)
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bch[kq], acc[i], 0, 0, 0);
                 if (kq < 3) {
 #pragma unroll
-                    for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < NI; ++i)
                         afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), zero[i]);
                 }
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < NI; ++i)
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bcl[kq], acc[i], 0, 0, 0);
                 if (kq < 3) {
 #pragma unroll
-                    for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < NI; ++i)
                         afc[i] = afn[i];
                 }
             }
@@ -588,14 +592,14 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         }
         if (hb + 1 < nhb) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
                 for (int ch = 0; ch < 2; ++ch)
                     A[i][ch] = An[i][ch];
         }
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
         by_row(i, u[i]);
     const uint32_t n = n0 + lr;
     if (n >= ntok)
@@ -605,7 +609,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     if (a.ksplit > 1) {
         constexpr uint32_t NW = PAIR ? 2 : 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             float *pp = a.part + ((size_t)(ks * NW + (PAIR ? i : 0)) * a.part_rows + orow) * a.zrows;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -621,14 +625,14 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const uint32_t r = m0 + lb[0] + 8 * (e / 4) + 4 * p + (e % 4);
-            const float g = acc[0][e] * xs, uu = acc[1][e] * xs;
+            const float g = acc[0][e] * xs, uu = acc[NI - 1][e] * xs;
             if (r < a.zrows)
                 out[r] = g / (1.0f + expf(-g)) * uu;
         }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
@@ -640,12 +644,20 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32(const GemmArgs a)
 {
-    gemm_small_body<false>(a);
+    gemm_small_body<false, 2>(a);
 }
 
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32(const GemmArgs a)
 {
-    gemm_small_body<true>(a);
+    gemm_small_body<true, 2>(a);
+}
+
+// One 32-row tile per wave (128 rows per workgroup, 144 VGPRs: three waves per
+// SIMD): faster for the ungrouped projections of up to 2048 rows at 64 tokens,
+// slower for the expert and 6144-row shapes.
+extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32n1(const GemmArgs a)
+{
+    gemm_small_body<false, 1>(a);
 }
 
 // Sums the K slices of a split GEMM in slice order and applies its epilogue:
