@@ -705,6 +705,7 @@ struct lfm_engine {
     float *x = nullptr, *y = nullptr, *qkv = nullptr, *sw = nullptr, *rlogits = nullptr,
           *logits = nullptr, *hpart = nullptr, *apart = nullptr;
     float *rpart = nullptr; // fused router partial sums [ROUTE_EXPERTS + 1][ROUTE_PARTS]
+    float *xw = nullptr;    // fused router: the new residual times the FFN norm weight [dim]
     std::vector<uint16_t *> kc, vc;
     // attention layers: attn_q, attn_k and attn_v rows concatenated into one
     // Q6_K tensor (plane layout), so prefill projects q, k, v in one GEMM
@@ -919,6 +920,7 @@ static int launch_out_proj(lfm_engine *e, uint32_t l, MatvecArgs &m, bool fuse)
     ra.rw = f32(e, "blk.%u.ffn_gate_inp.weight", l);
     ra.rnorm = f32(e, "blk.%u.ffn_norm.weight", l);
     ra.rpart = e->rpart;
+    ra.xw = e->xw;
     return launch_t(e->K->matvec_route, dim3(ROUTE_PARTS), 64 * ROUTE_ROWS, 0, e->stream, ra);
 }
 
@@ -1057,6 +1059,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
     if (fused) {
         g.route.logits = nullptr;
         g.route.rpart = e->rpart;
+        g.route.xw = e->xw;
         RC(launch_gateup_fused(e, g));
     } else {
         RC(launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, g));
@@ -1203,6 +1206,9 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMalloc(&e->sw, swn * 4));
     HIPCHK(hipMalloc(&e->rlogits, 64 * 4));
     HIPCHK(hipMalloc(&e->rpart, (ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4));
+    HIPCHK(hipMalloc(&e->xw, ROUTE_WIDTH * 4));
+    HIPCHK(hipMemset(e->rpart, 0, (ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4));
+    HIPCHK(hipMemset(e->xw, 0, ROUTE_WIDTH * 4));
     HIPCHK(hipMalloc(&e->logits, (size_t)hp.vocab * 4));
     HIPCHK(hipMemset(e->logits, 0, (size_t)hp.vocab * 4));
     HIPCHK(hipMalloc(&e->hpart, e->head_grid * 2 * 4));
@@ -1288,7 +1294,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (auto &kv : e->tensors)
         (void)hipFree(kv.second.dev);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
-                    e->rlogits, e->rpart, e->logits, e->hpart, e->apart, e->rope,
+                    e->rlogits, e->rpart, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot};
@@ -1785,6 +1791,7 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
             if (fused) {
                 a.route.logits = nullptr;
                 a.route.rpart = e->rpart;
+                a.route.xw = e->xw;
                 rc = launch_gateup_fused(e, a);
             } else {
                 rc = launch_shape(e->K->gateup, hp.n_used * hp.expert_ff, e->stream, a);

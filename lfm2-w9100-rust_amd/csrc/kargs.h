@@ -107,6 +107,7 @@ struct Route {
     uint32_t n_expert, n_used;
     uint32_t *sel_out;   // written by one wave: ids[8] then weights[8] (float bits)
     const float *rpart;  // fused router: [ROUTE_EXPERTS + 1][ROUTE_PARTS] partial sums
+    const float *xw;     // fused router: x_new * w_norm, the FFN's input before 1/rms [width]
 };
 
 // Fused router (the model's 32 experts at width 2048): the output projection
@@ -125,6 +126,7 @@ struct MatvecRouteArgs { // y += W x (mode 1) and the router partial sums of the
     const float *rw;     // router weights [ROUTE_EXPERTS][rows] f32
     const float *rnorm;  // RMSNorm weight of the FFN input [rows]
     float *rpart;        // [ROUTE_EXPERTS + 1][ROUTE_PARTS]
+    float *xw;           // [rows]: y_new * rnorm, read by the gate/up kernel
 };
 
 struct GateUpArgs {      // sw = silu(Wg h) * (Wu h), dense or routed

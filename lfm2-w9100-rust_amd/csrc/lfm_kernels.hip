@@ -364,7 +364,8 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArg
 // (row r) loads R[e][r] for e = lane % 32 and w_norm[r] with its weights; once
 // its y[r] is known, lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32
 // y[r]^2, and wave 0 adds the workgroup's rows in order, leaving the partials
-// column-major in rpart for k_gateup8f.  The grid is exactly rows / ROUTE_ROWS.
+// column-major in rpart for k_gateup8f.  Lane 0 also stores y[r] * w_norm[r]
+// in xw, the gate/up kernel's input.  The grid is exactly rows / ROUTE_ROWS.
 extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(const MatvecRouteArgs ra)
 {
     const MatvecArgs &a = ra.m;
@@ -391,8 +392,10 @@ extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(
     lanex_lds(X, xs, b, c, active);
     const float p = wave_sum(active ? lane_dot(w, X) : 0.f);
     const float v = yold + inv * p;
-    if (lane == 0)
+    if (lane == 0) {
         a.y[r] = v;
+        ra.xw[r] = v * nwr;
+    }
     if (lane < ROUTE_EXPERTS)
         part[wave][lane] = rwe * (v * nwr);
     else if (lane == ROUTE_EXPERTS)
@@ -928,14 +931,15 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
 // FUSED: the router logits are the sums of the partials left by
-// k_q6_matvec_route (256 threads: thread t adds float4 t + 256k, k < 4, of the
-// 32 expert columns and float4 t % 32 of the x^2 column, then each half-wave
-// sums one column), logit = dot / sqrt(sum x^2 / n + eps) as in k_router.
+// k_q6_matvec_route (each thread adds float4s of the 32 expert columns and one
+// of the x^2 column, then a wave or half-wave sums one column), logit = dot /
+// sqrt(sum x^2 / n + eps) as in k_router.  Its input needs no staging: each
+// lane loads its 32 values of xw = x_new * w_norm (stored by k_q6_matvec_route)
+// along with the partials, and 1 / rms comes from the x^2 column.
 // Routed: work item (rank, row) reads expert ids[rank]'s rows.  The router
 // logits are the first load; every wave computes the routing itself as soon as
-// they arrive and issues its weight loads, so the weight stream starts before
-// the input vector is staged.  Workgroup 0 stores the routing (ids, weight
-// bits) for the down projection.  Dense: the weight loads go out first.
+// they arrive and issues its weight loads.  Workgroup 0 stores the routing (ids,
+// weight bits) for the down projection.  Dense: the weight loads go out first.
 template <int NW, int G, bool FUSED>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
@@ -966,7 +970,11 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     }
     RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
     XRaw raw;
-    x_issue(a.src, n, a.st, raw);
+    LaneX X;
+    if constexpr (FUSED)
+        load_lanex(X, a.route.xw, b, c); // n = 2048: every lane is active
+    else
+        x_issue(a.src, n, a.st, raw);
     if constexpr (FUSED) {
         float f[NK + 1];
 #pragma unroll
@@ -1022,7 +1030,10 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
         }
         if (halted)
             return;
-        inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
+        if constexpr (FUSED) // RMSNorm's 1 / rms from the partial sums of x^2
+            inv = 1.0f / sqrtf(rsum[ROUTE_EXPERTS] / (float)n + a.src.eps);
+        else
+            inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
         fill_items(buf, first, W, total, load);
     } else {
         fill_items(buf, first, W, total, load);
@@ -1031,8 +1042,8 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
             return;
         inv = x_stage<NW>(a.src, n, a.st, raw, xs, red);
     }
-    LaneX X;
-    lanex_lds(X, xs, b, c, active);
+    if constexpr (!FUSED)
+        lanex_lds(X, xs, b, c, active);
     for (uint32_t it0 = first; it0 < total; it0 += G * W) {
         if (it0 != first)
             fill_items(buf, it0, W, total, load);
