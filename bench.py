@@ -3,15 +3,18 @@
 model at 4096 context on one MI355X, plus the Q6_K matvec HBM roofline and the
 CPU restatement of the reference path timed on the host.
 
-Workload (one step = one decode token): 24 layers (18 gated short-conv, 6 GQA at
-layers 2,6,10,14,18,21), dense SwiGLU ff 7168 in layers 0-1, MoE 32 experts top-4
-ff 1792 in layers 2-23, vocab 65536 tied Q6_K head; seeded random weights;
-prompt of (4096 - steps) uniform ids prefilled, then `steps` greedy tokens at
-positions 3840..4095.  Warmup steps run first and the resident state is then
-restored to the end of the prompt, so the timed steps are exactly the workload.
+Workload: 24 layers (18 gated short-conv, 6 GQA at layers 2,6,10,14,18,21),
+dense SwiGLU ff 7168 in layers 0-1, MoE 32 experts top-4 ff 1792 in layers
+2-23, vocab 65536 tied Q6_K head; seeded random weights; a 3840-token prompt
+of uniform ids prefilled in one call, then greedy decode at positions
+3840..4095 (ctx 4096).  One step = one decode token.  The K timed steps run
+from position 3840 in segments of at most 256 tokens; before each segment the
+resident state is restored (untimed) to the end of the prompt, so every timed
+token is a token of the 3840 + 256 workload whatever K is.  When K < 256 the
+whole 256-token decode is timed once more and reported as `decode_256`.
 
-Prints one JSON line: metric, value (tok/s), ms_per_step, roofline of the dominant
-kernel, the CPU baseline and prefill figures.
+Prints one JSON line: metric, value (tok/s), ms_per_step, roofline of the
+dominant kernel, the CPU baseline and prefill figures.
 """
 import argparse
 import json
@@ -34,10 +37,41 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
 # counters read for a plain 512 MiB copy): 1.02 x the algorithmic 24 155 264 bytes.
 GATEUP_TRAFFIC_BYTES = 24584196
 SEED = 0x9E3779B97F4A7C15
+CTX = 4096          # context of the workload (positions 0..4095)
+N_PROMPT = 3840     # prompt tokens prefilled before decode
+DECODE_TOKENS = 256  # greedy tokens of the workload (positions 3840..4095)
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def decode_segments(steps, start=N_PROMPT, ctx=CTX):
+    """Lengths of the decode runs that make up `steps` timed steps: each run
+    starts at `start` (after a state restore) and stays below ctx."""
+    if steps < 1:
+        raise ValueError("steps must be >= 1")
+    span = ctx - start
+    if span < 1:
+        raise ValueError("no decode positions left between start and ctx")
+    full, rest = divmod(steps, span)
+    return [span] * full + ([rest] if rest else [])
+
+
+def cpu_decode_steps(max_steps, n_gpu_tokens, start, ctx=CTX):
+    """How many teacher-forced oracle steps can run: one per GPU token, at
+    positions start.. below ctx, at most max_steps."""
+    return max(0, min(max_steps, n_gpu_tokens, ctx - start))
+
+
+def affinity_cores():
+    """Host threads this process may use: the affinity mask, capped by
+    OMP_NUM_THREADS when the environment sets it."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
 
 
 def decode_bytes_per_token(hp, positions):
@@ -78,8 +112,8 @@ def prefill_flops(hp, n):
 
 
 def matvec_roofline(iters=200):
-    """cfg0 kernel: 6144x2048 Q6_K matvec, 64 rotating weight copies (660 MB >
-    the 256 MB Infinity Cache), HIP-event timing on the launch stream."""
+    """6144x2048 Q6_K matvec kernel, 64 rotating weight copies (660 MB > the
+    256 MB Infinity Cache), HIP-event timing on the launch stream."""
     rows, in_dim, ncopies = 6144, 2048, 64
     size = lfm_hip.q6k_nbytes(rows, in_dim)
     raw = lfm_hip.synth_q6k_blocks(SEED, "cfg0.weight", rows * in_dim // 256, threads=16)
@@ -96,23 +130,126 @@ def matvec_roofline(iters=200):
     return algo, ms_hbm, ms_mall
 
 
-def cpu_baseline(hp, snapshot, start_pos, gpu_tokens, first, budget_s=15.0, max_steps=128):
+# ---------------------------------------------------------------- CPU baseline
+def _timed(fn, min_s, max_reps):
+    """Mean seconds per call of fn() over at least one call, repeated until
+    min_s has passed or max_reps calls ran; returns (seconds, last result)."""
+    out, reps = None, 0
+    t0 = time.perf_counter()
+    while True:
+        out = fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or reps >= max_reps:
+            return dt / reps, out
+
+
+def _layer_hparams(**kw):
+    base = dict(dim=2048, heads=32, n_layers=1, attention_layers=(), kv=8, vocab=256,
+                eos=1 << 30, n_expert=32, n_used=4, expert_ff=1792, n_ff=256, dense_lead=0)
+    base.update(kw)
+    return lfm_hip.make_hparams(**base)
+
+
+def _oracle_engine(lfm_oracle, hp, opts, ctx, threads):
+    o = lfm_oracle.OracleEngine(hp, ctx=ctx, kv_f16=True)
+    for d in lfm_hip.model_tensor_descs(hp, opts):
+        o.set_tensor(d.name.decode(), int(d.ggml_type), d.shape,
+                     lfm_hip.synth_tensor(d, opts, threads=threads))
+    o.finalize()
+    return o
+
+
+def cpu_layer_baselines(lfm_oracle, cores):
+    """The single-op configurations on the oracle, on 1 thread (the reference's
+    CPU path is single-threaded) and on `cores` threads; the multi-threaded
+    results must be bit-identical to the 1-thread ones (only independent rows
+    and heads are split)."""
+    res = {}
+
+    def both(name, setup, run, unit_bytes=None, min_s=0.3, max_reps=20):
+        state = setup()
+        out = {}
+        ref = None
+        for th in (1, cores):
+            lfm_oracle.set_threads(th)
+            sec, val = _timed(lambda: run(state), min_s, max_reps)
+            key = "1_thread" if th == 1 else f"{th}_threads"
+            out[key] = {"us": round(sec * 1e6, 1)}
+            if unit_bytes:
+                out[key]["gbs"] = round(unit_bytes / sec / 1e9, 3)
+            if ref is None:
+                ref = val
+            else:
+                out["bit_identical"] = bool(np.array_equal(ref.view(np.uint32), val.view(np.uint32)))
+        res[name] = out
+        if not out["bit_identical"]:
+            raise RuntimeError(f"oracle {name}: {cores}-thread result differs from 1 thread")
+
+    # cfg0: 6144x2048 Q6_K matvec, f64 accumulation (q6k.rs:161-183)
+    def s0():
+        raw = lfm_hip.synth_q6k_blocks(SEED, "cfg0.weight", 6144 * 2048 // 256, threads=cores)
+        return raw, lfm_hip.synth_normal(SEED, "cfg0.x", 2048)
+    both("cfg0_q6k_matvec_6144x2048", s0, lambda s: lfm_oracle.q6k_matvec(s[0], 2048, 6144, s[1]),
+         unit_bytes=10354688)
+
+    # cfg1: one MoE FFN step (RMSNorm, router, top-4, 4 x SwiGLU experts, combine)
+    def s1():
+        hp = _layer_hparams()
+        o = _oracle_engine(lfm_oracle, hp, lfm_hip.synth_opts(SEED), 16, cores)
+        return o, lfm_hip.synth_normal(SEED, "cfg1.h", hp.dim)
+    both("cfg1_moe_step", s1, lambda s: s[0].run_ffn(0, s[1]), min_s=0.5, max_reps=10)
+
+    # cfg2: attention layer at L = 4096 (query at position 4095)
+    def s2():
+        hp = _layer_hparams(attention_layers=(0,), dense_lead=1)
+        o = _oracle_engine(lfm_oracle, hp, lfm_hip.synth_opts(SEED), CTX, cores)
+        p = CTX - 1
+        kv = lfm_hip.synth_normal(SEED, "cfg2.kv4096", 2 * p * 8 * 64).astype(np.float16)
+        snap = kv.astype(np.float32).tobytes()
+        return o, p, snap, lfm_hip.synth_normal(SEED, "cfg2.x4096", hp.dim)
+
+    def r2(s):
+        o, p, snap, x = s
+        o.restore(p, snap)
+        return o.run_mixer(0, x, p)
+    both("cfg2_attention_L4096", s2, r2, min_s=0.5, max_reps=10)
+
+    # cfg3: gated short-conv block, one token from a seeded 2-slot state
+    def s3():
+        hp = _layer_hparams(dense_lead=1)
+        o = _oracle_engine(lfm_oracle, hp, lfm_hip.synth_opts(SEED), 512, cores)
+        state = lfm_hip.synth_normal(SEED, "cfg3.state", hp.dim * 2).tobytes()
+        return o, state, lfm_hip.synth_normal(SEED, "cfg3.x", hp.dim)
+
+    def r3(s):
+        o, state, x = s
+        o.restore(0, state)
+        return o.run_mixer(0, x, 0)
+    both("cfg3_shortconv_step", s3, r3, min_s=0.3, max_reps=20)
+    return res
+
+
+def cpu_baseline(hp, snapshot, start_pos, gpu_tokens, first, cores, budget_s=12.0, max_steps=128):
     """The oracle (C restatement of the reference CPU path) on the host cores:
     resident state restored from the GPU at the end of the prompt, then greedy
-    decode steps teacher-forced with the GPU's tokens until ~budget_s."""
+    decode steps teacher-forced with the GPU's tokens until ~budget_s, at most
+    one per GPU token and never past ctx.  Also times the single-op
+    configurations on 1 thread and on all cores."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import lfm_oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    lfm_oracle.set_threads(threads)
-    o = lfm_oracle.OracleEngine(hp, ctx=4096, kv_f16=True)
-    for d in lfm_hip.model_tensor_descs(hp):
-        o.set_tensor(d.name.decode(), int(d.ggml_type), d.shape, lfm_hip.synth_tensor(d, threads=threads))
-    o.finalize()
+    t_layers = time.perf_counter()
+    layers = cpu_layer_baselines(lfm_oracle, cores)
+    log(f"[bench] cpu single-op configurations timed in {time.perf_counter() - t_layers:.1f} s")
+
+    lfm_oracle.set_threads(cores)
+    o = _oracle_engine(lfm_oracle, hp, lfm_hip.synth_opts(SEED), CTX, cores)
     o.restore(start_pos, snapshot)
+    limit = cpu_decode_steps(max_steps, len(gpu_tokens), start_pos)
     feed, steps, agree, compared = first, 0, 0, 0
     t0 = time.perf_counter()
-    while steps < max_steps and time.perf_counter() - t0 < budget_s:
+    while steps < limit and time.perf_counter() - t0 < budget_s:
         lo = o.forward([feed], start_pos + steps)
         srt = np.sort(lo)
         if srt[-1] - srt[-2] > 1e-3 * np.abs(lo).max():
@@ -122,19 +259,22 @@ def cpu_baseline(hp, snapshot, start_pos, gpu_tokens, first, budget_s=15.0, max_
         steps += 1
     dt = time.perf_counter() - t0
     o.close()
-    return {"value": steps / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(steps / dt, 3) if steps else None, "unit": "tok/s", "cores": cores,
+            "kind": "port",
             "sample": f"{steps} greedy decode steps of the full model at positions "
-                      f"{start_pos}..{start_pos + steps - 1} (ctx 4096), oracle state restored "
-                      f"from the GPU after prefill; {dt:.1f} s",
-            "tokens_compared": compared, "tokens_agree": agree}
+                      f"{start_pos}..{start_pos + steps - 1} (ctx {CTX}) on {cores} threads, "
+                      f"oracle state restored from the GPU after the {start_pos}-token prefill, "
+                      f"teacher-forced with the GPU's tokens; {dt:.1f} s",
+            "tokens_compared": compared, "tokens_agree": agree,
+            "single_op": layers,
+            "prefill": "not timed: the oracle's 3840-token prefill is minutes of host work"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--steps", type=int, default=DECODE_TOKENS)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--synthetic-state", action="store_true",
@@ -145,15 +285,16 @@ def main():
         print("bench.py measures one GPU: the batch-1 decode path runs on a single GPU and is "
               "not sharded here; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        sys.exit("--steps must be >= 1 and --warmup >= 0")
     assert lfm_hip.device_count() > 0, "no HIP device"
-    if args.steps < 1 or args.steps + 1 > args.ctx:
-        sys.exit("steps must be in 1..ctx-1")
+    cores = affinity_cores()
 
     hp = lfm_hip.make_hparams()
     t = time.perf_counter()
-    eng = lfm_hip.GpuEngine.load_synthetic(hp, lfm_hip.synth_opts(SEED), ctx=args.ctx, threads=16)
+    eng = lfm_hip.GpuEngine.load_synthetic(hp, lfm_hip.synth_opts(SEED), ctx=CTX, threads=16)
     log(f"[bench] model generated + uploaded in {time.perf_counter() - t:.1f} s on {eng.device_name}")
-    n_prompt = args.ctx - args.steps
+    n_prompt = N_PROMPT
     prompt = [int(v) for v in np.random.default_rng(SEED & 0xFFFFFFFF).integers(0, hp.vocab, n_prompt)]
 
     t = time.perf_counter()
@@ -176,20 +317,49 @@ def main():
     snap = eng.snapshot_resident_cache(n_prompt)
 
     if args.warmup > 0:
-        eng.decode_run(first, n_prompt, min(args.warmup, args.steps), eos=1 << 31)
+        eng.decode_run(first, n_prompt, min(args.warmup, CTX - n_prompt), eos=1 << 31)
+    # timed: K steps from position 3840, restoring the prompt state before each run
+    toks, dt, fdt = [], 0.0, None
+    for seg in decode_segments(args.steps):
         eng.restore_session(n_prompt, snap)
-    lfm_hip.lib().lfm_dev_synchronize()
-    t0 = time.perf_counter()
-    toks = eng.decode_run(first, n_prompt, args.steps, eos=1 << 31)
-    lfm_hip.lib().lfm_dev_synchronize()
-    dt = time.perf_counter() - t0
-    assert len(toks) == args.steps
+        lfm_hip.lib().lfm_dev_synchronize()
+        t0 = time.perf_counter()
+        out = eng.decode_run(first, n_prompt, seg, eos=1 << 31)
+        lfm_hip.lib().lfm_dev_synchronize()
+        sdt = time.perf_counter() - t0
+        dt += sdt
+        assert len(out) == seg
+        if not toks:
+            toks = out
+            if seg == DECODE_TOKENS:
+                fdt = sdt
+        elif out != toks[:seg]:
+            raise RuntimeError("decode from the same state gave different tokens")
     ms_per_step = dt * 1e3 / args.steps
     tok_s = args.steps / dt
-    wbytes, kvbytes = decode_bytes_per_token(hp, range(n_prompt, n_prompt + args.steps))
+    timed_pos = range(n_prompt, n_prompt + min(args.steps, CTX - n_prompt))
+    wbytes, kvbytes = decode_bytes_per_token(hp, timed_pos)
     decode_gbs = (wbytes + kvbytes) * tok_s / 1e9
     log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tok_s:.1f} tok/s, "
         f"{decode_gbs:.0f} GB/s algorithmic")
+
+    decode_256 = None
+    if fdt is None:
+        eng.restore_session(n_prompt, snap)
+        lfm_hip.lib().lfm_dev_synchronize()
+        t0 = time.perf_counter()
+        full = eng.decode_run(first, n_prompt, DECODE_TOKENS, eos=1 << 31)
+        lfm_hip.lib().lfm_dev_synchronize()
+        fdt = time.perf_counter() - t0
+        if full[:len(toks)] != toks:
+            raise RuntimeError("decode from the same state gave different tokens")
+        toks = full
+    if fdt is not None:
+        fw, fkv = decode_bytes_per_token(hp, range(n_prompt, CTX))
+        decode_256 = {"tokens": DECODE_TOKENS, "positions": f"{n_prompt}..{CTX - 1}",
+                      "ms": round(fdt * 1e3, 2), "tok_s": round(DECODE_TOKENS / fdt, 1),
+                      "hbm_gbs_algorithmic": round((fw + fkv) * DECODE_TOKENS / fdt / 1e9, 1)}
+        log(f"[bench] decode 256 tokens at {n_prompt}..{CTX - 1}: {fdt * 1e3:.1f} ms")
 
     chunked = None
     if not args.synthetic_state:
@@ -232,7 +402,7 @@ def main():
             "timing": "HIP events over a graph of 45 launches rotating 3 weight copies (gaps included)"}
         log(f"[bench] k_head4: {hus:.2f} us/launch = {hgbs:.0f} GB/s ({hgbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
         algo, ms_hbm, ms_mall = matvec_roofline()
-        extra["q6k_matvec_cfg0"] = {
+        extra["q6k_matvec_6144x2048"] = {
             "shape": "6144x2048", "algorithmic_bytes": algo,
             "us_per_launch": round(ms_hbm * 1e3, 3),
             "hbm_gbs": round(algo / (ms_hbm * 1e-3) / 1e9, 1),
@@ -244,28 +414,32 @@ def main():
                              "gbs_read_plus_write": round(2 * copy_bytes / (copy_us * 1e-6) / 1e9, 1)}
         log(f"[bench] plain copy {copy_bytes >> 20} MiB: {copy_us:.1f} us = "
             f"{extra['hbm_copy']['gbs_read_plus_write']:.0f} GB/s read+write")
-        log(f"[bench] q6k matvec cfg0: {ms_hbm * 1e3:.2f} us/launch = "
-            f"{extra['q6k_matvec_cfg0']['hbm_gbs']:.0f} GB/s (HBM, 64 rotating copies), "
-            f"{extra['q6k_matvec_cfg0']['cache_resident_gbs']:.0f} GB/s cache-resident")
+        log(f"[bench] q6k matvec 6144x2048: {ms_hbm * 1e3:.2f} us/launch = "
+            f"{extra['q6k_matvec_6144x2048']['hbm_gbs']:.0f} GB/s (HBM, 64 rotating copies), "
+            f"{extra['q6k_matvec_6144x2048']['cache_resident_gbs']:.0f} GB/s cache-resident")
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (oracle) ...")
-        cpu = cpu_baseline(hp, snap, n_prompt, toks, first)
-        log(f"[bench] cpu baseline {cpu['value']:.3f} tok/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline (oracle) on {cores} threads ...")
+        cpu = cpu_baseline(hp, snap, n_prompt, toks, first, cores)
+        log(f"[bench] cpu baseline {cpu['value']} tok/s on {cpu['cores']} threads, "
+            f"{cpu['tokens_agree']}/{cpu['tokens_compared']} margin-clear tokens agree")
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded random-init Q6_K weights and prompt ids)",
-        "config": {"workload": f"LFM2.5-8B-A1B-shaped Q6_K token loop, bs=1: prefill {n_prompt} "
-                               f"+ {args.steps} greedy decode steps at ctx {args.ctx}",
+        "config": {"workload": f"prefill {n_prompt} + {DECODE_TOKENS} greedy decode steps at "
+                               f"ctx {CTX} (LFM2.5-8B-A1B-shaped Q6_K token loop, bs=1)",
+                   "timed_steps": f"{args.steps} decode tokens from position {n_prompt}, in runs "
+                                  f"of at most {CTX - n_prompt} from the restored prompt state",
                    "layers": 24, "conv_layers": 18, "attention_layers": 6, "vocab": hp.vocab,
-                   "experts": "32 top-4", "ctx": args.ctx, "parallelism": "single GPU"},
+                   "experts": "32 top-4", "ctx": CTX, "parallelism": "single GPU"},
         "roofline": roof, "cpu_baseline": cpu,
         "decode_hbm_gbs": round(decode_gbs, 1),
         "decode_bytes_per_token": int(wbytes + kvbytes),
+        "decode_256": decode_256,
         "prefill": None if args.synthetic_state else {
             "tokens": n_prompt, "ms": round(prefill_s * 1e3, 1),
             "tok_s": round(n_prompt / prefill_s, 1),

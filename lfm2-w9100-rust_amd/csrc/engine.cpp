@@ -781,11 +781,20 @@ extern "C" int lfm_engine_create(const lfm_hparams *hp, int device, lfm_engine *
     lfm_engine *e = new lfm_engine();
     e->hp = *hp;
     e->device = device;
+    // The marketing name can be blank (it is on some boards); then the name
+    // falls back to the properties' name and finally to "AMD GPU <device>".
     char name[256] = {0};
     hipDeviceProp_t prop;
-    if (hipDeviceGetName(name, sizeof(name) - 1, device) == hipSuccess &&
-        hipGetDeviceProperties(&prop, device) == hipSuccess)
-        e->devname = std::string(name) + " (" + prop.gcnArchName + ")";
+    memset(&prop, 0, sizeof(prop));
+    if (hipDeviceGetName(name, sizeof(name) - 1, device) != hipSuccess)
+        name[0] = 0;
+    const bool have_prop = hipGetDeviceProperties(&prop, device) == hipSuccess;
+    std::string nm = name;
+    if (nm.empty() && have_prop)
+        nm = prop.name;
+    if (nm.empty())
+        nm = "AMD GPU " + std::to_string(device);
+    e->devname = have_prop && prop.gcnArchName[0] ? nm + " (" + prop.gcnArchName + ")" : nm;
     int rc = get_kernels(&e->K);
     if (rc == LFM_OK && hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
         rc = fail(LFM_EDEVICE, "hipStreamCreateWithFlags failed");
@@ -817,6 +826,32 @@ extern "C" int lfm_engine_hparams(const lfm_engine *e, lfm_hparams *out)
     return LFM_OK;
 }
 
+int lfm_check_tensor(const char *name, uint32_t type, const uint64_t *ne, uint32_t nd,
+                     size_t *want)
+{
+    if (!name || !ne || !want || nd == 0 || nd > 4)
+        return fail(LFM_EINVAL, "tensor: bad arguments (name, shape, or 1..4 dimensions)");
+    uint64_t n = 1;
+    for (uint32_t i = 0; i < nd; ++i) {
+        if (ne[i] == 0)
+            return fail(LFM_EINVAL, "%s: dimension %u is zero", name, i);
+        if (ne[i] > (1ull << 40) || n > (1ull << 40) / ne[i])
+            return fail(LFM_EINVAL, "%s: %u-dimensional shape too large", name, nd);
+        n *= ne[i];
+    }
+    if (type == LFM_GGML_TYPE_Q6_K) {
+        if (ne[0] % 256)
+            return fail(LFM_EINVAL, "%s: Q6_K row length %llu is not a multiple of 256", name,
+                        (unsigned long long)ne[0]);
+        *want = (size_t)(n / 256 * 210);
+    } else if (type == LFM_GGML_TYPE_F32) {
+        *want = (size_t)(n * 4);
+    } else {
+        return fail(LFM_EINVAL, "%s: unsupported ggml type %u (F32 and Q6_K only)", name, type);
+    }
+    return LFM_OK;
+}
+
 extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_t type,
                                         const uint64_t *ne, uint32_t nd, const void *host,
                                         size_t nbytes)
@@ -824,8 +859,10 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     RC(engine_dev(e));
     if (e->finalized)
         return fail(LFM_ESTATE, "tensors must be uploaded before lfm_engine_finalize");
-    if (!name || !ne || !host || nd == 0 || nd > 4)
-        return fail(LFM_EINVAL, "upload_tensor: bad arguments");
+    if (!host)
+        return fail(LFM_EINVAL, "upload_tensor: host pointer is null");
+    size_t want = 0;
+    RC(lfm_check_tensor(name, type, ne, nd, &want));
     DevTensor t;
     t.type = type;
     t.nd = nd;
@@ -833,17 +870,6 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     for (uint32_t i = 0; i < nd; ++i) {
         t.ne[i] = ne[i];
         n *= ne[i];
-    }
-    size_t want;
-    if (type == LFM_GGML_TYPE_Q6_K) {
-        if (ne[0] % 256)
-            return fail(LFM_EINVAL, "%s: Q6_K row length %llu is not a multiple of 256", name,
-                        (unsigned long long)ne[0]);
-        want = (size_t)(n / 256 * 210);
-    } else if (type == LFM_GGML_TYPE_F32) {
-        want = (size_t)(n * 4);
-    } else {
-        return fail(LFM_EINVAL, "%s: unsupported ggml type %u (F32 and Q6_K only)", name, type);
     }
     if (nbytes != want)
         return fail(LFM_EINVAL, "%s: %zu bytes given, %zu expected", name, nbytes, want);

@@ -63,9 +63,10 @@ struct Value {
 };
 
 // Elements per block and bytes per block of each ggml storage type the format
-// accepts (ggml's block structs; other type ids are rejected, as by the
-// reference's table at gguf.rs:174-192).  Q3_K and Q8_K use ggml's block sizes,
-// 110 and 292 bytes; no tensor of either type is uploaded to the engine.
+// accepts; other type ids are rejected.  The table is the reference parser's
+// (gguf.rs:174-192), so a file is accepted, rejected and sized exactly as there.
+// That includes its Q3_K and Q8_K entries, 112 and 288 bytes, where ggml's block
+// structs take 110 and 292; no tensor of either type is uploaded to the engine.
 bool block_info(uint32_t type, uint64_t *elems, uint64_t *bytes)
 {
     static const struct {
@@ -80,11 +81,11 @@ bool block_info(uint32_t type, uint64_t *elems, uint64_t *bytes)
         {8, 32, 34},    // Q8_0: f16 d, 32 int8
         {9, 32, 36},    // Q8_1: f16 d, s, 32 int8
         {10, 256, 84},  // Q2_K: 16 B scales, 64 B quants, f16 d, dmin
-        {11, 256, 110}, // Q3_K: 32 B high mask, 64 B quants, 12 B scales, f16 d
+        {11, 256, 112}, // Q3_K (ggml's block: 110 B)
         {12, 256, 144}, // Q4_K: f16 d, dmin, 12 B scales, 128 B quants
         {13, 256, 176}, // Q5_K: f16 d, dmin, 12 B scales, 32 B high bits, 128 B
         {14, 256, 210}, // Q6_K: 128 B low bits, 64 B high bits, 16 int8 scales, f16 d
-        {15, 256, 292}, // Q8_K: f32 d, 256 int8, 16 int16 block sums
+        {15, 256, 288}, // Q8_K (ggml's block: 292 B)
     };
     for (const auto &t : table)
         if (t.type == type) {
@@ -812,10 +813,30 @@ extern "C" int lfm_gguf_hparams(const lfm_gguf *g, int strict, lfm_hparams *out)
 // GpuEngine::load's staging loop (engine/src/gpu_lfm.rs:64-97): every F32 and
 // Q6_K tensor, in file order, is read into one host staging buffer sized for the
 // largest and uploaded; tensors of other types are skipped.
+// Every F32 / Q6_K tensor of the file has a shape the engine takes (no zero
+// dimension, whole Q6_K rows): checked on the host before any upload.
+static int check_gguf_tensors(const lfm_gguf *g)
+{
+    for (const TensorEntry &t : g->tensors) {
+        if (t.type != LFM_GGML_TYPE_F32 && t.type != LFM_GGML_TYPE_Q6_K)
+            continue;
+        if (t.ne.size() > 4)
+            return fail(LFM_EINVAL, "%s: %zu dimensions (the engine takes 1..4)", t.name.c_str(),
+                        t.ne.size());
+        size_t want = 0;
+        RC(lfm_check_tensor(t.name.c_str(), t.type, t.ne.data(), (uint32_t)t.ne.size(), &want));
+        if (want != t.nbytes)
+            return fail(LFM_EINTERNAL, "%s: %zu bytes by shape, %llu in the file table",
+                        t.name.c_str(), want, (unsigned long long)t.nbytes);
+    }
+    return LFM_OK;
+}
+
 extern "C" int lfm_engine_load_gguf(lfm_engine *e, const lfm_gguf *g)
 {
     if (!e || !g)
         return fail(LFM_EINVAL, "null argument");
+    RC(check_gguf_tensors(g));
     uint64_t most = 0;
     for (const TensorEntry &t : g->tensors)
         if (t.type == LFM_GGML_TYPE_F32 || t.type == LFM_GGML_TYPE_Q6_K)
@@ -843,7 +864,9 @@ extern "C" int lfm_engine_open_gguf(const char *path, int device, uint32_t ctx, 
     RC(lfm_gguf_open(path, &g));
     lfm_hparams hp;
     lfm_engine *e = nullptr;
-    int rc = lfm_gguf_hparams(g, strict, &hp);
+    int rc = check_gguf_tensors(g);
+    if (rc == LFM_OK)
+        rc = lfm_gguf_hparams(g, strict, &hp);
     if (rc == LFM_OK && (hp.n_expert < 4 || hp.n_expert > 64))
         rc = fail(LFM_EINVAL, "resident routing supports 4..=64 experts");
     if (rc == LFM_OK)

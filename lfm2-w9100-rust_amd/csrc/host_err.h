@@ -5,6 +5,8 @@
 #pragma once
 
 #include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
 
 // Formats the message, stores it for lfm_last_error() and returns `code`.
 __attribute__((visibility("hidden"))) int lfm_vfail(int code, const char *fmt, va_list ap);
@@ -17,3 +19,11 @@ __attribute__((format(printf, 2, 3))) static inline int fail(int code, const cha
     va_end(ap);
     return rc;
 }
+
+// Checks one tensor's type and shape as lfm_engine_upload_tensor takes
+// them (F32 or Q6_K, 1..4 dimensions, none of them zero, Q6_K rows a multiple of
+// 256) and sets *want to the bytes the tensor must have.  Host-only: the GGUF
+// loaders run it over a whole file before any device work.
+__attribute__((visibility("hidden"))) int lfm_check_tensor(const char *name, uint32_t type,
+                                                           const uint64_t *ne, uint32_t nd,
+                                                           size_t *want);

@@ -19,8 +19,8 @@ from model_util import small_hparams
 _FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q",
         11: "<q", 12: "<d"}
 _BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
-          9: (32, 36), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176),
-          14: (256, 210), 15: (256, 292)}
+          9: (32, 36), 10: (256, 84), 11: (256, 112), 12: (256, 144), 13: (256, 176),
+          14: (256, 210), 15: (256, 288)}
 
 
 def enc_str(s):
@@ -96,6 +96,18 @@ def test_tensor_sizes_known_answers(tmp_path):
     assert got == {name: nb for name, _, _, nb in cases}
 
 
+def test_block_table_is_the_reference_parsers(tmp_path):
+    # ggml_type_block_info (gguf.rs:174-192): Q3_K takes 112 bytes and Q8_K 288 per
+    # 256 elements there (ggml's structs: 110 and 292).  A drop-in reader sizes,
+    # places and accepts tensors exactly as the reference does.
+    tensors = [("q3", [512], 11, 0), ("q8", [256], 15, 224)]
+    data = build(tensors=tensors)
+    with L.GgufFile.parse(data) as f:
+        assert f.tensor("q3").nbytes == 224 and f.tensor("q8").nbytes == 288
+    # the same file one byte short of the reference's Q8_K size is out of bounds
+    parse_err(data[:-1])
+
+
 @pytest.mark.parametrize("dims,t", [([100], 14), ([10], 999), ([2**64 - 1, 2], 0)])
 def test_tensor_size_errors(dims, t):
     # Q6_K element count not a multiple of 256, unknown type, overflowing dims
@@ -142,6 +154,23 @@ def test_truncated_header():
 def test_empty_tensor():
     with L.GgufFile.parse(build(tensors=[("empty", [0, 2048], 0, 0)])) as f:
         assert f.tensor("empty").nbytes == 0
+
+
+@pytest.mark.parametrize("dims,t", [([0, 2048], 14), ([2048, 0], 14), ([0], 0)])
+def test_empty_tensor_is_rejected_by_the_engine_loader(tmp_path, dims, t):
+    # An empty tensor parses (test_empty_tensor) but the engine takes no zero
+    # dimension: lfm_engine_open_gguf reports it before any device work (no
+    # division by a zero row length, no device needed to see the error).
+    meta = lfm_meta()
+    p = str(tmp_path / "empty.gguf")
+    with open(p, "wb") as fh:
+        fh.write(build(meta=meta, tensors=[("blk.0.attn_norm.weight", [2048], 0, 0),
+                                           ("token_embd.weight", dims, t, 8192)]))
+    eng = L.C.c_void_p()
+    rc = L.lib().lfm_engine_open_gguf(p.encode(), 0, 0, 1, L.C.byref(eng))
+    assert rc == L.LFM_EINVAL, (rc, L.lib().lfm_last_error())
+    assert b"dimension" in L.lib().lfm_last_error()
+    assert not eng.value
 
 
 def test_array_and_bool_metadata():
