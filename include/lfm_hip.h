@@ -143,6 +143,15 @@ int lfm_device_name(const lfm_engine *e, char *buf, size_t cap);
 int lfm_engine_run_mixer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos);
 int lfm_engine_run_ffn(lfm_engine *e, uint32_t layer, float *x);
 int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *weights, uint32_t cap);
+/* A whole layer as the decode step runs it (resident_graph.rs:237-503 for one
+ * layer): mixer, then FFN with the MoE router fused into the mixer's output
+ * projection where the step fuses it, so lfm_engine_last_route then returns the
+ * routing of the step's own kernels.  x_mid (dim floats, may be NULL) receives
+ * the residual between the two halves, i.e. the FFN input the routing saw. */
+int lfm_engine_run_layer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos, float *x_mid);
+/* *fused = 1 when MoE layer `layer` routes through the fused router in the
+ * decode step (32 experts, dim 2048), else 0. */
+int lfm_engine_fused_router(const lfm_engine *e, uint32_t layer, int *fused);
 
 /* Mean duration of the routed MoE gate/up kernel (the largest share of a decode
  * step), timed with HIP events over one graph of `reps` rounds across every MoE

@@ -1961,6 +1961,44 @@ extern "C" int lfm_engine_run_ffn(lfm_engine *e, uint32_t layer, float *x)
     return run_layer_part(e, layer, x, 0, false);
 }
 
+// One whole layer as the decode step runs it: the mixer, then the FFN enqueued
+// right after with the router fused into the mixer's output projection (when
+// the shape has the fused router), so the routing comes from the same kernels
+// and the same partial sums as in the captured step.  x_mid (optional)
+// receives the residual between the halves: the FFN's input.
+extern "C" int lfm_engine_run_layer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos,
+                                    float *x_mid)
+{
+    RC(need_final(e));
+    if (!x)
+        return fail(LFM_EINVAL, "x is null");
+    if (layer >= e->hp.n_layers)
+        return fail(LFM_ERANGE, "layer %u >= %u", layer, e->hp.n_layers);
+    if (pos >= e->ctx)
+        return fail(LFM_ERANGE, "position %u >= ctx %u", pos, e->ctx);
+    const size_t nb = (size_t)e->hp.dim * 4;
+    HIPCHK(hipMemcpyAsync(e->x, x, nb, hipMemcpyHostToDevice, e->stream));
+    RC(set_state(e, 0, pos, 0, 0xFFFFFFFFu));
+    RC(enq_mixer(e, layer, false, true));
+    if (x_mid)
+        HIPCHK(hipMemcpyAsync(x_mid, e->x, nb, hipMemcpyDeviceToHost, e->stream));
+    RC(enq_ffn(e, layer, true));
+    HIPCHK(hipMemcpyAsync(x, e->x, nb, hipMemcpyDeviceToHost, e->stream));
+    HIPCHK(hipStreamSynchronize(e->stream));
+    return LFM_OK;
+}
+
+// Whether MoE layer `layer` routes through the fused router in the decode step.
+extern "C" int lfm_engine_fused_router(const lfm_engine *e, uint32_t layer, int *fused)
+{
+    if (!e || !fused)
+        return fail(LFM_EINVAL, "null argument");
+    if (layer >= e->hp.n_layers)
+        return fail(LFM_ERANGE, "layer %u >= %u", layer, e->hp.n_layers);
+    *fused = fused_router(e, layer) ? 1 : 0;
+    return LFM_OK;
+}
+
 extern "C" int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *w, uint32_t cap)
 {
     RC(need_final(e));

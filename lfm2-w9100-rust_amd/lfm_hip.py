@@ -150,6 +150,8 @@ def lib():
         "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
+        "lfm_engine_run_layer": (i32, [P, u32, pf32, u32, pf32]),
+        "lfm_engine_fused_router": (i32, [P, u32, C.POINTER(C.c_int)]),
         "lfm_engine_time_moe_gateup": (i32, [P, u32, pf32, C.POINTER(u64)]),
         "lfm_engine_time_head": (i32, [P, u32, u32, pf32, C.POINTER(u64)]),
         "lfm_dev_alloc": (i32, [sz, C.POINTER(P)]), "lfm_dev_free": (i32, [P]),
@@ -772,6 +774,19 @@ class GpuEngine:
         xa = np.array(x, dtype=np.float32, copy=True)
         _check(lib().lfm_engine_run_ffn(self._e, layer, _f32p(xa)))
         return xa
+
+    def run_layer(self, layer: int, x: np.ndarray, pos: int):
+        """One whole layer as the decode step runs it (fused router where the step
+        fuses it): returns (x after the layer, x between mixer and FFN)."""
+        xa = np.array(x, dtype=np.float32, copy=True)
+        mid = np.empty_like(xa)
+        _check(lib().lfm_engine_run_layer(self._e, layer, _f32p(xa), pos, _f32p(mid)))
+        return xa, mid
+
+    def fused_router(self, layer: int) -> bool:
+        v = C.c_int(0)
+        _check(lib().lfm_engine_fused_router(self._e, layer, C.byref(v)))
+        return bool(v.value)
 
     def last_route(self):
         ids = np.zeros(8, dtype=np.uint32)

@@ -692,6 +692,21 @@ int oracle_run_mixer(oracle_engine *e, uint32_t l, float *x, uint32_t n, int64_t
     return rc;
 }
 
+/* lfm.rs:599-607: router logits [nf][n_expert] of normed columns fnorm (the
+ * f32 sequential ffn_gate_inp matmul), and the layer's bias vector. */
+static int router_logits(oracle_engine *e, uint32_t l, const float *fnorm, size_t nf,
+                         float *router, const float **bias)
+{
+    char nm[128];
+    int rc = mul_mat_weight(e, NAME(nm, l, "ffn_gate_inp.weight"), e->hp.dim, e->hp.n_expert,
+                            fnorm, nf, router);
+    tensor *bt = find(e, NAME(nm, l, "exp_probs_b.bias"));
+    if (rc || !bt || !bt->f32)
+        return -3;
+    *bias = bt->f32;
+    return 0;
+}
+
 /* lfm.rs:539-670 on columns [f_off, f_off + nf) of x. */
 static int ffn_cols(oracle_engine *e, uint32_t l, float *x, size_t f_off, size_t nf)
 {
@@ -725,9 +740,8 @@ static int ffn_cols(oracle_engine *e, uint32_t l, float *x, size_t f_off, size_t
     } else {
         size_t ne = hp->n_expert, nu = hp->n_used, eff = hp->expert_ff;
         float *router = (float *)malloc(ne * nf * sizeof(float));
-        rc = mul_mat_weight(e, NAME(nm, l, "ffn_gate_inp.weight"), dim, ne, fnorm, nf, router);
-        tensor *bt = find(e, NAME(nm, l, "exp_probs_b.bias"));
-        if (rc || !bt || !bt->f32) {
+        const float *bias = NULL;
+        if (router_logits(e, l, fnorm, nf, router, &bias)) {
             free(router), free(fnorm);
             return -3;
         }
@@ -741,7 +755,7 @@ static int ffn_cols(oracle_engine *e, uint32_t l, float *x, size_t f_off, size_t
         for (size_t j = 0; j < nf && !rc; j++) {
             uint32_t sel[8];
             float wsel[8];
-            oracle_route(router + j * ne, bt->f32, (uint32_t)ne, (uint32_t)nu, sel, wsel,
+            oracle_route(router + j * ne, bias, (uint32_t)ne, (uint32_t)nu, sel, wsel,
                          e->route_scores[l]);
             for (size_t r = 0; r < nu; r++) {
                 e->route_ids[l][r] = sel[r];
@@ -776,6 +790,32 @@ int oracle_run_ffn(oracle_engine *e, uint32_t l, float *x, uint32_t n)
     if (!e || l >= e->hp.n_layers || n == 0)
         return -1;
     return ffn_cols(e, l, x, 0, n);
+}
+
+/* The routing step of ffn_cols alone (lfm.rs:599-637): RMSNorm of x with the
+ * layer's ffn_norm, router logits, selection and weights; x is not changed. */
+int oracle_route_layer(oracle_engine *e, uint32_t l, const float *x, uint32_t *ids, float *w,
+                       float *scores, float *logits)
+{
+    if (!e || l >= e->hp.n_layers || l < e->hp.dense_lead || !x || !ids || !w)
+        return -1;
+    char nm[128];
+    const float *ffn_norm = f32_of(e, NAME(nm, l, "ffn_norm.weight"));
+    if (!ffn_norm)
+        return -3;
+    size_t dim = e->hp.dim, ne = e->hp.n_expert;
+    float *fnorm = (float *)malloc(dim * sizeof(float));
+    float *router = (float *)malloc(ne * sizeof(float));
+    rms_norm(e, x, ffn_norm, 1, fnorm);
+    const float *bias = NULL;
+    int rc = router_logits(e, l, fnorm, 1, router, &bias);
+    if (!rc) {
+        oracle_route(router, bias, (uint32_t)ne, e->hp.n_used, ids, w, scores);
+        if (logits)
+            memcpy(logits, router, ne * sizeof(float));
+    }
+    free(fnorm), free(router);
+    return rc;
 }
 
 int oracle_embed(oracle_engine *e, uint32_t token, float *out)

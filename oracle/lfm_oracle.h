@@ -111,6 +111,12 @@ int oracle_snapshot(const oracle_engine *e, uint32_t valid_tokens, uint8_t *buf,
 int oracle_restore(oracle_engine *e, uint32_t valid_tokens, const uint8_t *buf, size_t len);
 void oracle_reset(oracle_engine *e);
 
+/* The routing of one residual vector x[dim] at MoE layer l, by the same code
+ * as oracle_run_ffn (lfm.rs:599-637): ids/w[n_used], scores[n_expert]
+ * (sigmoid + bias), logits[n_expert] (may be NULL).  x is not changed. */
+int oracle_route_layer(oracle_engine *e, uint32_t l, const float *x, uint32_t *ids, float *w,
+                       float *scores, float *logits);
+
 /* Last MoE routing decision of a layer (ids + weights), for id parity checks. */
 int oracle_last_route(const oracle_engine *e, uint32_t layer, uint32_t *ids, float *w,
                       float *scores);

@@ -74,6 +74,7 @@ def lib():
         "oracle_restore": (C.c_int, [P, u32, pu8, sz]),
         "oracle_reset": (None, [P]),
         "oracle_last_route": (C.c_int, [P, u32, pu32, pf, pf]),
+        "oracle_route_layer": (C.c_int, [P, u32, pf, pu32, pf, pf, pf]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -269,6 +270,20 @@ class OracleEngine:
         lib().oracle_last_route(self._e, layer, ids.ctypes.data_as(C.POINTER(C.c_uint32)), _f(w),
                                 _f(scores))
         return [int(i) for i in ids[: self.hp.n_used]], w[: self.hp.n_used].copy(), scores
+
+    def route_layer(self, layer: int, x: np.ndarray):
+        """Routing of residual x at MoE layer `layer` (ids, weights, scores, logits)."""
+        xa = np.ascontiguousarray(x, dtype=np.float32)
+        ids = np.zeros(8, dtype=np.uint32)
+        w = np.zeros(8, dtype=np.float32)
+        scores = np.zeros(self.hp.n_expert, dtype=np.float32)
+        logits = np.zeros(self.hp.n_expert, dtype=np.float32)
+        rc = lib().oracle_route_layer(self._e, layer, _f(xa), ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                      _f(w), _f(scores), _f(logits))
+        if rc:
+            raise ValueError(f"route_layer: {rc}")
+        n = self.hp.n_used
+        return [int(i) for i in ids[:n]], w[:n].copy(), scores, logits
 
     def close(self):
         if self._e:

@@ -106,3 +106,36 @@ def test_powi_is_square_and_multiply(oracle):
             base = np.float32(base * base)
         assert oracle.powi(float(a), p) == r
         assert abs(float(r) / float(np.float64(a) ** p) - 1) < 1e-5
+
+
+def test_route_layer_is_the_ffn_routing(oracle):
+    """oracle_route_layer (the routing alone, used to check the GPU's fused router)
+    is the routing run_ffn takes, and its logits match a float64 numpy statement of
+    RMSNorm + the f32 router matmul (lfm.rs:599-607) to f32 rounding."""
+    import lfm_hip
+    from model_util import model_tensors, oracle_engine, small_hparams
+
+    hp = small_hparams(kinds=("conv", "conv"), n_expert=16, dense_lead=1)
+    tensors = model_tensors(hp, lfm_hip.synth_opts(0x51, bias_sigma=0.1))
+    by_name = {name: data for name, _, _, data in tensors}
+    o = oracle_engine(oracle, hp, tensors, ctx=8)
+    norm_w = by_name["blk.1.ffn_norm.weight"].astype(np.float64)
+    rw = by_name["blk.1.ffn_gate_inp.weight"].astype(np.float64).reshape(hp.n_expert, hp.dim)
+    bias = by_name["blk.1.exp_probs_b.bias"].astype(np.float64)
+    for s in range(20):
+        x = lfm_hip.synth_normal(0x77 + s, "route.layer", hp.dim)
+        ids, w, scores, logits = o.route_layer(1, x)
+        o.run_ffn(1, x)
+        ids2, w2, scores2 = o.last_route(1)
+        assert ids == ids2 and np.array_equal(w, w2) and np.array_equal(scores, scores2)
+        x64 = x.astype(np.float64)
+        h = x64 / np.sqrt(np.mean(x64 * x64) + 1e-5) * norm_w
+        lg = rw @ h
+        assert np.allclose(logits, lg, rtol=1e-5, atol=1e-6)
+        p = 1.0 / (1.0 + np.exp(-lg))
+        sc = p + bias
+        assert np.allclose(scores, sc, rtol=0, atol=1e-6)
+        order = np.argsort(-sc, kind="stable")
+        if sc[order[3]] - sc[order[4]] > 1e-5:
+            assert ids == [int(i) for i in order[:4]]
+            assert np.allclose(w, p[order[:4]] / p[order[:4]].sum(), rtol=1e-5)
