@@ -210,6 +210,16 @@ int lfm_q6k_gemm(const void *packed_dev, uint64_t rows, uint64_t in_dim, const f
 
 /* ---- argmax (engine/src/kernels/persistent.rs:11-53 semantics) ------------ */
 int lfm_argmax(const float *v_dev, uint32_t n, uint32_t *index, float *value);
+/* No counterpart in the reference.  The argmax of lfm_argmax (same kernels, same
+ * result) for callers that cannot allocate device memory: tight serving loops and
+ * harnesses that forbid hipMalloc.  It allocates nothing: its state block and
+ * first-stage partials live in a fixed 8448-byte device array of the library's
+ * own code object, one copy per device, whose address the device's first
+ * launching call (lfm_engine_create, lfm_argmax, ...) takes; before that it
+ * returns LFM_ESTATE.  The array size does not depend on n (at most 1024
+ * first-stage workgroups, grid-stride beyond).  Every call on a device shares
+ * that device's array: calls that overlap on one device race. */
+int lfm_argmax_noalloc(const float *v_dev, uint32_t n, uint32_t *index, float *value);
 
 /* ---- synthetic model (seeded; identical bytes on every host) -------------- */
 typedef struct lfm_tensor_desc {

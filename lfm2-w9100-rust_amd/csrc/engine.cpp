@@ -26,6 +26,7 @@
 #include "../../include/lfm_hip.h"
 #include "host_err.h"
 #include "kargs.h"
+#include "launch_host.h"
 
 // ------------------------------------------------------------------ errors
 static thread_local std::string g_err;
@@ -254,6 +255,14 @@ static int get_kernels(Kernels **out)
         (void)hipModuleUnload(k->pmod);
         delete k;
         return fail(LFM_EDEVICE, "device state allocation failed");
+    }
+    const int src = lfm_noalloc_setup(dev);
+    if (src != LFM_OK) {
+        (void)hipFree(k->idle_st);
+        (void)hipModuleUnload(k->mod);
+        (void)hipModuleUnload(k->pmod);
+        delete k;
+        return src;
     }
     g_kernels[dev] = k;
     *out = k;
@@ -648,14 +657,30 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     return rc;
 }
 
-// Stand-alone argmax uses a small private state block per device.
+uint32_t lfm_argmax_grid(uint32_t n)
+{
+    return std::max<uint32_t>(1, std::min<uint32_t>((n + 255) / 256, NOALLOC_ARGMAX_WGS));
+}
+
+int lfm_argmax_enqueue(const float *v, uint32_t n, DevState *st, float *partial, hipStream_t s)
+{
+    Kernels *K;
+    RC(get_kernels(&K));
+    const uint32_t grid = lfm_argmax_grid(n);
+    ArgmaxArgs a{v, partial, n, st};
+    FinalArgs f{partial, grid, nullptr, 0, st};
+    RC(launch(K->argmax, dim3(grid), 0, s, a));
+    return launch(K->argmax_final, dim3(1), 0, s, f);
+}
+
+// Stand-alone argmax with a state block and partials allocated per call.
 extern "C" int lfm_argmax(const float *v, uint32_t n, uint32_t *index, float *value)
 {
     if (!v || n == 0 || !index)
         return fail(LFM_EINVAL, "lfm_argmax: empty input");
     Kernels *K;
     RC(get_kernels(&K));
-    const uint32_t grid = std::min<uint32_t>((n + 255) / 256, 1024);
+    const uint32_t grid = lfm_argmax_grid(n);
     DevState *st = nullptr;
     float *partial = nullptr;
     HIPCHK(hipMalloc(&st, sizeof(DevState)));
@@ -663,11 +688,7 @@ extern "C" int lfm_argmax(const float *v, uint32_t n, uint32_t *index, float *va
     DevState h;
     memset(&h, 0, sizeof(h));
     HIPCHK(hipMemcpy(st, &h, sizeof(h), hipMemcpyHostToDevice));
-    ArgmaxArgs a{v, partial, n, st};
-    FinalArgs f{partial, grid, nullptr, 0, st};
-    int rc = launch(K->argmax, dim3(grid), 0, nullptr, a);
-    if (rc == LFM_OK)
-        rc = launch(K->argmax_final, dim3(1), 0, nullptr, f);
+    int rc = lfm_argmax_enqueue(v, n, st, partial, nullptr);
     if (rc == LFM_OK) {
         HIPCHK(hipDeviceSynchronize());
         HIPCHK(hipMemcpy(&h, st, sizeof(h), hipMemcpyDeviceToHost));

@@ -164,6 +164,7 @@ def lib():
         "lfm_q6k_matvec_time": (i32, [P, u32, u64, u64, P, P, u32, pf32]),
         "lfm_q6k_gemm": (i32, [P, u64, u64, P, u32, P, P]),
         "lfm_argmax": (i32, [P, u32, pu32, pf32]),
+        "lfm_argmax_noalloc": (i32, [P, u32, pu32, pf32]),
         "lfm_synth_default_opts": (None, [C.POINTER(SynthOpts)]),
         "lfm_model_tensor_count": (i32, [C.POINTER(Hparams)]),
         "lfm_model_tensor_desc": (i32, [C.POINTER(Hparams), C.POINTER(SynthOpts), i32,
@@ -637,6 +638,15 @@ def argmax(v: np.ndarray):
     b = DeviceBuffer.from_array(v)
     idx, val = C.c_uint32(0), C.c_float(0)
     _check(lib().lfm_argmax(b.ptr, v.size, C.byref(idx), C.byref(val)))
+    return idx.value, val.value
+
+
+def argmax_device(buf: "DeviceBuffer", n: int, noalloc: bool = False):
+    """Argmax of n floats already on the device -> (index, value); noalloc uses
+    the entry point that allocates nothing (lfm_argmax_noalloc)."""
+    idx, val = C.c_uint32(0), C.c_float(0)
+    fn = lib().lfm_argmax_noalloc if noalloc else lib().lfm_argmax
+    _check(fn(buf.ptr, n, C.byref(idx), C.byref(val)))
     return idx.value, val.value
 
 
