@@ -1,11 +1,15 @@
-"""The command-line drivers on the GPU, against the same engine driven in-process.
+"""The command-line drivers on the GPU, against the oracle and against the same
+engine driven in-process.
 
 lfm2-greedy (engine/src/main.rs:157-280, --tokens form): the result object's keys
 and tokens, the BENCH_TIMING line, and LFM_FORWARD_OUT_DIR's per-step logits.
 api_stream (engine/src/bin/api_stream.rs:33-85): ready / accepted / delta / result
 events, a prompt longer than one 64-token prefill chunk, a second request on a
 fresh session, and a validation error in between.  The in-process replica makes
-the same engine calls, so tokens must be identical."""
+the same engine calls, so tokens must be identical.  Every token the drivers
+print is also checked against the oracle (fed from the seeded generator, not the
+file), teacher-forced with the drivers' own tokens: equal wherever the oracle's
+top-2 margin exceeds 1e-3 * max|logit|."""
 import json
 import os
 import subprocess
@@ -14,26 +18,57 @@ import numpy as np
 import pytest
 
 from conftest import PKG
+from model_util import model_tensors, oracle_engine, top2_margin
 
 pytestmark = pytest.mark.gpu
+OPTS_SEED = 11
 
 GREEDY = os.path.join(PKG, "lfm2-greedy")
 API = os.path.join(PKG, "api_stream")
 ENV = dict(os.environ, LFM_ANY_GEOMETRY="1")
 
 
+def cli_hparams(L):
+    return L.make_hparams(dim=512, heads=8, n_layers=3, attention_layers=(1,), kv=2, vocab=1000,
+                          eos=1 << 30, n_expert=8, n_used=4, expert_ff=512, n_ff=1024,
+                          dense_lead=1)
+
+
 @pytest.fixture(scope="module")
 def model(gpu, tmp_path_factory):
     L = gpu
-    hp = L.make_hparams(dim=512, heads=8, n_layers=3, attention_layers=(1,), kv=2, vocab=1000,
-                        eos=1 << 30, n_expert=8, n_used=4, expert_ff=512, n_ff=1024,
-                        dense_lead=1)
     p = str(tmp_path_factory.mktemp("cli") / "cli.gguf")
-    L.write_synthetic_gguf(p, hp, L.synth_opts(seed=11, bias_sigma=0.1), threads=16)
+    L.write_synthetic_gguf(p, cli_hparams(L), L.synth_opts(seed=OPTS_SEED, bias_sigma=0.1),
+                           threads=16)
     return p
 
 
-def test_lfm2_greedy_tokens(gpu, model, tmp_path):
+@pytest.fixture(scope="module")
+def cli_oracle(gpu, oracle):
+    hp = cli_hparams(gpu)
+    o = oracle_engine(oracle, hp, model_tensors(hp, gpu.synth_opts(seed=OPTS_SEED, bias_sigma=0.1)),
+                      ctx=4096)
+    yield o
+    o.close()
+
+
+def oracle_check(oracle, o, prompt, tokens):
+    """The greedy tokens a driver printed for `prompt` (tokens[0] from the prompt's
+    last logits) against the oracle, teacher-forced; returns how many were
+    margin-clear (all of those must be equal)."""
+    o.reset()
+    lo = o.forward(prompt, 0)
+    compared = 0
+    for s, t in enumerate(tokens):
+        if top2_margin(lo) > 1e-3 * float(np.abs(lo).max()):
+            assert t == oracle.argmax(lo), (s, t, oracle.argmax(lo))
+            compared += 1
+        if s + 1 < len(tokens):
+            lo = o.forward([t], len(prompt) + s)
+    return compared
+
+
+def test_lfm2_greedy_tokens(gpu, oracle, cli_oracle, model, tmp_path):
     L = gpu
     prompt, n = [5, 999, 0, 17, 256, 3], 12
     print("lfm2-greedy", prompt, n, flush=True)
@@ -59,6 +94,9 @@ def test_lfm2_greedy_tokens(gpu, model, tmp_path):
     want = [first] + e.decode_run(first, len(prompt), n - 1)
     e.close()
     assert out["tokens"] == want
+    compared = oracle_check(oracle, cli_oracle, prompt, out["tokens"])
+    print(f"lfm2-greedy: {compared}/{n} margin-clear tokens equal to the oracle's")
+    assert compared >= n // 2
 
     # host loop with every step's logits kept (main.rs:155-165, 192-219)
     keep = tmp_path / "steps"
@@ -74,7 +112,7 @@ def test_lfm2_greedy_tokens(gpu, model, tmp_path):
     assert np.array_equal(l0, logits)
 
 
-def test_api_stream_session(gpu, model):
+def test_api_stream_session(gpu, oracle, cli_oracle, model):
     L = gpu
     long_prompt = [int(x) for x in np.random.default_rng(2).integers(0, 1000, 100)]
     reqs = [{"id": "r1", "tokens": long_prompt, "n": 6},
@@ -119,4 +157,7 @@ def test_api_stream_session(gpu, model):
             pos += 1
         assert got["tokens"] == toks, (q["id"], got["tokens"], toks)
         assert [d["token"] for d in deltas if d["id"] == q["id"]] == toks
+        compared = oracle_check(oracle, cli_oracle, q["tokens"], got["tokens"])
+        print(f"api_stream {q['id']}: {compared}/{q['n']} margin-clear tokens equal to the oracle's")
+        assert compared >= q["n"] // 2
     e.close()
