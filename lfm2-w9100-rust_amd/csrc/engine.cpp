@@ -707,6 +707,7 @@ struct DevTensor {
     uint32_t nd = 0;
     uint64_t ne[4] = {1, 1, 1, 1};
     void *dev = nullptr;
+    void *tdev = nullptr; // router weights [ROUTE_WIDTH][ROUTE_EXPERTS]: the transposed copy
     size_t nbytes = 0;
     Q6T q6{};
 };
@@ -725,7 +726,8 @@ struct lfm_engine {
     uint32_t *ids = nullptr, *out_tokens = nullptr, *sel = nullptr;
     float *x = nullptr, *y = nullptr, *qkv = nullptr, *sw = nullptr, *rlogits = nullptr,
           *logits = nullptr, *hpart = nullptr, *apart = nullptr;
-    float *rpart = nullptr; // fused router partial sums [ROUTE_EXPERTS + 1][ROUTE_PARTS]
+    float *rpart = nullptr; // fused router expert partial sums [ROUTE_QUADS][ROUTE_PARTS] float4
+    float *rss = nullptr;   // fused router x^2 partial sums [ROUTE_PARTS]
     float *xw = nullptr;    // fused router: the new residual times the FFN norm weight [dim]
     std::vector<uint16_t *> kc, vc;
     // attention layers: attn_q, attn_k and attn_v rows concatenated into one
@@ -897,9 +899,33 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     auto old = e->tensors.find(name);
     if (old != e->tensors.end()) {
         (void)hipFree(old->second.dev);
+        if (old->second.tdev)
+            (void)hipFree(old->second.tdev);
         e->tensors.erase(old);
     }
-    HIPCHK(hipMalloc(&t.dev, want));
+    // Router weights at the fused router's shape ([ROUTE_WIDTH inputs] x
+    // [ROUTE_EXPERTS experts], expert-major as in the file) also get a
+    // transposed copy [input][expert]: the output projection reads one input
+    // row's 32 weights as one 128-byte line.
+    const size_t nlen = strlen(name), slen = strlen("ffn_gate_inp.weight");
+    if (type == LFM_GGML_TYPE_F32 && nd == 2 && ne[0] == ROUTE_WIDTH && ne[1] == ROUTE_EXPERTS &&
+        nlen >= slen && strcmp(name + nlen - slen, "ffn_gate_inp.weight") == 0) {
+        std::vector<float> tr((size_t)ROUTE_WIDTH * ROUTE_EXPERTS);
+        const float *src = (const float *)host;
+        for (uint32_t ex = 0; ex < ROUTE_EXPERTS; ++ex)
+            for (uint32_t k = 0; k < ROUTE_WIDTH; ++k)
+                tr[(size_t)k * ROUTE_EXPERTS + ex] = src[(size_t)ex * ROUTE_WIDTH + k];
+        HIPCHK(hipMalloc(&t.tdev, tr.size() * 4));
+        if (hipMemcpy(t.tdev, tr.data(), tr.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(t.tdev);
+            return fail(LFM_EDEVICE, "%s: transposed copy failed", name);
+        }
+    }
+    if (hipMalloc(&t.dev, want) != hipSuccess) {
+        if (t.tdev)
+            (void)hipFree(t.tdev);
+        return fail(LFM_EDEVICE, "%s: device allocation of %zu bytes failed", name, want);
+    }
     t.nbytes = want;
     hipError_t ce;
     if (type == LFM_GGML_TYPE_Q6_K) {
@@ -912,6 +938,8 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     }
     if (ce != hipSuccess) {
         (void)hipFree(t.dev);
+        if (t.tdev)
+            (void)hipFree(t.tdev);
         return fail(LFM_EDEVICE, "%s: upload of %zu bytes failed: %s", name, want,
                     hipGetErrorString(ce));
     }
@@ -964,9 +992,12 @@ static int launch_out_proj(lfm_engine *e, uint32_t l, MatvecArgs &m, bool fuse)
         return fail(LFM_EINTERNAL, "fused router: unexpected output projection shape");
     MatvecRouteArgs ra;
     ra.m = m;
-    ra.rw = f32(e, "blk.%u.ffn_gate_inp.weight", l);
+    ra.rwt = (const float *)tensor(e, "blk.%u.ffn_gate_inp.weight", l)->tdev;
+    if (!ra.rwt)
+        return fail(LFM_EINTERNAL, "fused router: layer %u has no transposed router weights", l);
     ra.rnorm = f32(e, "blk.%u.ffn_norm.weight", l);
     ra.rpart = e->rpart;
+    ra.rss = e->rss;
     ra.xw = e->xw;
     return launch_t(e->K->matvec_route, dim3(ROUTE_PARTS), 64 * ROUTE_ROWS, 0, e->stream, ra);
 }
@@ -1106,6 +1137,7 @@ static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
     if (fused) {
         g.route.logits = nullptr;
         g.route.rpart = e->rpart;
+        g.route.rss = e->rss;
         g.route.xw = e->xw;
         RC(launch_gateup_fused(e, g));
     } else {
@@ -1252,9 +1284,11 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMalloc(&e->qkv, (dim + 2 * max_hdkv) * 4));
     HIPCHK(hipMalloc(&e->sw, swn * 4));
     HIPCHK(hipMalloc(&e->rlogits, 64 * 4));
-    HIPCHK(hipMalloc(&e->rpart, (ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4));
+    HIPCHK(hipMalloc(&e->rpart, ROUTE_EXPERTS * ROUTE_PARTS * 4));
+    HIPCHK(hipMalloc(&e->rss, ROUTE_PARTS * 4));
     HIPCHK(hipMalloc(&e->xw, ROUTE_WIDTH * 4));
-    HIPCHK(hipMemset(e->rpart, 0, (ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4));
+    HIPCHK(hipMemset(e->rpart, 0, ROUTE_EXPERTS * ROUTE_PARTS * 4));
+    HIPCHK(hipMemset(e->rss, 0, ROUTE_PARTS * 4));
     HIPCHK(hipMemset(e->xw, 0, ROUTE_WIDTH * 4));
     HIPCHK(hipMalloc(&e->logits, (size_t)hp.vocab * 4));
     HIPCHK(hipMemset(e->logits, 0, (size_t)hp.vocab * 4));
@@ -1338,10 +1372,13 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipGraphExecDestroy(e->g_layers);
     if (e->g_decode)
         (void)hipGraphExecDestroy(e->g_decode);
-    for (auto &kv : e->tensors)
+    for (auto &kv : e->tensors) {
         (void)hipFree(kv.second.dev);
+        if (kv.second.tdev)
+            (void)hipFree(kv.second.tdev);
+    }
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
-                    e->rlogits, e->rpart, e->xw, e->logits, e->hpart, e->apart, e->rope,
+                    e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot};
@@ -1838,6 +1875,7 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
             if (fused) {
                 a.route.logits = nullptr;
                 a.route.rpart = e->rpart;
+                a.route.rss = e->rss;
                 a.route.xw = e->xw;
                 rc = launch_gateup_fused(e, a);
             } else {

@@ -106,15 +106,20 @@ struct Route {
     const float *bias;
     uint32_t n_expert, n_used;
     uint32_t *sel_out;   // written by one wave: ids[8] then weights[8] (float bits)
-    const float *rpart;  // fused router: [ROUTE_EXPERTS + 1][ROUTE_PARTS] partial sums
+    const float *rpart;  // fused router: expert partial sums, [ROUTE_QUADS][ROUTE_PARTS] float4
+    const float *rss;    // fused router: partial sums of x_new^2 [ROUTE_PARTS]
     const float *xw;     // fused router: x_new * w_norm, the FFN's input before 1/rms [width]
 };
 
 // Fused router (the model's 32 experts at width 2048): the output projection
 // before the FFN runs ROUTE_PARTS workgroups of ROUTE_ROWS rows; each leaves
 // the partial dots sum_r R[e][r] * (x_new[r] * w_norm[r]) and sum_r x_new[r]^2
-// of its rows, which the gate/up kernel adds up.
+// of its rows, which the gate/up kernel adds up.  The expert partials are
+// stored quad-major: float4 q of workgroup p (experts 4q .. 4q+3) at
+// rpart[q * ROUTE_PARTS + p], so a workgroup writes 8 aligned 16-byte pieces and
+// a reader wave sums one quad's column with one float4 per lane and row.
 #define ROUTE_EXPERTS 32
+#define ROUTE_QUADS (ROUTE_EXPERTS / 4)
 #ifndef ROUTE_ROWS
 #define ROUTE_ROWS 8
 #endif
@@ -123,9 +128,10 @@ struct Route {
 
 struct MatvecRouteArgs { // y += W x (mode 1) and the router partial sums of the new y
     MatvecArgs m;
-    const float *rw;     // router weights [ROUTE_EXPERTS][rows] f32
+    const float *rwt;    // router weights transposed, [rows][ROUTE_EXPERTS] f32
     const float *rnorm;  // RMSNorm weight of the FFN input [rows]
-    float *rpart;        // [ROUTE_EXPERTS + 1][ROUTE_PARTS]
+    float *rpart;        // [ROUTE_QUADS][ROUTE_PARTS] float4 (see above)
+    float *rss;          // [ROUTE_PARTS]
     float *xw;           // [rows]: y_new * rnorm, read by the gate/up kernel
 };
 

@@ -361,11 +361,13 @@ extern "C" __global__ __launch_bounds__(1024) void k_q6_matvec16(const MatvecArg
 
 // Output projection y += W x (mode 1) with the router's first stage
 // (lfm.rs:599-607): one wave per row, ROUTE_ROWS rows per workgroup.  Wave w
-// (row r) loads R[e][r] for e = lane % 32 and w_norm[r] with its weights; once
-// its y[r] is known, lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32
-// y[r]^2, and wave 0 adds the workgroup's rows in order, leaving the partials
-// column-major in rpart for k_gateup8f.  Lane 0 also stores y[r] * w_norm[r]
-// in xw, the gate/up kernel's input.  The grid is exactly rows / ROUTE_ROWS.
+// (row r) loads row r of the transposed router weights (the 32 experts' R[e][r],
+// one 128-byte line) and w_norm[r] with its weights; once its y[r] is known,
+// lane e < 32 forms R[e][r] * (y[r] * w_norm[r]) and lane 32 y[r]^2.  Lanes
+// q < 8 of wave 0 then add the workgroup's rows in order for experts 4q..4q+3
+// and store them as one float4 (quad-major rpart), lane 8 the y^2 sum (rss).
+// Lane 0 also stores y[r] * w_norm[r] in xw, the gate/up kernel's input.  The
+// grid is exactly rows / ROUTE_ROWS.
 extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(const MatvecRouteArgs ra)
 {
     const MatvecArgs &a = ra.m;
@@ -382,7 +384,7 @@ extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(
     ISSUE_ORDER();
     const Lane w = load_lane_c(a.w, r, b, c);
     const float yold = a.y[r + vzero()];
-    const float rwe = ra.rw[(size_t)(lane & (ROUTE_EXPERTS - 1)) * a.w.rows + r];
+    const float rwe = ra.rwt[(size_t)r * ROUTE_EXPERTS + (lane & (ROUTE_EXPERTS - 1))];
     const float nwr = ra.rnorm[r + vzero()];
     keep_issued();
     if (halted)
@@ -401,12 +403,22 @@ extern "C" __global__ __launch_bounds__(64 * ROUTE_ROWS) void k_q6_matvec_route(
     else if (lane == ROUTE_EXPERTS)
         part[wave][lane] = v * v;
     __syncthreads();
-    if (wave == 0 && lane <= ROUTE_EXPERTS) {
+    if (wave == 0 && lane < ROUTE_QUADS) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < ROUTE_ROWS; ++i) {
+            acc.x += part[i][4 * lane + 0];
+            acc.y += part[i][4 * lane + 1];
+            acc.z += part[i][4 * lane + 2];
+            acc.w += part[i][4 * lane + 3];
+        }
+        reinterpret_cast<float4 *>(ra.rpart)[lane * ROUTE_PARTS + blockIdx.x] = acc;
+    } else if (wave == 0 && lane == ROUTE_QUADS) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < ROUTE_ROWS; ++i)
-            acc += part[i][lane];
-        ra.rpart[lane * ROUTE_PARTS + blockIdx.x] = acc;
+            acc += part[i][ROUTE_EXPERTS];
+        ra.rss[blockIdx.x] = acc;
     }
 }
 // Q6_K matvec for rows longer than 8 blocks (dense FFN down, 7168 inputs):
@@ -931,9 +943,9 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 
 // sw = g / (1 + exp(-g)) * u with g = Wg h, u = Wu h (lfm.rs:578-582, 655-659).
 // FUSED: the router logits are the sums of the partials left by
-// k_q6_matvec_route (each thread adds float4s of the 32 expert columns and one
-// of the x^2 column, then a wave or half-wave sums one column), logit = dot /
-// sqrt(sum x^2 / n + eps) as in k_router.  Its input needs no staging: each
+// k_q6_matvec_route: wave w adds quad w's column (experts 4w..4w+3; each lane
+// four rows, in row order, then a wave sum per expert) and every wave the x^2
+// column; logit = dot / sqrt(sum x^2 / n + eps) as in k_router.  Its input needs no staging: each
 // lane loads its 32 values of xw = x_new * w_norm (stored by k_q6_matvec_route)
 // along with the partials, and 1 / rms comes from the x^2 column.
 // Routed: work item (rank, row) reads expert ids[rank]'s rows.  The router
@@ -943,7 +955,7 @@ extern "C" __global__ __launch_bounds__(256) void k_router(const RouterArgs a)
 template <int NW, int G, bool FUSED>
 __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
 {
-    static_assert(!FUSED || NW == 4 || NW == 8 || NW == 16, "fused router: 4, 8 or 16 waves");
+    static_assert(!FUSED || NW == ROUTE_QUADS, "fused router: one wave per quad of experts");
     const uint32_t halted = load_halt(a.st);
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[NW];
@@ -955,18 +967,17 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     const uint32_t n = a.wg.nb * 256;
     const uint32_t ff = a.ff, total = (routed ? a.route.n_used : 1u) * ff;
     const uint32_t W = gridDim.x * NW, first = blockIdx.x * NW + wave;
-    // router partial sums: column e (ROUTE_PARTS floats) holds QC float4; thread
-    // t loads float4 t + 64*NW*k of the 32 expert columns and float4 t % QC of
-    // the x^2 column
-    constexpr int QC = ROUTE_PARTS / 4, NK = ROUTE_EXPERTS * QC / (64 * NW);
-    static_assert(QC == 32 || QC == 64, "a column is a half wave or a wave of float4");
+    // router partial sums: lane l of wave w loads rows l + 64k (k < NK) of quad
+    // w's column and float4 l of the x^2 column
+    constexpr int NK = ROUTE_PARTS / 64;
+    static_assert(ROUTE_PARTS == 256, "a wave holds the x^2 column as one float4 per lane");
     float4 pv[NK + 1];
     if constexpr (FUSED) {
-        const float4 *pp = reinterpret_cast<const float4 *>(a.route.rpart);
+        const float4 *pp = reinterpret_cast<const float4 *>(a.route.rpart) + wave * ROUTE_PARTS;
 #pragma unroll
         for (int k = 0; k < NK; ++k)
-            pv[k] = pp[threadIdx.x + 64 * NW * k];
-        pv[NK] = pp[ROUTE_EXPERTS * QC + (threadIdx.x & (QC - 1))];
+            pv[k] = pp[lane + 64 * k];
+        pv[NK] = reinterpret_cast<const float4 *>(a.route.rss)[lane];
     }
     RouteIn rin = route_load_all(a.route, a.src.x_out ? a.src.x_out : a.src.x);
     XRaw raw;
@@ -976,28 +987,23 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
     else
         x_issue(a.src, n, a.st, raw);
     if constexpr (FUSED) {
-        float f[NK + 1];
+        float4 q = pv[0];
 #pragma unroll
-        for (int k = 0; k <= NK; ++k)
-            f[k] = (pv[k].x + pv[k].y) + (pv[k].z + pv[k].w);
-        if constexpr (QC == 32) { // two columns per wave (one per half)
-            half_wave_sums<NK + 1>(f);
-            if ((lane & 31) == 31) {
+        for (int k = 1; k < NK; ++k) {
+            q.x += pv[k].x;
+            q.y += pv[k].y;
+            q.z += pv[k].z;
+            q.w += pv[k].w;
+        }
+        float f[5] = {q.x, q.y, q.z, q.w,
+                      (pv[NK].x + pv[NK].y) + (pv[NK].z + pv[NK].w)};
+        wave_sums<5>(f);
+        if (lane == 0) {
 #pragma unroll
-                for (int k = 0; k < NK; ++k)
-                    rsum[wave * 2 + (lane >> 5) + 2 * NW * k] = f[k];
-                if (threadIdx.x == 31)
-                    rsum[ROUTE_EXPERTS] = f[NK];
-            }
-        } else { // one column per wave
-            wave_sums<NK + 1>(f);
-            if (lane == 0) {
-#pragma unroll
-                for (int k = 0; k < NK; ++k)
-                    rsum[wave + NW * k] = f[k];
-                if (threadIdx.x == 0)
-                    rsum[ROUTE_EXPERTS] = f[NK];
-            }
+            for (int c = 0; c < 4; ++c)
+                rsum[4 * wave + c] = f[c];
+            if (wave == 0)
+                rsum[ROUTE_EXPERTS] = f[4];
         }
         __syncthreads();
         // logit = dot / sqrt(sum x^2 / n + eps), with the hardware reciprocal
