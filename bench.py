@@ -277,6 +277,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-decode-256", action="store_true",
+                    help="when --steps < 256, skip the extra untimed-for-value full 256-token "
+                         "decode pass (rocprofv3 kernel tracing faults on a host-side buffer over "
+                         "one 256-replay decode call; traced runs use --steps 64 and this flag)")
     ap.add_argument("--synthetic-state", action="store_true",
                     help="skip the prefill: restore a seeded binary16 KV / conv state for the "
                          "prompt positions instead (isolates decode kernels for profiling)")
@@ -344,7 +348,7 @@ def main():
         f"{decode_gbs:.0f} GB/s algorithmic")
 
     decode_256 = None
-    if fdt is None:
+    if fdt is None and not args.no_decode_256:
         eng.restore_session(n_prompt, snap)
         lfm_hip.lib().lfm_dev_synchronize()
         t0 = time.perf_counter()
