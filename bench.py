@@ -34,8 +34,8 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
 # HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes over this bench
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the scales are what the two
-# counters read for a plain 512 MiB copy): 1.02 x the algorithmic 24 155 264 bytes.
-GATEUP_TRAFFIC_BYTES = 24584196
+# counters read for a plain 512 MiB copy): 1.018 x the algorithmic 24 155 264 bytes.
+GATEUP_TRAFFIC_BYTES = 24588390
 SEED = 0x9E3779B97F4A7C15
 CTX = 4096          # context of the workload (positions 0..4095)
 N_PROMPT = 3840     # prompt tokens prefilled before decode
