@@ -622,10 +622,20 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     hipStream_t s = (hipStream_t)stream;
     uint16_t *hi = nullptr, *lo = nullptr;
     float *scale = nullptr;
-    HIPCHK(hipMalloc(&hi, (size_t)T * in_dim * 2));
-    HIPCHK(hipMalloc(&lo, (size_t)T * in_dim * 2));
+    // small calls (T <= GEMM_TOKENS) use the token-blocked layout, rows padded to 32
+    const size_t hrows = T <= GEMM_TOKENS ? (T + 31) / 32 * 32 : T;
+    HIPCHK(hipMalloc(&hi, hrows * in_dim * 2));
+    HIPCHK(hipMalloc(&lo, hrows * in_dim * 2));
     HIPCHK(hipMalloc(&scale, (size_t)T * 4));
-    SplitArgs sa{x, nullptr, 0.f, hi, lo, scale, T, (uint32_t)in_dim};
+    SplitArgs sa;
+    memset(&sa, 0, sizeof(sa));
+    sa.x = x;
+    sa.hi = hi;
+    sa.lo = lo;
+    sa.scale = scale;
+    sa.T = T;
+    sa.K = (uint32_t)in_dim;
+    sa.mode = T <= GEMM_TOKENS ? SPLIT_BLOCKED : SPLIT_ROWMAJOR;
     int rc = launch(K->split_rows, dim3(T), 0, s, sa);
     GemmArgs ga;
     memset(&ga, 0, sizeof(ga));
@@ -743,7 +753,7 @@ struct lfm_engine {
         float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr, *part = nullptr;
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
-        uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr;
+        uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr, *pos = nullptr;
     } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
@@ -1336,7 +1346,12 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         // batched prefill buffers, sized for a whole context in one call
         const size_t TC = e->ctx, E = hp.n_expert;
         const size_t wide = std::max<size_t>((size_t)hp.n_ff, 4 * (size_t)hp.expert_ff);
-        const size_t hmax = std::max<size_t>({TC * dim, TC * hp.n_ff, TC * 4 * hp.expert_ff});
+        // row-major hi / lo of a large call, or the token-blocked ones of a small call
+        // (rows padded to 32; the grouped expert inputs reserve a padded list per expert)
+        const size_t ts = (std::min<size_t>(TC, GEMM_TOKENS) + 31) / 32 * 32;
+        const size_t kmax = std::max<size_t>({(size_t)dim, (size_t)hp.n_ff, (size_t)hp.expert_ff});
+        const size_t hmax = std::max<size_t>({TC * dim, TC * hp.n_ff, TC * 4 * hp.expert_ff, ts * kmax,
+                                              E * ts * std::max<size_t>(dim, hp.expert_ff)});
         const size_t bcxw = std::max<size_t>(3 * (size_t)dim, (size_t)dim + 2 * max_hdkv);
         HIPCHK(hipMalloc(&e->pf.x, TC * dim * 4));
         HIPCHK(hipMalloc(&e->pf.bcx, TC * bcxw * 4));
@@ -1350,6 +1365,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.logits, TC * E * 4));
         HIPCHK(hipMalloc(&e->pf.wsel, TC * 4 * 4));
         HIPCHK(hipMalloc(&e->pf.sel, TC * 4 * 4));
+        HIPCHK(hipMalloc(&e->pf.pos, TC * 4 * 4));
         HIPCHK(hipMalloc(&e->pf.counts, E * 4));
         HIPCHK(hipMalloc(&e->pf.tok, E * TC * 4));
         HIPCHK(hipMalloc(&e->pf.slot, E * TC * 4));
@@ -1381,7 +1397,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
-                    e->pf.slot};
+                    e->pf.slot, e->pf.pos};
     for (void *p : bufs)
         if (p)
             (void)hipFree(p);
@@ -1411,12 +1427,35 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
 // matrix-core GEMM over the T tokens of the call, the conv is parallel in t,
 // attention is causal over the binary16 cache.  Leaves the last token's
 // residual in e->x (the decode path's residual) for the head.
-static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t T, uint32_t K)
+// RMSNorm (optional) + binary16 hi / lo split of `rows` activation rows for a
+// GEMM of a T-token call: row-major for large calls, token-blocked for the
+// small-call kernels (T <= GEMM_TOKENS), whose B reads expect that layout.
+// grouped: the rows feed the expert GEMMs; spr = expert slots per row (4 for
+// the token rows of the gate/up input, 1 for the slot rows of the down input).
+static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
+                    uint32_t T, bool grouped = false, uint32_t spr = 1)
 {
     if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
         return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
-    SplitArgs a{x, norm, e->hp.eps, e->pf.hi, e->pf.lo, e->pf.scale, T, K};
-    RC(launch(e->K->split_rows, dim3(T), 0, e->stream, a));
+    SplitArgs a;
+    memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.norm_w = norm;
+    a.eps = e->hp.eps;
+    a.hi = e->pf.hi;
+    a.lo = e->pf.lo;
+    a.scale = e->pf.scale;
+    a.T = rows;
+    a.K = K;
+    a.mode = T > GEMM_TOKENS ? SPLIT_ROWMAJOR : grouped ? SPLIT_GROUPED : SPLIT_BLOCKED;
+    if (a.mode == SPLIT_GROUPED) {
+        a.sel = e->pf.sel;
+        a.pos = e->pf.pos;
+        a.spr = spr;
+        a.n_used = e->hp.n_used;
+        a.rpe = (T + 31) / 32 * 32;
+    }
+    RC(launch(e->K->split_rows, dim3(rows), 0, e->stream, a));
     e->dispatches += 1;
     return LFM_OK;
 }
@@ -1463,6 +1502,7 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t 
     g.slot = e->pf.slot;
     g.counts = e->pf.counts;
     g.list_stride = e->ctx;
+    g.rpz = (T + 31) / 32 * 32;
     return launch_gemm(e->K, e->stream, g, true, T, e->hp.n_expert, 4 * T, e->hp.n_used, e->pf.part,
                        GEMM_PART_BYTES / 4, &e->dispatches);
 }
@@ -1483,6 +1523,7 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t
     g.slot = e->pf.slot;
     g.counts = e->pf.counts;
     g.list_stride = e->ctx;
+    g.rpz = (T + 31) / 32 * 32;
     g.zrows = zrows;
     g.c = c;
     g.ldc = ldc;
@@ -1494,14 +1535,14 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
-    RC(pf_split(e, e->pf.x, f32(e, "blk.%u.attn_norm.weight", l), T, dim));
+    RC(pf_split(e, e->pf.x, f32(e, "blk.%u.attn_norm.weight", l), T, dim, T));
     if (kv == 0) {
         RC(pf_gemm(e, q6(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0));
         ConvPrefillArgs c{e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l], e->pf.y, T,
                           dim};
         RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
         RC(launch(e->K->conv_state, dim3((dim + 255) / 256), 0, e->stream, c));
-        RC(pf_split(e, e->pf.y, nullptr, T, dim));
+        RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
         RC(pf_gemm(e, q6(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
         e->dispatches += 2;
         return LFM_OK;
@@ -1535,7 +1576,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
     } else {
         RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
     }
-    RC(pf_split(e, e->pf.y, nullptr, T, dim));
+    RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     RC(pf_gemm(e, q6(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
     e->dispatches += 2;
     return LFM_OK;
@@ -1549,10 +1590,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     const float *norm = f32(e, "blk.%u.ffn_norm.weight", l);
     if (l < hp.dense_lead) {
         const uint32_t ff = hp.n_ff;
-        RC(pf_split(e, x, norm, T, dim));
+        RC(pf_split(e, x, norm, T, dim, T));
         RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate.weight", l), q6(e, "blk.%u.ffn_up.weight", l), ff, T,
                           nullptr, e->pf.g, ff));
-        RC(pf_split(e, e->pf.g, nullptr, T, ff));
+        RC(pf_split(e, e->pf.g, nullptr, T, ff, T));
         RC(pf_gemm(e, q6(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
         return LFM_OK;
     }
@@ -1564,13 +1605,13 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     else
         RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
     RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
-                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx};
+                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx, e->pf.pos};
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
-    RC(pf_split(e, x, norm, T, dim));
+    RC(pf_split(e, x, norm, T, dim, T, true, 4));
     RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), q6(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
-    RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff)); // slots are token * 4 + rank
+    RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
     bool combined = false;
     RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,

@@ -197,13 +197,33 @@ struct CopyArgs { // plain device copy (achievable-bandwidth reference)
 // ---- prefill (multi-token) path ----------------------------------------------
 // RMSNorm (optional) + binary16 hi/lo split of T rows of K floats, with a per-row
 // power-of-two scale so that |x / scale| < 2^14 (hi/lo then hold ~22 bits).
+// Activations for the small-call GEMMs (calls of up to GEMM_TOKENS tokens) are
+// token-blocked: element k of logical row L at
+//   ((L / 32) * (K / 8) + k / 8) * 256 + (L % 32) * 8 + k % 8   (binary16),
+// so the B fragment of 32 rows and 8 k's is 512 contiguous bytes.
+__host__ __device__ inline size_t blocked_index(uint32_t L, uint32_t k, uint32_t K)
+{
+    return (((size_t)(L >> 5) * (K >> 3) + (k >> 3)) << 8) + ((L & 31) << 3) + (k & 7);
+}
+
+#define SPLIT_ROWMAJOR 0 // hi / lo [T][K] (large calls)
+#define SPLIT_BLOCKED 1  // blocked, logical row = source row
+#define SPLIT_GROUPED 2  // blocked, logical rows of the expert slots (see SplitArgs)
+
 struct SplitArgs {
     const float *x;      // [T][K]
     const float *norm_w; // nullable
     float eps;
-    uint16_t *hi, *lo;   // [T][K] binary16
-    float *scale;        // [T]
+    uint16_t *hi, *lo;   // binary16, layout by `mode`
+    float *scale;        // [T], per source row
     uint32_t T, K;
+    uint32_t mode;       // SPLIT_*
+    // SPLIT_GROUPED: source row t feeds slots s = t * spr .. t * spr + spr - 1 (spr 4:
+    // token rows of the gate/up input, spr 1: slot rows of the down input); slot s
+    // with rank s % 4 < n_used goes to logical row sel[s] * rpe + pos[s] (expert
+    // sel[s], index pos[s] in its token list, rpe rows reserved per expert)
+    const uint32_t *sel, *pos;
+    uint32_t spr, n_used, rpe;
 };
 
 // C[slot(n)][col0 + r] (+)= scale[tok(n)] * sum_k W[z*zrows + r][k] * X[tok(n)][k]
@@ -225,6 +245,7 @@ struct GemmArgs {
     // part[((s * (pair ? 2 : 1) + weight) * part_rows + out_row) * zrows + row]
     float *part;
     uint32_t ksplit, nz, part_rows;
+    uint32_t rpz;           // small calls, grouped: blocked activation rows per group (x 32)
 };
 
 struct GemmReduceArgs {    // c (+)= sum_s part[s] in slice order; pair: silu(g) * u
@@ -291,6 +312,7 @@ struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token
     uint32_t *tok;        // [n_expert][list_stride] activation row (token)
     uint32_t *slot;       // [n_expert][list_stride] slot = t*4 + rank
     uint32_t T, n_expert, n_used, list_stride;
+    uint32_t *pos;        // [T*4]: index of slot t*4 + rank in its expert's list
 };
 
 struct CombinePrefillArgs {  // x[t] += sum_r w[t][r] * D[t*4 + r] (rank order)

@@ -79,12 +79,38 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
     if (tid == 0)
         a.scale[t] = scale;
-    _Float16 *hi = reinterpret_cast<_Float16 *>(a.hi) + (size_t)t * a.K;
-    _Float16 *lo = reinterpret_cast<_Float16 *>(a.lo) + (size_t)t * a.K;
+    _Float16 *hi = reinterpret_cast<_Float16 *>(a.hi);
+    _Float16 *lo = reinterpret_cast<_Float16 *>(a.lo);
+    if (a.mode == SPLIT_ROWMAJOR) {
+        hi += (size_t)t * a.K;
+        lo += (size_t)t * a.K;
+#pragma unroll
+        for (int i = 0; i < SPLIT_NPT; ++i)
+            if (i < (int)nk)
+                split_f16(v[i] * rs, hi[i * WG_THREADS + tid], lo[i * WG_THREADS + tid]);
+        return;
+    }
+    _Float16 h[SPLIT_NPT], l[SPLIT_NPT];
 #pragma unroll
     for (int i = 0; i < SPLIT_NPT; ++i)
-        if (i < (int)nk)
-            split_f16(v[i] * rs, hi[i * WG_THREADS + tid], lo[i * WG_THREADS + tid]);
+        split_f16(v[i] * rs, h[i], l[i]);
+    const uint32_t nd = a.mode == SPLIT_GROUPED ? a.spr : 1u;
+    for (uint32_t j = 0; j < nd; ++j) { // uniform
+        uint32_t L = t;
+        if (a.mode == SPLIT_GROUPED) {
+            const uint32_t s = t * a.spr + j;
+            if ((s & 3) >= a.n_used)
+                continue;
+            L = a.sel[s] * a.rpe + a.pos[s];
+        }
+#pragma unroll
+        for (int i = 0; i < SPLIT_NPT; ++i)
+            if (i < (int)nk) {
+                const size_t o = blocked_index(L, i * WG_THREADS + tid, a.K);
+                hi[o] = h[i];
+                lo[o] = l[i];
+            }
+    }
 }
 
 #define TM 256 // weight rows per workgroup (4 waves of 64 rows)
@@ -467,8 +493,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         lb[i] = PAIR ? wave * 32 : wave * 32 * NI + i * 32;
         arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
     }
-    const uint32_t col = min(n0 + lr, ntok - 1);
-    const size_t brow = (size_t)(tokl ? tokl[col] : col) * K;
+    // activations token-blocked: this wave's 32 columns are logical tile lt (group
+    // z's tiles start at z * rpz / 32); lane (lr, p) reads k-piece 2q + p of row lr,
+    // lanes past the tile's last column re-read that column (same addresses, so an
+    // expert tile of ~8 tokens reads ~8 rows' bytes)
+    const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
+    const size_t btile = (size_t)lt * (K >> 3) * 256 + min(lr, ntok - 1 - n0) * 8;
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
@@ -486,11 +516,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     };
     // activation fragments of stage st: k-step ks reads k-piece ks * 2 + p
     auto loadB = [=](uint32_t st, half8 (&bh)[4], half8 (&bl)[4]) {
-        const size_t k = brow + ((size_t)kb0 * 4 + st) * TK;
+        const size_t kp0 = ((size_t)kb0 * 4 + st) * (TK / 8) + p;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            bh[q] = *reinterpret_cast<const half8 *>(xh + k + (q * 2 + p) * 8);
-            bl[q] = *reinterpret_cast<const half8 *>(xl + k + (q * 2 + p) * 8);
+            const size_t o = btile + (kp0 + 2 * q) * 256;
+            bh[q] = *reinterpret_cast<const half8 *>(xh + o);
+            bl[q] = *reinterpret_cast<const half8 *>(xl + o);
         }
     };
     auto loadD = [=](uint32_t kb, float (&d)[NI]) { // this lane's A rows, block kb of the slice
@@ -1152,6 +1183,8 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const Rou
         if (hit) {
             a.tok[(size_t)e * a.list_stride + off + before] = t;
             a.slot[(size_t)e * a.list_stride + off + before] = t * 4 + rank_of_e;
+            if (a.pos)
+                a.pos[t * 4 + rank_of_e] = off + before;
         }
         __syncthreads();
         if (tid == 0)
