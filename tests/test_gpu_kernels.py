@@ -103,17 +103,20 @@ def test_argmax_cases(gpu, oracle):
 
 
 @pytest.mark.parametrize("rows,in_dim,T", [(6144, 2048, 200), (130, 256, 7), (1792, 2048, 129),
-                                           (2048, 7168, 64), (256, 1792, 1)])
+                                           (2048, 7168, 64), (256, 1792, 1), (2048, 2048, 31),
+                                           (512, 1024, 32), (6144, 2048, 33), (1792, 2048, 128)])
 def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
     """Matrix-core GEMM (binary16 sc*(q-32) weights, hi/lo activations, fp32 d
-    scaling) against the f64 q6k_matvec oracle per token: rel-L2 <= 1e-5."""
+    scaling) against the f64 q6k_matvec oracle per token: rel-L2 <= 1e-5.  Calls
+    of up to 128 tokens read token-blocked activations (32-row tiles), so the
+    tokens on either side of a tile edge are checked too."""
     raw = blocks(rows * in_dim // 256, rows * 7 + T).reshape(-1)
     rng = np.random.default_rng(T)
     x = rng.standard_normal((T, in_dim)).astype(np.float32)
     x[0] *= 1000.0  # per-row scaling keeps large activations exact
     w = gpu.Q6Weight(raw, rows, in_dim)
     y = gpu.q6k_gemm(w, x)
-    for t in sorted({0, T // 2, T - 1}):
+    for t in sorted({0, T // 2, T - 1} | {t for t in (31, 32, 63, 64, 95, 96) if t < T}):
         ref = oracle.q6k_matvec(raw, in_dim, rows, x[t])
         err = rel_l2(y[t], ref)
         assert err <= 1e-5, (t, err)

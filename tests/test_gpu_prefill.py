@@ -71,8 +71,10 @@ def test_prefill_real_width(gpu, oracle, real_width, n):
     check_prefill(gpu, oracle, hp, tensors, n, ctx=512)
 
 
-@pytest.mark.parametrize("n", [129, 400])
+@pytest.mark.parametrize("n", [100, 128, 129, 400])
 def test_prefill_crowded_experts(gpu, oracle, crowded, n):
+    """8 experts top-2: at 100 and 128 tokens (small calls) experts hold more than one
+    32-row tile of gathered activations; at 129 and 400 the large-call kernels run."""
     hp, tensors = crowded
     check_prefill(gpu, oracle, hp, tensors, n, ctx=512)
 
