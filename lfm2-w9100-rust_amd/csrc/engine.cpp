@@ -373,6 +373,9 @@ extern "C" int lfm_dev_free(void *ptr)
 extern "C" int lfm_memcpy_htod(void *dst, const void *src, size_t n)
 {
     HIPCHK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+    // from pageable memory the copy may still be in flight when hipMemcpy
+    // returns: wait, so that work on any stream sees the data
+    HIPCHK(hipDeviceSynchronize());
     return LFM_OK;
 }
 extern "C" int lfm_memcpy_dtoh(void *dst, const void *src, size_t n)
@@ -1842,18 +1845,24 @@ extern "C" int lfm_restore_session(lfm_engine *e, uint32_t valid, const uint8_t 
             kh.resize((size_t)kv * e->ctx * 64);
             for (int which = 0; which < 2; ++which) {
                 uint16_t *dst = which ? e->vc[l] : e->kc[l];
-                HIPCHK(hipMemcpy(kh.data(), dst, kh.size() * 2, hipMemcpyDeviceToHost));
+                HIPCHK(hipMemcpyAsync(kh.data(), dst, kh.size() * 2, hipMemcpyDeviceToHost, e->stream));
+                HIPCHK(hipStreamSynchronize(e->stream));
                 for (uint32_t t = 0; t < valid; ++t)
                     for (uint32_t h = 0; h < kv; ++h)
                         for (uint32_t d = 0; d < 64; ++d)
                             kh[((size_t)h * e->ctx + t) * 64 + d] = lfm_f32_to_f16(in[o++]);
-                HIPCHK(hipMemcpy(dst, kh.data(), kh.size() * 2, hipMemcpyHostToDevice));
+                HIPCHK(hipMemcpyAsync(dst, kh.data(), kh.size() * 2, hipMemcpyHostToDevice, e->stream));
+                HIPCHK(hipStreamSynchronize(e->stream));
             }
         } else {
-            HIPCHK(hipMemcpy(e->conv[l], in + o, (size_t)e->hp.dim * 2 * 4, hipMemcpyHostToDevice));
+            HIPCHK(hipMemcpyAsync(e->conv[l], in + o, (size_t)e->hp.dim * 2 * 4, hipMemcpyHostToDevice,
+                                  e->stream));
+            HIPCHK(hipStreamSynchronize(e->stream));
             o += (size_t)e->hp.dim * 2;
         }
     }
+    // (every copy above ran on the engine stream and was waited for before its
+    // host buffer was reused: later engine work and the caller see the state)
     return LFM_OK;
 }
 
