@@ -107,7 +107,8 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows;
+        gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
+        tile_pack;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -238,7 +239,7 @@ static int get_kernels(Kernels **out)
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
                 {&k->gemm_q6_t32n1, "k_gemm_q6_t32n1"},
                 {&k->attn_merge_split, "k_attn_merge_split"}, {&k->reduce_combine, "k_reduce_combine"}, {&k->router_small, "k_router_prefill_small"},
-                {&k->embed_rows, "k_embed_rows"}};
+                {&k->embed_rows, "k_embed_rows"}, {&k->tile_pack, "k_q6_tile_pack"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
         if (e != hipSuccess) {
@@ -419,6 +420,33 @@ static Q6T q6view(const void *dev, uint64_t rows, uint64_t in_dim)
     t.rows = (uint32_t)rows;
     t.nb = (uint32_t)(in_dim / 256);
     return t;
+}
+
+// The prefill GEMMs' copy of a row-major Q6_K matrix of src.rows / group_rows
+// slices in 32-row tiles (layout at Q6Tiles), written by k_q6_tile_pack on s.
+static int make_tiles(Kernels *K, hipStream_t s, const Q6T &src, uint32_t group_rows, void **dev, Q6Tiles *out)
+{
+    *dev = nullptr;
+    if (group_rows == 0 || src.rows % group_rows)
+        return fail(LFM_EINVAL, "tile copy: %u rows are not whole slices of %u", src.rows, group_rows);
+    const uint32_t gtiles = (group_rows + 31) / 32;
+    const uint64_t tiles = (uint64_t)(src.rows / group_rows) * gtiles, ntb = tiles * src.nb;
+    if (ntb > 0x7FFFFFFFull)
+        return fail(LFM_EINVAL, "tile copy: %llu tile-blocks exceed the grid", (unsigned long long)ntb);
+    if (hipMalloc(dev, ntb * TILE_BYTES) != hipSuccess) {
+        *dev = nullptr;
+        return fail(LFM_EDEVICE, "tile copy: device allocation of %llu bytes failed",
+                    (unsigned long long)(ntb * TILE_BYTES));
+    }
+    TilePackArgs a{src, (uint8_t *)*dev, group_rows, gtiles, (uint32_t)tiles};
+    const int rc = launch_t(K->tile_pack, dim3((uint32_t)ntb), 64, 0, s, a);
+    if (rc != LFM_OK) {
+        (void)hipFree(*dev);
+        *dev = nullptr;
+        return rc;
+    }
+    *out = Q6Tiles{(const uint8_t *)*dev, (uint32_t)tiles, src.nb, gtiles, group_rows};
+    return LFM_OK;
 }
 
 static int check_q6_args(const void *packed, uint64_t rows, uint64_t in_dim)
@@ -642,7 +670,9 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     int rc = launch(K->split_rows, dim3(T), 0, s, sa);
     GemmArgs ga;
     memset(&ga, 0, sizeof(ga));
-    ga.w = q6view(packed, rows, in_dim);
+    void *tiles = nullptr;
+    if (rc == LFM_OK)
+        rc = make_tiles(K, s, q6view(packed, rows, in_dim), (uint32_t)rows, &tiles, &ga.w);
     ga.x_hi = hi;
     ga.x_lo = lo;
     ga.xscale = scale;
@@ -667,6 +697,8 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     (void)hipFree(scale);
     if (part)
         (void)hipFree(part);
+    if (tiles)
+        (void)hipFree(tiles);
     return rc;
 }
 
@@ -723,6 +755,8 @@ struct DevTensor {
     void *tdev = nullptr; // router weights [ROUTE_WIDTH][ROUTE_EXPERTS]: the transposed copy
     size_t nbytes = 0;
     Q6T q6{};
+    void *tiles_dev = nullptr; // prefill GEMM weights: the 32-row tile copy (at finalize)
+    Q6Tiles tiles{};
 };
 
 struct lfm_engine {
@@ -747,6 +781,8 @@ struct lfm_engine {
     // Q6_K tensor (plane layout), so prefill projects q, k, v in one GEMM
     std::vector<Q6T> qkvw;
     std::vector<void *> qkvdev;
+    std::vector<Q6Tiles> qkvt; // tile copies of qkvw (prefill)
+    std::vector<void *> qkvtdev;
     std::vector<float *> conv;
     uint32_t head_grid = 1, nchunk = 1;
     float *rope = nullptr; // [ctx][32] (cos, sin)
@@ -914,6 +950,8 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
         (void)hipFree(old->second.dev);
         if (old->second.tdev)
             (void)hipFree(old->second.tdev);
+        if (old->second.tiles_dev)
+            (void)hipFree(old->second.tiles_dev);
         e->tensors.erase(old);
     }
     // Router weights at the fused router's shape ([ROUTE_WIDTH inputs] x
@@ -972,6 +1010,8 @@ static const float *f32(lfm_engine *e, const char *fmt, uint32_t l = 0)
     return (const float *)tensor(e, fmt, l)->dev;
 }
 static Q6T q6(lfm_engine *e, const char *fmt, uint32_t l = 0) { return tensor(e, fmt, l)->q6; }
+// the prefill GEMMs' tile copy (made at finalize for every GEMM weight)
+static Q6Tiles q6tiles(lfm_engine *e, const char *fmt, uint32_t l = 0) { return tensor(e, fmt, l)->tiles; }
 
 // ------------------------------------------------------------------ step plan
 static XSrc xsrc(const float *x, const float *norm, float eps)
@@ -1330,6 +1370,30 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         }
         e->qkvw[l] = q6view(dst, rows, (uint64_t)nb * 256);
     }
+    // The prefill GEMMs read their weights from 32-row tile copies (one contiguous
+    // 1 KB / 512 B stretch per wave and load instead of 32 rows' pieces).
+    e->qkvtdev.assign(hp.n_layers, nullptr);
+    e->qkvt.assign(hp.n_layers, Q6Tiles{});
+    for (uint32_t l = 0; l < hp.n_layers; ++l)
+        if (hp.kv_heads[l])
+            RC(make_tiles(e->K, e->stream, e->qkvw[l], e->qkvw[l].rows, &e->qkvtdev[l], &e->qkvt[l]));
+    static const char *const gemm_weights[] = {"shortconv.in_proj.weight", "shortconv.out_proj.weight",
+                                               "attn_output.weight",       "ffn_gate.weight",
+                                               "ffn_up.weight",            "ffn_down.weight",
+                                               "ffn_gate_exps.weight",     "ffn_up_exps.weight",
+                                               "ffn_down_exps.weight"};
+    for (auto &kv : e->tensors) {
+        DevTensor &t = kv.second;
+        const size_t n = kv.first.size();
+        bool gemm = false;
+        for (const char *suf : gemm_weights) {
+            const size_t m = strlen(suf);
+            gemm = gemm || (n > m && kv.first.compare(n - m, m, suf) == 0 && kv.first[n - m - 1] == '.');
+        }
+        if (gemm && t.type == LFM_GGML_TYPE_Q6_K && t.nd >= 2 && !t.tiles_dev)
+            RC(make_tiles(e->K, e->stream, t.q6, (uint32_t)t.ne[1], &t.tiles_dev, &t.tiles));
+    }
+    HIPCHK(hipStreamSynchronize(e->stream));
     e->kc.assign(hp.n_layers, nullptr);
     e->vc.assign(hp.n_layers, nullptr);
     e->conv.assign(hp.n_layers, nullptr);
@@ -1395,7 +1459,12 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipFree(kv.second.dev);
         if (kv.second.tdev)
             (void)hipFree(kv.second.tdev);
+        if (kv.second.tiles_dev)
+            (void)hipFree(kv.second.tiles_dev);
     }
+    for (void *p : e->qkvtdev)
+        if (p)
+            (void)hipFree(p);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
@@ -1463,7 +1532,7 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
     return LFM_OK;
 }
 
-static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
+static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
                    uint32_t mode)
 {
     GemmArgs g;
@@ -1485,7 +1554,7 @@ static int pf_gemm(lfm_engine *e, const Q6T &w, uint32_t T, float *c, uint32_t l
 // for `zrows` rows per weight (128 of each per workgroup).  Dense (tok null): the
 // T tokens of the call; grouped: z = expert over the per-expert token lists, as
 // pf_gemm_grouped.
-static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t zrows, uint32_t T,
+static int pf_gemm_swiglu(lfm_engine *e, const Q6Tiles &wg, const Q6Tiles &wu, uint32_t zrows, uint32_t T,
                           const uint32_t *tok, float *c, uint32_t ldc)
 {
     GemmArgs g;
@@ -1512,7 +1581,7 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6T &wg, const Q6T &wu, uint32_t 
 
 // Grouped expert GEMM: z = expert, rows zrows per expert, activation rows from
 // `tok`, output rows `slot`, counts per expert on the device.
-static int pf_gemm_grouped(lfm_engine *e, const Q6T &w, uint32_t zrows, uint32_t T,
+static int pf_gemm_grouped(lfm_engine *e, const Q6Tiles &w, uint32_t zrows, uint32_t T,
                            const uint32_t *tok, float *c, uint32_t ldc,
                            const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr)
 {
@@ -1540,18 +1609,18 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
     const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
     RC(pf_split(e, e->pf.x, f32(e, "blk.%u.attn_norm.weight", l), T, dim, T));
     if (kv == 0) {
-        RC(pf_gemm(e, q6(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0));
+        RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0));
         ConvPrefillArgs c{e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l], e->pf.y, T,
                           dim};
         RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
         RC(launch(e->K->conv_state, dim3((dim + 255) / 256), 0, e->stream, c));
         RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
-        RC(pf_gemm(e, q6(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
+        RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
         e->dispatches += 2;
         return LFM_OK;
     }
     const uint32_t hdkv = 64 * kv, w = dim + 2 * hdkv;
-    RC(pf_gemm(e, e->qkvw[l], T, e->pf.bcx, w, 0, 0)); // rows q | k | v = columns of bcx
+    RC(pf_gemm(e, e->qkvt[l], T, e->pf.bcx, w, 0, 0)); // rows q | k | v = columns of bcx
     RopeKvArgs r{e->pf.bcx, f32(e, "blk.%u.attn_q_norm.weight", l),
                  f32(e, "blk.%u.attn_k_norm.weight", l), e->rope, hp.eps, e->kc[l], e->vc[l], T,
                  start, hp.heads, kv, e->ctx};
@@ -1580,7 +1649,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
     }
     RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
-    RC(pf_gemm(e, q6(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
+    RC(pf_gemm(e, q6tiles(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
     e->dispatches += 2;
     return LFM_OK;
 }
@@ -1594,10 +1663,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     if (l < hp.dense_lead) {
         const uint32_t ff = hp.n_ff;
         RC(pf_split(e, x, norm, T, dim, T));
-        RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate.weight", l), q6(e, "blk.%u.ffn_up.weight", l), ff, T,
+        RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate.weight", l), q6tiles(e, "blk.%u.ffn_up.weight", l), ff, T,
                           nullptr, e->pf.g, ff));
         RC(pf_split(e, e->pf.g, nullptr, T, ff, T));
-        RC(pf_gemm(e, q6(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
+        RC(pf_gemm(e, q6tiles(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
         return LFM_OK;
     }
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
@@ -1612,12 +1681,12 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
     RC(pf_split(e, x, norm, T, dim, T, true, 4));
-    RC(pf_gemm_swiglu(e, q6(e, "blk.%u.ffn_gate_exps.weight", l), q6(e, "blk.%u.ffn_up_exps.weight", l), eff,
+    RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
     bool combined = false;
-    RC(pf_gemm_grouped(e, q6(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,
+    RC(pf_gemm_grouped(e, q6tiles(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,
                        &combined));
     if (!combined)
         RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread

@@ -226,12 +226,43 @@ struct SplitArgs {
     uint32_t spr, n_used, rpe;
 };
 
+// Q6_K weights in 32-row tiles, the prefill GEMMs' copy (the matvecs read the
+// row-major planes of Q6T).  The matrix is `groups` slices of R rows (experts, or
+// one); tile t covers rows 32 (t % gtiles) .. + 31 of slice t / gtiles, gtiles =
+// ceil(R / 32), rows past R zero.  Tile-block tb = t * nb + kb holds those rows'
+// Q6_K block kb, as four planes over all tiles * nb tile-blocks, each ordered so
+// that lane l = 32 p + r of a wave (row r) loads one contiguous stretch.  In terms
+// of row r's block in the Q6T planes:
+//   ql [tb][q < 4][l][16 B]  its ql chunk 2q + p
+//   qh [tb][q < 4][l][8 B]   its qh bytes 8 (2q + p) .. + 7
+//   sc [tb][h < 2][r][8 B]   its scale groups 2h, 2h + 1
+//   d  [tb][r][2 B]          its d
+// 6720 B per tile-block, 210 B per row and block as in the row-major planes.
+#define TILE_QL 4096u
+#define TILE_QH 2048u
+#define TILE_SC 512u
+#define TILE_D 64u
+#define TILE_BYTES (TILE_QL + TILE_QH + TILE_SC + TILE_D)
+struct Q6Tiles {
+    const uint8_t *base;
+    uint32_t tiles;  // over all slices
+    uint32_t nb;     // Q6_K blocks per row
+    uint32_t gtiles; // tiles per slice
+    uint32_t rows;   // rows per slice (R)
+};
+
+struct TilePackArgs {   // row-major planes -> Q6Tiles
+    Q6T src;            // groups * group_rows rows
+    uint8_t *dst;
+    uint32_t group_rows, gtiles, tiles;
+};
+
 // C[slot(n)][col0 + r] (+)= scale[tok(n)] * sum_k W[z*zrows + r][k] * X[tok(n)][k]
 // for r < zrows, n < count; blockIdx.z = z selects a weight slice (expert) and
-// its token list (grouped GEMM).  Plain GEMM: zrows = w.rows, lists null.
+// its token list (grouped GEMM).  Plain GEMM: zrows = the rows of w, lists null.
 struct GemmArgs {
-    Q6T w;
-    Q6T w2;                 // pair kernel: the up weight (gate in w), same shape
+    Q6Tiles w;
+    Q6Tiles w2;             // pair kernel: the up weight (gate in w), same shape
     const uint16_t *x_hi, *x_lo;
     const float *xscale;
     const uint32_t *tok;    // [z][list_stride] activation rows, nullable

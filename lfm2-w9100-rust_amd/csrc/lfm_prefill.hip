@@ -146,6 +146,60 @@ struct AChunk {
     uint32_t sc;
 };
 
+// Lane `lane` (row lane % 32 of the tile, chunk parity lane / 32) of tile-block tb
+// of the Q6Tiles planes at wb (ntb tile-blocks): chunks 4h + p and 4h + 2 + p of
+// its row, i.e. half h of the block (5 loads: ql 1 KB and qh 512 B contiguous per
+// wave and chunk pair, both chunks' scale groups as one 8-byte load).
+__device__ __forceinline__ void load_tile_chunks(const uint8_t *wb, size_t ntb, size_t tb, uint32_t h,
+                                                 uint32_t lane, AChunk (&A)[2])
+{
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+        const uint32_t q = 2 * h + ch;
+        A[ch].ql = *reinterpret_cast<const uint4 *>(wb + tb * TILE_QL + q * 1024 + lane * 16);
+        A[ch].qh = *reinterpret_cast<const uint2 *>(wb + ntb * TILE_QL + tb * TILE_QH + q * 512 + lane * 8);
+    }
+    const uint2 sc = *reinterpret_cast<const uint2 *>(wb + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + h * 256 +
+                                                      (lane & 31) * 8);
+    A[0].sc = sc.x;
+    A[1].sc = sc.y;
+}
+
+// binary16 bits of d of row r of tile-block tb
+__device__ __forceinline__ uint32_t tile_d(const uint8_t *wb, size_t ntb, size_t tb, uint32_t r)
+{
+    return reinterpret_cast<const uint16_t *>(wb + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r];
+}
+
+// Row-major Q6_K planes -> Q6Tiles (the layout is described with the struct).
+// Workgroup tb (64 lanes, lane l = 32 p + r) writes tile-block tb: rows past the
+// slice's end are zero (d = 0: they contribute zero weights).
+extern "C" __global__ __launch_bounds__(64) void k_q6_tile_pack(const TilePackArgs a)
+{
+    const uint32_t tb = blockIdx.x, l = threadIdx.x, p = l >> 5, r = l & 31;
+    const uint32_t nb = a.src.nb, t = tb / nb, kb = tb - t * nb;
+    const uint32_t g = t / a.gtiles, row = (t - g * a.gtiles) * 32 + r;
+    const bool ok = row < a.group_rows;
+    const size_t nblk = (size_t)a.src.rows * nb, ntb = (size_t)a.tiles * nb;
+    const size_t blk = ((size_t)g * a.group_rows + (ok ? row : 0)) * nb + kb;
+    const uint8_t *s = a.src.base;
+    uint8_t *d = a.dst;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t c = 2 * q + p;
+        const uint4 vl = ok ? *reinterpret_cast<const uint4 *>(s + blk * 128 + c * 16) : make_uint4(0, 0, 0, 0);
+        const uint2 vh = ok ? *reinterpret_cast<const uint2 *>(s + nblk * 128 + blk * 64 + c * 8) : make_uint2(0, 0);
+        *reinterpret_cast<uint4 *>(d + tb * TILE_QL + q * 1024 + l * 16) = vl;
+        *reinterpret_cast<uint2 *>(d + ntb * TILE_QL + tb * TILE_QH + q * 512 + l * 8) = vh;
+    }
+    const uint2 vs = ok ? *reinterpret_cast<const uint2 *>(s + nblk * 192 + blk * 16 + p * 8) : make_uint2(0, 0);
+    *reinterpret_cast<uint2 *>(d + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + p * 256 + r * 8) = vs;
+    if (p == 0) {
+        const uint16_t vd = ok ? reinterpret_cast<const uint16_t *>(s + nblk * 208)[blk] : (uint16_t)0;
+        reinterpret_cast<uint16_t *>(d + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r] = vd;
+    }
+}
+
 // The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in
 // MFMA A-operand order, or zeros when the block scale d is zero.  Exact while
 // |sc * (q6 - 32)| <= 2048, within 1/2 ulp otherwise.
@@ -223,7 +277,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
-    const uint32_t rbase = z * a.zrows;
     const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
@@ -233,14 +286,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     __shared__ float dsh[2][TM], rsh[2][TM];
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
-    const size_t nblk = (size_t)a.w.rows * nb;
-    // row tile i of the wave: tile rows vb[i] .. vb[i] + 31, rows lb[i] .. of weight i (pair)
-    uint32_t vb[2], lb[2], arow[2];
+    const size_t ntb = (size_t)a.w.tiles * nb;
+    // row tile i of the wave: tile rows vb[i] .. vb[i] + 31, rows lb[i] .. of weight
+    // i (pair), weight tile wt[i] (tiles past the slice's last one read that one:
+    // their rows are not stored)
+    uint32_t vb[2], lb[2], wt[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         vb[i] = PAIR ? i * 128 + wave * 32 : wave * 64 + i * 32;
         lb[i] = PAIR ? wave * 32 : vb[i];
-        arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
+        wt[i] = z * a.w.gtiles + min((m0 + lb[i]) >> 5, a.w.gtiles - 1);
     }
     // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
     // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
@@ -255,17 +310,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) { // half block of the slice
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
-            const size_t blk = (size_t)arow[i] * nb + kb;
-#pragma unroll
-            for (int ch = 0; ch < 2; ++ch) {
-                const uint32_t c = 4 * h + 2 * ch + p;
-                A[i][ch].ql = *reinterpret_cast<const uint4 *>(wb + blk * 128 + c * 16);
-                A[i][ch].qh = *reinterpret_cast<const uint2 *>(wb + nblk * 128 + blk * 64 + c * 8);
-                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(wb + nblk * 192 + blk * 16 + (c >> 1) * 4);
-            }
-        }
+        for (int i = 0; i < 2; ++i)
+            load_tile_chunks(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
     auto loadB = [&](uint32_t st) { // stage st of the slice
         const uint32_t buf = st & 1;
@@ -279,10 +325,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
                                              (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
         }
     };
-    auto loadD = [=](uint32_t kb) -> float { // d of tile row tid, block kb of the slice
+    // d of tile row tid, block kb of the slice, as binary16 bits (converted where
+    // used, so the load does not wait for the weights issued before it)
+    auto loadD = [=](uint32_t kb) -> uint32_t {
         const uint8_t *wb = PAIR && tid >= 128 ? a.w2.base : a.w.base;
-        const uint32_t row = rbase + min(m0 + (PAIR ? tid & 127 : tid), a.zrows - 1);
-        return half_bits_to_float(reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)row * nb + kb0 + kb]);
+        const uint32_t v = PAIR ? tid & 127 : tid;
+        const uint32_t t = z * a.w.gtiles + min((m0 + v) >> 5, a.w.gtiles - 1);
+        return tile_d(wb, ntb, (size_t)t * nb + kb0 + kb, v & 31);
     };
     floatx16 acc[2][NJ];
 #pragma unroll
@@ -315,11 +364,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     AChunk A[2][2], An[2][2];
     loadA(0, A);
     loadB(0);
-    set_d(0, loadD(0));
+    set_d(0, half_bits_to_float(loadD(0)));
     __builtin_amdgcn_s_waitcnt(0);
     loadB(1);
     loadA(1, An);
-    float dnext = 0.f;
+    uint32_t dnext = 0;
     __syncthreads();
     for (uint32_t hb = 0; hb < nhb; ++hb) {
         const uint32_t db = (hb >> 1) & 1;
@@ -369,7 +418,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
                 }
             }
             if (q == 0 && (hb & 1) && hb + 1 < nhb) // stage 4kb + 2: publish block kb + 1's scale
-                set_d(((hb >> 1) + 1) & 1, dnext);
+                set_d(((hb >> 1) + 1) & 1, half_bits_to_float(dnext));
             __builtin_amdgcn_s_waitcnt(0); // this wave's pieces of stage st + 1 have landed
             __syncthreads();
             if (st + 2 < nst)
@@ -479,19 +528,20 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
     if (m0 >= a.zrows || n0 >= ntok)
         return;
-    const uint32_t rbase = z * a.zrows;
     const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
     const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
-    const size_t nblk = (size_t)a.w.rows * nb;
-    uint32_t lb[NI], arow[NI];
+    const size_t ntb = (size_t)a.w.tiles * nb;
+    // row tile i of the wave: rows lb[i] .. + 31 of the workgroup's, weight tile wt[i]
+    // (tiles past the slice's last one read that one: their rows are not stored)
+    uint32_t lb[NI], wt[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         lb[i] = PAIR ? wave * 32 : wave * 32 * NI + i * 32;
-        arow[i] = rbase + min(m0 + lb[i] + lr, a.zrows - 1);
+        wt[i] = z * a.w.gtiles + min((m0 + lb[i]) >> 5, a.w.gtiles - 1);
     }
     // activations token-blocked: this wave's 32 columns are logical tile lt (group
     // z's tiles start at z * rpz / 32); lane (lr, p) reads k-piece 2q + p of row lr,
@@ -502,17 +552,8 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
-            const size_t blk = (size_t)arow[i] * nb + kb;
-#pragma unroll
-            for (int ch = 0; ch < 2; ++ch) {
-                const uint32_t c = 4 * h + 2 * ch + p;
-                A[i][ch].ql = *reinterpret_cast<const uint4 *>(wb + blk * 128 + c * 16);
-                A[i][ch].qh = *reinterpret_cast<const uint2 *>(wb + nblk * 128 + blk * 64 + c * 8);
-                A[i][ch].sc = *reinterpret_cast<const uint32_t *>(wb + nblk * 192 + blk * 16 + (c >> 1) * 4);
-            }
-        }
+        for (int i = 0; i < NI; ++i)
+            load_tile_chunks(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
     // activation fragments of stage st: k-step ks reads k-piece ks * 2 + p
     auto loadB = [=](uint32_t st, half8 (&bh)[4], half8 (&bl)[4]) {
@@ -524,13 +565,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             bl[q] = *reinterpret_cast<const half8 *>(xl + o);
         }
     };
-    auto loadD = [=](uint32_t kb, float (&d)[NI]) { // this lane's A rows, block kb of the slice
+    // this lane's A rows' block scales d, block kb of the slice, as binary16 bits
+    // (converted where used, so the load does not wait for the weights issued before it)
+    auto loadD = [=](uint32_t kb, uint32_t (&d)[NI]) {
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint8_t *wb = PAIR && i ? a.w2.base : a.w.base;
-            d[i] = half_bits_to_float(
-                reinterpret_cast<const uint16_t *>(wb + nblk * 208)[(size_t)arow[i] * nb + kb0 + kb]);
-        }
+        for (int i = 0; i < NI; ++i)
+            d[i] = tile_d(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb0 + kb, lr);
     };
     floatx16 acc[NI];
 #pragma unroll
@@ -545,10 +585,11 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         for (int e = 0; e < 16; ++e)
             acc[i][e] *= __shfl(v, 8 * (e / 4) + 4 * p + (e % 4), 64);
     };
-    float u[NI], dcur[NI], dnext[NI];
+    float u[NI], dcur[NI];
+    uint32_t dbits[NI], dnext[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
-        u[i] = 1.0f, dnext[i] = 0.f;
+        u[i] = 1.0f, dnext[i] = 0;
     auto enter_block = [&](bool first) { // accumulators: sum_b d_b P_b / u
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -563,14 +604,17 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     AChunk A[NI][2], An[NI][2];
     half8 bch[4], bcl[4], bnh[4], bnl[4];
     loadA(0, A);
-    loadD(0, dcur);
+    loadD(0, dbits);
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        dcur[i] = half_bits_to_float(dbits[i]);
     loadB(0, bch, bcl);
     enter_block(true);
     for (uint32_t hb = 0; hb < nhb; ++hb) {
         if ((hb & 1) == 0 && hb > 0) {
 #pragma unroll
             for (int i = 0; i < NI; ++i)
-                dcur[i] = dnext[i];
+                dcur[i] = half_bits_to_float(dnext[i]);
             enter_block(false);
         }
         bool zero[NI];

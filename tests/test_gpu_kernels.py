@@ -104,12 +104,15 @@ def test_argmax_cases(gpu, oracle):
 
 @pytest.mark.parametrize("rows,in_dim,T", [(6144, 2048, 200), (130, 256, 7), (1792, 2048, 129),
                                            (2048, 7168, 64), (256, 1792, 1), (2048, 2048, 31),
-                                           (512, 1024, 32), (6144, 2048, 33), (1792, 2048, 128)])
+                                           (512, 1024, 32), (6144, 2048, 33), (1792, 2048, 128),
+                                           (1000, 512, 150), (1000, 512, 40)])
 def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
     """Matrix-core GEMM (binary16 sc*(q-32) weights, hi/lo activations, fp32 d
     scaling) against the f64 q6k_matvec oracle per token: rel-L2 <= 1e-5.  Calls
     of up to 128 tokens read token-blocked activations (32-row tiles), so the
-    tokens on either side of a tile edge are checked too."""
+    tokens on either side of a tile edge are checked too.  The weights are read
+    from a copy in 32-row tiles whose rows past the matrix are zero: 130 and
+    1000 rows end inside a tile, with both the 128-token and the 32-token tiles."""
     raw = blocks(rows * in_dim // 256, rows * 7 + T).reshape(-1)
     rng = np.random.default_rng(T)
     x = rng.standard_normal((T, in_dim)).astype(np.float32)
