@@ -113,6 +113,10 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     }
 }
 
+// s_waitcnt immediate (gfx9 encoding): vector-memory count <= n, LDS/scalar count 0,
+// export count unconstrained.
+#define WAITCNT_VM_LGKM0(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4))
+
 #define TM 256 // weight rows per workgroup (4 waves of 64 rows)
 #define TN 128 // token columns per workgroup (each wave covers all of them)
 #define TK 64  // K elements per stage (a quarter Q6_K block)
@@ -543,27 +547,32 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         lb[i] = PAIR ? wave * 32 : wave * 32 * NI + i * 32;
         wt[i] = z * a.w.gtiles + min((m0 + lb[i]) >> 5, a.w.gtiles - 1);
     }
-    // activations token-blocked: this wave's 32 columns are logical tile lt (group
-    // z's tiles start at z * rpz / 32); lane (lr, p) reads k-piece 2q + p of row lr,
-    // lanes past the tile's last column re-read that column (same addresses, so an
-    // expert tile of ~8 tokens reads ~8 rows' bytes)
+    // Activations token-blocked: the workgroup's 32 columns are logical tile lt
+    // (group z's tiles start at z * rpz / 32), whose 64-wide stage is 4 KB of hi and
+    // 4 KB of lo, contiguous.  The four waves load a stage into one LDS buffer
+    // (wave w: k-pieces 2w, 2w + 1, i.e. kilobyte w of each half; lanes past the
+    // tile's last column re-read that column, so an expert tile of ~8 tokens reads
+    // ~8 rows' bytes), double-buffered with one barrier per stage, and read their
+    // MFMA B fragments from there.
     const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
-    const size_t btile = (size_t)lt * (K >> 3) * 256 + min(lr, ntok - 1 - n0) * 8;
+    const size_t bsrc = (size_t)lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8;
+    __shared__ __attribute__((aligned(16))) _Float16 Bsh[2][2][8 * 256];
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             load_tile_chunks(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
-    // activation fragments of stage st: k-step ks reads k-piece ks * 2 + p
-    auto loadB = [=](uint32_t st, half8 (&bh)[4], half8 (&bl)[4]) {
-        const size_t kp0 = ((size_t)kb0 * 4 + st) * (TK / 8) + p;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const size_t o = btile + (kp0 + 2 * q) * 256;
-            bh[q] = *reinterpret_cast<const half8 *>(xh + o);
-            bl[q] = *reinterpret_cast<const half8 *>(xl + o);
-        }
+    // stage st's tile into LDS buffer st & 1 (this wave's two 16-byte pieces per lane)
+    auto loadB = [&](uint32_t st) {
+        const uint32_t buf = st & 1;
+        const size_t o = bsrc + ((size_t)kb0 * 4 + st) * (TK / 8) * 256;
+        __builtin_amdgcn_global_load_lds((const void *)(xh + o),
+                                         (__attribute__((address_space(3))) void *)&Bsh[buf][0][wave * 512],
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void *)(xl + o),
+                                         (__attribute__((address_space(3))) void *)&Bsh[buf][1][wave * 512],
+                                         16, 0, 0);
     };
     // this lane's A rows' block scales d, block kb of the slice, as binary16 bits
     // (converted where used, so the load does not wait for the weights issued before it)
@@ -602,13 +611,14 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     };
     const uint32_t nst = nbl * 4, nhb = nbl * 2;
     AChunk A[NI][2], An[NI][2];
-    half8 bch[4], bcl[4], bnh[4], bnl[4];
     loadA(0, A);
     loadD(0, dbits);
+    loadB(0);
+    __builtin_amdgcn_s_waitcnt(0); // stage 0's tile (and the first weights) have landed
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < NI; ++i)
         dcur[i] = half_bits_to_float(dbits[i]);
-    loadB(0, bch, bcl);
     enter_block(true);
     for (uint32_t hb = 0; hb < nhb; ++hb) {
         if ((hb & 1) == 0 && hb > 0) {
@@ -628,7 +638,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             // waiting for them does not wait for the next half block's weights and
             // scales, issued after them and used two stages later.
             if (st + 1 < nst)
-                loadB(st + 1, bnh, bnl);
+                loadB(st + 1); // into buffer 1 - q: every wave finished it before the last barrier
             if (q == 0) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (hb + 1 < nhb)
@@ -637,7 +647,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                     loadD((hb >> 1) + 1, dnext);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            half8 afc[NI];
+            half8 afc[NI], bch[4], bcl[4];
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) { // k-step kq reads k-piece 2 kq + p of row lr
+                bch[kq] = *reinterpret_cast<const half8 *>(&Bsh[q][0][(2 * kq + p) * 256 + lr * 8]);
+                bcl[kq] = *reinterpret_cast<const half8 *>(&Bsh[q][1][(2 * kq + p) * 256 + lr * 8]);
+            }
 #pragma unroll
             for (int i = 0; i < NI; ++i)
                 afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
@@ -661,9 +676,20 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                         afc[i] = afn[i];
                 }
             }
-#pragma unroll
-            for (int kq = 0; kq < 4; ++kq)
-                bch[kq] = bnh[kq], bcl[kq] = bnl[kq];
+            if (st + 1 < nst) {
+                // The next stage's tile has landed and every wave is done with buffer
+                // q.  Loads retire in issue order and the tile was issued before the
+                // next half block's weights (5 loads per tile) and block scales:
+                // waiting until at most 5 NI loads are outstanding leaves those weights
+                // in flight.
+                asm volatile("" ::: "memory");
+                if (q == 0 && hb + 1 < nhb)
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(5 * NI));
+                else
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+            }
         }
         if (hb + 1 < nhb) {
 #pragma unroll
