@@ -1504,11 +1504,10 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
 // small-call kernels (T <= GEMM_TOKENS), whose B reads expect that layout.
 // grouped: the rows feed the expert GEMMs; spr = expert slots per row (4 for
 // the token rows of the gate/up input, 1 for the slot rows of the down input).
-static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
-                    uint32_t T, bool grouped = false, uint32_t spr = 1)
+// The split's arguments for `rows` rows of width K in a call of T tokens.
+static SplitArgs split_args(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
+                            uint32_t T, bool grouped = false, uint32_t spr = 1)
 {
-    if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
-        return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
     SplitArgs a;
     memset(&a, 0, sizeof(a));
     a.x = x;
@@ -1527,6 +1526,15 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
         a.n_used = e->hp.n_used;
         a.rpe = (T + 31) / 32 * 32;
     }
+    return a;
+}
+
+static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
+                    uint32_t T, bool grouped = false, uint32_t spr = 1)
+{
+    if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
+        return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
+    const SplitArgs a = split_args(e, x, norm, rows, K, T, grouped, spr);
     RC(launch(e->K->split_rows, dim3(rows), 0, e->stream, a));
     e->dispatches += 1;
     return LFM_OK;
@@ -1672,15 +1680,16 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
     RouterPrefillArgs ra{x, norm, f32(e, "blk.%u.ffn_gate_inp.weight", l), hp.eps, e->pf.logits, T,
                          dim, E};
+    RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
+                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx, e->pf.pos};
     if (T <= GEMM_TOKENS) // few tokens: one workgroup per (expert, token)
         RC(launch(e->K->router_small, dim3(E, T), 0, e->stream, ra));
     else
         RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
-    RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
-                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx, e->pf.pos};
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
     RC(pf_split(e, x, norm, T, dim, T, true, 4));
+    e->dispatches += 3;
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
@@ -1690,7 +1699,7 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
                        &combined));
     if (!combined)
         RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread
-    e->dispatches += combined ? 3 : 4;
+    e->dispatches += combined ? 0 : 1;
     return LFM_OK;
 }
 

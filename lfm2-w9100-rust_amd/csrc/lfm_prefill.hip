@@ -33,26 +33,28 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
 // RMSNorm (optional) of T rows of x [T][K], then a binary16 hi/lo split of
 // x / scale with scale = 2^(e - 14) for max|x| = m * 2^e (so |x / scale| < 2^14).
 // One workgroup per token row; K is a multiple of 256 up to 8192 (the engine's
-// widths), so thread tid keeps its elements tid + 256 i in registers and the
-// row is read from memory once.
-#define SPLIT_NPT 32
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
+// widths).  Thread tid owns the 8-element pieces p = tid + 256 i of the row
+// (elements 8p .. 8p + 7), kept in registers, so the row is read once with
+// 16-byte loads and each piece's hi and lo are one 16-byte store in either
+// layout (row-major, or the token-blocked one where a piece of a logical row is
+// 16 contiguous bytes).
+#define SPLIT_NP 4 // pieces per thread: K <= 256 * 8 * SPLIT_NP
+
+// Pieces v of row t (np of them valid for this thread), RMS-normed here when
+// a.norm_w is set, split into hi / lo of v / scale (scale[t] written): into row
+// t (SPLIT_ROWMAJOR) or into the nl logical rows L[j] of the token-blocked layout.
+__device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8], const uint32_t *L,
+                                             uint32_t nl)
 {
-    const uint32_t t = blockIdx.x;
-    if (t >= a.T)
-        return;
-    const uint32_t tid = threadIdx.x, nk = a.K / WG_THREADS;
-    const float *x = a.x + (size_t)t * a.K;
+    const uint32_t tid = threadIdx.x, npc = a.K >> 3;
     __shared__ float red[4], redm[4];
-    float v[SPLIT_NPT];
-#pragma unroll
-    for (int i = 0; i < SPLIT_NPT; ++i)
-        v[i] = i < (int)nk ? x[i * WG_THREADS + tid] : 0.f;
     if (a.norm_w) { // uniform
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < SPLIT_NPT; ++i)
-            ss += v[i] * v[i];
+        for (int i = 0; i < SPLIT_NP; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                ss += v[i][j] * v[i][j];
         ss = wave_sum(ss);
         if ((tid & 63) == 0)
             red[tid >> 6] = ss;
@@ -60,14 +62,24 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
         const float tot = ((red[0] + red[1]) + red[2]) + red[3];
         const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
-        for (int i = 0; i < SPLIT_NPT; ++i)
-            if (i < (int)nk)
-                v[i] = v[i] * inv * a.norm_w[i * WG_THREADS + tid];
+        for (int i = 0; i < SPLIT_NP; ++i) {
+            const uint32_t pc = tid + WG_THREADS * i;
+            if (pc < npc) {
+                const float4 n0 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc);
+                const float4 n1 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc + 4);
+                const float nw[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    v[i][j] = v[i][j] * inv * nw[j];
+            }
+        }
     }
     float amax = 0.f;
 #pragma unroll
-    for (int i = 0; i < SPLIT_NPT; ++i)
-        amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < SPLIT_NP; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            amax = fmaxf(amax, fabsf(v[i][j]));
     amax = wave_max(amax);
     if ((tid & 63) == 0)
         redm[tid >> 6] = amax;
@@ -79,38 +91,62 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
     if (tid == 0)
         a.scale[t] = scale;
-    _Float16 *hi = reinterpret_cast<_Float16 *>(a.hi);
-    _Float16 *lo = reinterpret_cast<_Float16 *>(a.lo);
-    if (a.mode == SPLIT_ROWMAJOR) {
-        hi += (size_t)t * a.K;
-        lo += (size_t)t * a.K;
+    half8 *hi = reinterpret_cast<half8 *>(a.hi), *lo = reinterpret_cast<half8 *>(a.lo);
 #pragma unroll
-        for (int i = 0; i < SPLIT_NPT; ++i)
-            if (i < (int)nk)
-                split_f16(v[i] * rs, hi[i * WG_THREADS + tid], lo[i * WG_THREADS + tid]);
-        return;
-    }
-    _Float16 h[SPLIT_NPT], l[SPLIT_NPT];
+    for (int i = 0; i < SPLIT_NP; ++i) {
+        const uint32_t pc = tid + WG_THREADS * i;
+        if (pc >= npc)
+            continue;
+        half8 h, l;
 #pragma unroll
-    for (int i = 0; i < SPLIT_NPT; ++i)
-        split_f16(v[i] * rs, h[i], l[i]);
-    const uint32_t nd = a.mode == SPLIT_GROUPED ? a.spr : 1u;
-    for (uint32_t j = 0; j < nd; ++j) { // uniform
-        uint32_t L = t;
-        if (a.mode == SPLIT_GROUPED) {
-            const uint32_t s = t * a.spr + j;
-            if ((s & 3) >= a.n_used)
-                continue;
-            L = a.sel[s] * a.rpe + a.pos[s];
+        for (int j = 0; j < 8; ++j) {
+            _Float16 hh, ll;
+            split_f16(v[i][j] * rs, hh, ll);
+            h[j] = hh;
+            l[j] = ll;
         }
-#pragma unroll
-        for (int i = 0; i < SPLIT_NPT; ++i)
-            if (i < (int)nk) {
-                const size_t o = blocked_index(L, i * WG_THREADS + tid, a.K);
-                hi[o] = h[i];
-                lo[o] = l[i];
+        if (a.mode == SPLIT_ROWMAJOR) {
+            hi[(size_t)t * npc + pc] = h;
+            lo[(size_t)t * npc + pc] = l;
+        } else {
+            for (uint32_t q = 0; q < nl; ++q) { // uniform
+                const size_t o = ((size_t)(L[q] >> 5) * npc + pc) * 32 + (L[q] & 31);
+                hi[o] = h;
+                lo[o] = l;
             }
+        }
     }
+}
+
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
+{
+    const uint32_t t = blockIdx.x;
+    if (t >= a.T)
+        return;
+    const uint32_t tid = threadIdx.x, npc = a.K >> 3;
+    const float *x = a.x + (size_t)t * a.K;
+    float v[SPLIT_NP][8];
+#pragma unroll
+    for (int i = 0; i < SPLIT_NP; ++i) {
+        const uint32_t pc = tid + WG_THREADS * i;
+        float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+        if (pc < npc) {
+            x0 = *reinterpret_cast<const float4 *>(x + 8 * pc);
+            x1 = *reinterpret_cast<const float4 *>(x + 8 * pc + 4);
+        }
+        v[i][0] = x0.x, v[i][1] = x0.y, v[i][2] = x0.z, v[i][3] = x0.w;
+        v[i][4] = x1.x, v[i][5] = x1.y, v[i][6] = x1.z, v[i][7] = x1.w;
+    }
+    uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
+    if (a.mode == SPLIT_GROUPED) { // uniform
+        nl = 0;
+        for (uint32_t j = 0; j < a.spr; ++j) {
+            const uint32_t s = t * a.spr + j;
+            if ((s & 3) < a.n_used)
+                L[nl++] = a.sel[s] * a.rpe + a.pos[s];
+        }
+    }
+    split_pieces(a, t, v, L, nl);
 }
 
 // s_waitcnt immediate (gfx9 encoding): vector-memory count <= n, LDS/scalar count 0,
