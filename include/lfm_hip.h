@@ -88,8 +88,11 @@ int lfm_engine_create(const lfm_hparams *hp, int device, lfm_engine **out);
 int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_t ggml_type,
                              const uint64_t *ne, uint32_t n_dims, const void *host,
                              size_t nbytes);
-/* Verifies every tensor is present, allocates the resident state and captures
- * the decode graph.  Must precede any forward call. */
+/* Verifies every tensor is present, allocates the resident state, makes the
+ * prefill GEMMs' 32-row tile copies of their weights and captures the decode
+ * graph.  Must precede any forward call.  A failure after the tensor check
+ * (a device allocation) leaves the engine unusable: later calls to finalize
+ * return LFM_ESTATE, and the engine is to be destroyed. */
 int lfm_engine_finalize(lfm_engine *e);
 /* GpuEngine::set_ctx (gpu_lfm.rs:117): context capacity, 1..LFM_MAX_CTX.
  * Must be called before lfm_engine_finalize (default 4096). */

@@ -764,6 +764,7 @@ struct lfm_engine {
     int device = 0;
     uint32_t ctx = LFM_MAX_CTX;
     bool finalized = false;
+    bool finalize_started = false; // device allocation of lfm_engine_finalize began
     hipStream_t stream = nullptr;
     Kernels *K = nullptr;
     std::unordered_map<std::string, DevTensor> tensors;
@@ -1292,6 +1293,11 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         if (!ok)
             return fail(LFM_EINVAL, "tensor %s has the wrong type or shape", d.name);
     }
+    // From here on device buffers are allocated; a failure part-way leaves the
+    // engine to be destroyed (a second attempt would allocate them again).
+    if (e->finalize_started)
+        return fail(LFM_ESTATE, "an earlier lfm_engine_finalize failed part-way; destroy the engine");
+    e->finalize_started = true;
     const uint32_t dim = hp.dim;
     uint32_t max_hdkv = 0;
     for (uint32_t l = 0; l < hp.n_layers; ++l)
