@@ -324,7 +324,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TNW * TK];
     __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TNW * TK];
     __shared__ float dsh[2][TM], rsh[2][TM];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index as a wave-uniform value, so that the row-tile and weight
+    // addresses derived from it stay in scalar registers
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
     const size_t ntb = (size_t)a.w.tiles * nb;
     // row tile i of the wave: tile rows vb[i] .. vb[i] + 31, rows lb[i] .. of weight
@@ -340,12 +342,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
     // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
     // k-piece j ^ ((t >> 1) & 7)
-    uint32_t bsrc[NJ], bkq[NJ];
+    // (each piece's offset in halves, row * K + its swizzled k-piece, is below the
+    // hi / lo buffers' size: at most 4 slot rows per token of a 4096-token context
+    // at K = 1792, or 4096 rows of K <= 8192, well under 2^32)
+    uint32_t boff[NJ];
 #pragma unroll
     for (int v = 0; v < NJ; ++v) {
         const uint32_t t = (tid + GEMM_NTH * v) >> 3, col = min(n0 + t, ntok - 1);
-        bsrc[v] = tokl ? tokl[col] : col;
-        bkq[v] = ((tid & 7) ^ ((t >> 1) & 7)) * 8;
+        boff[v] = (tokl ? tokl[col] : col) * K + ((tid & 7) ^ ((t >> 1) & 7)) * 8;
     }
     auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) { // half block of the slice
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
@@ -355,13 +359,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     };
     auto loadB = [&](uint32_t st) { // stage st of the slice
         const uint32_t buf = st & 1;
-        const size_t k = ((size_t)kb0 * 4 + st) * TK;
+        const uint32_t k = (kb0 * 4 + st) * TK;
 #pragma unroll
         for (int v = 0; v < NJ; ++v) {
             const uint32_t u0 = (GEMM_NTH * v + 64 * wave) * 8;
-            __builtin_amdgcn_global_load_lds((const void *)(xh + (size_t)bsrc[v] * K + k + bkq[v]),
+            __builtin_amdgcn_global_load_lds((const void *)(xh + (boff[v] + k)),
                                              (__attribute__((address_space(3))) void *)&Bh[buf][u0], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void *)(xl + (size_t)bsrc[v] * K + k + bkq[v]),
+            __builtin_amdgcn_global_load_lds((const void *)(xl + (boff[v] + k)),
                                              (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
         }
     };
@@ -430,27 +434,28 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
                 const uint32_t kp = ks * 2 + p;
-                half8 afn[2], bfh[NJ], bfl[NJ];
+                // token tile j's fragments are read one tile ahead (two in registers)
+                half8 afn[2], bfh[2], bfl[2];
+                bfh[0] = *reinterpret_cast<const half8 *>(&Bh[q][swz(lr, kp)]);
+                bfl[0] = *reinterpret_cast<const half8 *>(&Bl[q][swz(lr, kp)]);
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) {
-                    bfh[j] = *reinterpret_cast<const half8 *>(&Bh[q][swz(j * 32 + lr, kp)]);
-                    bfl[j] = *reinterpret_cast<const half8 *>(&Bl[q][swz(j * 32 + lr, kp)]);
-                }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j], acc[i][j], 0, 0, 0);
-                if (ks < 3) {
+                    if (j + 1 < NJ) {
+                        bfh[(j + 1) & 1] = *reinterpret_cast<const half8 *>(&Bh[q][swz((j + 1) * 32 + lr, kp)]);
+                        bfl[(j + 1) & 1] = *reinterpret_cast<const half8 *>(&Bl[q][swz((j + 1) * 32 + lr, kp)]);
+                    }
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
-                        afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j & 1], acc[i][j], 0, 0, 0);
+                    if (j == 1 && ks < 3) {
+#pragma unroll
+                        for (int i = 0; i < 2; ++i)
+                            afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j & 1], acc[i][j], 0, 0, 0);
                 }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j], acc[i][j], 0, 0, 0);
                 if (ks < 3) {
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
@@ -572,7 +577,9 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
     const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
     const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index as a wave-uniform value, so that the row-tile and weight
+    // addresses derived from it stay in scalar registers
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const uint32_t p = lane >> 5, lr = lane & 31;
     const size_t ntb = (size_t)a.w.tiles * nb;
     // row tile i of the wave: rows lb[i] .. + 31 of the workgroup's, weight tile wt[i]
