@@ -648,6 +648,10 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
         return fail(LFM_EINVAL, "lfm_q6k_gemm: empty input");
     if (in_dim > 8192)
         return fail(LFM_EINVAL, "lfm_q6k_gemm: in_dim up to 8192");
+    // the GEMM kernels address the binary16 activation copies (T rows, padded to 32
+    // for small calls) with byte offsets below 2^31
+    if (((uint64_t)T + 31) * in_dim * 2 > 0x7fffffffull)
+        return fail(LFM_EINVAL, "lfm_q6k_gemm: (T + 31) x in_dim x 2 bytes must stay below 2 GiB");
     Kernels *K;
     RC(get_kernels(&K));
     hipStream_t s = (hipStream_t)stream;
@@ -1432,6 +1436,8 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.g, TC * wide * 4));
         HIPCHK(hipMalloc(&e->pf.d, TC * 4 * dim * 4));
         HIPCHK(hipMalloc(&e->pf.part, GEMM_PART_BYTES));
+        if (hmax * 2 > 0x7fffffffull) // the GEMM kernels use 32-bit byte offsets into hi / lo
+            return fail(LFM_ERANGE, "prefill activation copies of %zu bytes exceed 2 GiB", hmax * 2);
         HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));

@@ -163,6 +163,45 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
 // 16 consecutive tokens fall in distinct banks.
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kp) { return r * TK + ((kp ^ ((r >> 1) & 7)) << 3); }
 
+// Activation tiles reach LDS by 16-byte buffer loads (buffer_load_dwordx4 ... lds):
+// lane l's 16 bytes at byte offset voff of the buffer behind rs land in unit l of
+// the wave's 1 KB at dst.  Unlike global_load_lds, which the compiler's wait
+// insertion counts as an access to two memories (after which any use of a loaded
+// register waits for every outstanding load), a buffer load keeps the
+// vector-memory counter in issue order.  The restrict-qualified LDS pointers of
+// these helpers give the DMA and the fragment reads alias scopes, from which the
+// compiler sees that reading one buffer need not wait for the load into the other.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t act_rsrc(const uint16_t *base)
+{
+    // raw buffer: stride 0, offsets below 2^31 bytes (the host bounds the
+    // activation buffers), data format dword
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, _Float16 *__restrict__ dst)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, 0, 0, 0);
+}
+// One stage of a large call's hi and lo tiles: piece v of this wave, at byte offset
+// boff[v] + k of the hi / lo buffers, to 16-byte units 256 v + 64 wave + lane of
+// the tile (one call site per buffer pair, so that the compiler's per-store wait
+// slots are not exhausted).
+template <int NJ>
+__device__ __forceinline__ void lds_dma_stage(__amdgpu_buffer_rsrc_t rh, __amdgpu_buffer_rsrc_t rl, const uint32_t (&boff)[NJ],
+                                              uint32_t k, uint32_t wave, _Float16 *__restrict__ bh,
+                                              _Float16 *__restrict__ bl)
+{
+#pragma unroll
+    for (int v = 0; v < NJ; ++v) {
+        const uint32_t u0 = (256 * v + 64 * wave) * 8;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, (__attribute__((address_space(3))) void *)&bh[u0], 16, boff[v] + k, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (__attribute__((address_space(3))) void *)&bl[u0], 16, boff[v] + k, 0, 0, 0);
+    }
+}
+__device__ __forceinline__ half8 lds_frag(const _Float16 *__restrict__ b, uint32_t off)
+{
+    return *reinterpret_cast<const half8 *>(b + off);
+}
+
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // Two codes c0, c1 (bytes 0, 1 or 2, 3 of `c`) -> half2 (c - 32) exactly: the
 // byte permute forms binary16 0x64cc = 1024 + c, then 1056 is subtracted.
@@ -278,7 +317,7 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 //   * weights never touch LDS: each lane loads its rows' Q6_K bytes one half
 //     block ahead into registers and decodes the MFMA A fragments itself, the
 //     next k-step's fragments while the current k-step's MFMAs run;
-//   * activation tiles go global -> LDS directly (global_load_lds_dwordx4),
+//   * activation tiles go global -> LDS directly (buffer_load_dwordx4 ... lds),
 //     double-buffered, one barrier per stage;
 //   * the super-block scale d is folded into the accumulators: they hold
 //     sum_b d_b P_b / u with u the last nonzero d seen, so entering block b
@@ -289,6 +328,33 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool z
 // one XCD share activation tiles in its L2.  With ksplit > 1 the grid's z also
 // enumerates K slices: a workgroup runs its slice's blocks only and writes its
 // sums to part, which k_gemm_reduce adds up in slice order.
+// A lane's 16 accumulator rows of a 32-row tile are rb + 8 (e / 4) + e % 4 (rb =
+// the tile's first row + 4 p).  Writes v (add false) or adds it (add true) to those
+// rows of out below zrows.  With every row in range the old values are read in one
+// batch before the stores: element by element, each read would wait for the
+// previous store's address check and read in turn.
+__device__ __forceinline__ void store_rows16(float *out, uint32_t rb, uint32_t zrows, const float (&v)[16], bool add)
+{
+    if (rb + 27 < zrows) {
+        float o[16];
+        if (add) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                o[e] = out[rb + 8 * (e / 4) + (e % 4)];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            out[rb + 8 * (e / 4) + (e % 4)] = add ? o[e] + v[e] : v[e];
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const uint32_t r = rb + 8 * (e / 4) + (e % 4);
+        if (r < zrows)
+            out[r] = add ? out[r] + v[e] : v[e];
+    }
+}
+
 template <bool PAIR, int NJ>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 {
@@ -319,10 +385,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         return;
     const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
-    const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
-    const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
-    __shared__ __attribute__((aligned(16))) _Float16 Bh[2][TNW * TK];
-    __shared__ __attribute__((aligned(16))) _Float16 Bl[2][TNW * TK];
+    const __amdgpu_buffer_rsrc_t xh = act_rsrc(a.x_hi), xl = act_rsrc(a.x_lo);
+    // the two buffers of the hi and lo tiles as separate arrays, picked by the
+    // (unrolled) stage parity: the compiler can then tell that a stage's LDS reads do
+    // not touch the buffer the next tile is being loaded into, and does not wait for
+    // that load before them
+    __shared__ __attribute__((aligned(16))) _Float16 Bh0[TNW * TK], Bh1[TNW * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl0[TNW * TK], Bl1[TNW * TK];
     __shared__ float dsh[2][TM], rsh[2][TM];
     // the wave index as a wave-uniform value, so that the row-tile and weight
     // addresses derived from it stay in scalar registers
@@ -342,14 +411,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     // activation pieces: wave w, piece v fills 16-byte units 256v + 64w + lane of
     // a tile, i.e. token t = (tid + 256v) >> 3, unit j = tid & 7, which holds
     // k-piece j ^ ((t >> 1) & 7)
-    // (each piece's offset in halves, row * K + its swizzled k-piece, is below the
-    // hi / lo buffers' size: at most 4 slot rows per token of a 4096-token context
-    // at K = 1792, or 4096 rows of K <= 8192, well under 2^32)
+    // (each piece's byte offset, 2 (row * K + its swizzled k-piece), is below the
+    // hi / lo buffers' size, which the host keeps under 2^31 bytes)
     uint32_t boff[NJ];
 #pragma unroll
     for (int v = 0; v < NJ; ++v) {
         const uint32_t t = (tid + GEMM_NTH * v) >> 3, col = min(n0 + t, ntok - 1);
-        boff[v] = (tokl ? tokl[col] : col) * K + ((tid & 7) ^ ((t >> 1) & 7)) * 8;
+        boff[v] = ((tokl ? tokl[col] : col) * K + ((tid & 7) ^ ((t >> 1) & 7)) * 8) * 2;
     }
     auto loadA = [=](uint32_t half, AChunk (&A)[2][2]) { // half block of the slice
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
@@ -357,17 +425,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         for (int i = 0; i < 2; ++i)
             load_tile_chunks(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
-    auto loadB = [&](uint32_t st) { // stage st of the slice
-        const uint32_t buf = st & 1;
-        const uint32_t k = (kb0 * 4 + st) * TK;
-#pragma unroll
-        for (int v = 0; v < NJ; ++v) {
-            const uint32_t u0 = (GEMM_NTH * v + 64 * wave) * 8;
-            __builtin_amdgcn_global_load_lds((const void *)(xh + (boff[v] + k)),
-                                             (__attribute__((address_space(3))) void *)&Bh[buf][u0], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void *)(xl + (boff[v] + k)),
-                                             (__attribute__((address_space(3))) void *)&Bl[buf][u0], 16, 0, 0);
-        }
+    auto loadB = [&](uint32_t st, int buf) { // stage st of the slice into buffer buf = st & 1
+        _Float16 *bh = buf ? Bh1 : Bh0, *bl = buf ? Bl1 : Bl0;
+        static_assert(GEMM_NTH == 256, "piece layout");
+        lds_dma_stage<NJ>(xh, xl, boff, (kb0 * 4 + st) * TK * 2, wave, bh, bl);
     };
     // d of tile row tid, block kb of the slice, as binary16 bits (converted where
     // used, so the load does not wait for the weights issued before it)
@@ -406,79 +467,108 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     };
     const uint32_t nst = nbl * 4, nhb = nbl * 2; // stages; half block hb = stages 2hb, 2hb + 1
     AChunk A[2][2], An[2][2];
+    uint32_t dnext = 0;
+    float dnextf = 0.f;
+    bool zero[2];
+    // Stage st = 2 hb + q: issue stage st + 1's tile into buffer 1 - q (every wave
+    // finished reading it before the last barrier; stages 0 and 1 come from the
+    // prologue), then the next half block's weights and block scale at q = 0, then
+    // the MFMAs over buffer q, then wait for stage st + 1's tile and meet at the
+    // barrier.  The buffers arrive as restrict-qualified pointers so that the
+    // compiler sees that the stage's LDS reads do not touch the tile in flight.
+    auto stage = [&](uint32_t hb, int q, const _Float16 *__restrict__ bh, const _Float16 *__restrict__ bl,
+                     _Float16 *__restrict__ nh, _Float16 *__restrict__ nl) {
+        const uint32_t st = hb * 2 + q;
+        if (st >= 1 && st + 1 < nst)
+            lds_dma_stage<NJ>(xh, xl, boff, (kb0 * 4 + st + 1) * TK * 2, wave, nh, nl);
+        if (q == 0) {
+            if (hb > 0) { // the half block's weights, loaded one half block ahead
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int ch = 0; ch < 2; ++ch)
+                        A[i][ch] = An[i][ch];
+            }
+            if (hb + 1 < nhb)
+                loadA(hb + 1, An);
+            if ((hb & 1) == 0 && hb + 2 < nhb)
+                dnext = loadD((hb >> 1) + 1);
+        }
+        half8 afc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
+            const uint32_t kp = ks * 2 + p;
+            // token tile j's fragments are read one tile ahead (two in registers)
+            half8 afn[2], bfh[2], bfl[2];
+            bfh[0] = lds_frag(bh, swz(lr, kp));
+            bfl[0] = lds_frag(bl, swz(lr, kp));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if (j + 1 < NJ) {
+                    bfh[(j + 1) & 1] = lds_frag(bh, swz((j + 1) * 32 + lr, kp));
+                    bfl[(j + 1) & 1] = lds_frag(bl, swz((j + 1) * 32 + lr, kp));
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j & 1], acc[i][j], 0, 0, 0);
+                if (j == 1 && ks < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j & 1], acc[i][j], 0, 0, 0);
+            }
+            if (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    afc[i] = afn[i];
+            }
+        }
+        if (q == 0 && (hb & 1) && hb + 1 < nhb) // stage 4kb + 2: publish block kb + 1's scale
+            set_d(((hb >> 1) + 1) & 1, dnextf);
+        if (st + 1 < nst) {
+            // This wave's pieces of stage st + 1 have landed.  At q = 0 the next half
+            // block's weights (10 loads) and perhaps a block scale, issued after
+            // those pieces (loads retire in issue order), stay in flight: they are
+            // used a stage later.  The wait also retires this wave's LDS writes, so a
+            // bare barrier (no fence, which would wait for every load) publishes them.
+            asm volatile("" ::: "memory");
+            if (q == 0 && hb + 1 < nhb) {
+                if ((hb & 1) == 0 && hb + 2 < nhb)
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(11));
+                else
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(10));
+            } else {
+                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
+            }
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+    };
     loadA(0, A);
-    loadB(0);
+    loadB(0, 0);
     set_d(0, half_bits_to_float(loadD(0)));
     __builtin_amdgcn_s_waitcnt(0);
-    loadB(1);
-    loadA(1, An);
-    uint32_t dnext = 0;
+    loadB(1, 1);
     __syncthreads();
     for (uint32_t hb = 0; hb < nhb; ++hb) {
         const uint32_t db = (hb >> 1) & 1;
         if ((hb & 1) == 0 && hb > 0)
             rescale(db);
-        if ((hb & 1) == 0 && hb + 2 < nhb)
-            dnext = loadD((hb >> 1) + 1);
-        bool zero[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             zero[i] = dsh[db][vb[i] + lr] == 0.f;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) { // stage st = 2hb + q reads buffer q
-            const uint32_t st = hb * 2 + q;
-            half8 afc[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
-                const uint32_t kp = ks * 2 + p;
-                // token tile j's fragments are read one tile ahead (two in registers)
-                half8 afn[2], bfh[2], bfl[2];
-                bfh[0] = *reinterpret_cast<const half8 *>(&Bh[q][swz(lr, kp)]);
-                bfl[0] = *reinterpret_cast<const half8 *>(&Bl[q][swz(lr, kp)]);
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) {
-                    if (j + 1 < NJ) {
-                        bfh[(j + 1) & 1] = *reinterpret_cast<const half8 *>(&Bh[q][swz((j + 1) * 32 + lr, kp)]);
-                        bfl[(j + 1) & 1] = *reinterpret_cast<const half8 *>(&Bl[q][swz((j + 1) * 32 + lr, kp)]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfh[j & 1], acc[i][j], 0, 0, 0);
-                    if (j == 1 && ks < 3) {
-#pragma unroll
-                        for (int i = 0; i < 2; ++i)
-                            afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bfl[j & 1], acc[i][j], 0, 0, 0);
-                }
-                if (ks < 3) {
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        afc[i] = afn[i];
-                }
-            }
-            if (q == 0 && (hb & 1) && hb + 1 < nhb) // stage 4kb + 2: publish block kb + 1's scale
-                set_d(((hb >> 1) + 1) & 1, half_bits_to_float(dnext));
-            __builtin_amdgcn_s_waitcnt(0); // this wave's pieces of stage st + 1 have landed
-            __syncthreads();
-            if (st + 2 < nst)
-                loadB(st + 2); // into the buffer every wave has just finished reading
-        }
-        if (hb + 1 < nhb) { // the half block is done: take the next, prefetch the one after
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int ch = 0; ch < 2; ++ch)
-                    A[i][ch] = An[i][ch];
-            if (hb + 2 < nhb)
-                loadA(hb + 2, An);
-        }
+        stage(hb, 0, Bh0, Bl0, Bh1, Bl1);
+        stage(hb, 1, Bh1, Bl1, Bh0, Bl0);
+        if ((hb & 1) == 0 && hb + 2 < nhb) // landed at the half block's last wait
+            dnextf = half_bits_to_float(dnext);
     }
+    __syncthreads();
     rsh[0][tid] = u;
     __syncthreads();
     rescale(0);
@@ -495,35 +585,33 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
             for (int i = 0; i < 2; ++i) {
                 const uint32_t wi = PAIR ? i : 0;
                 float *pp = a.part + ((size_t)(ks * NW + wi) * a.part_rows + orow) * a.zrows;
+                float v[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
-                    if (r < a.zrows)
-                        pp[r] = acc[i][j][e] * xs;
-                }
+                for (int e = 0; e < 16; ++e)
+                    v[e] = acc[i][j][e] * xs;
+                store_rows16(pp, m0 + lb[i] + 4 * p, a.zrows, v, false);
             }
             continue;
         }
         float *out = a.c + (size_t)orow * a.ldc + a.col0;
         if (PAIR) {
+            float v[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t r = m0 + lb[0] + 8 * (e / 4) + 4 * p + (e % 4);
                 const float g = acc[0][j][e] * xs, u = acc[1][j][e] * xs;
-                if (r < a.zrows)
-                    out[r] = g / (1.0f + expf(-g)) * u;
+                v[e] = g / (1.0f + expf(-g)) * u;
             }
+            store_rows16(out, m0 + lb[0] + 4 * p, a.zrows, v, false);
             continue;
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) {
+            float v[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
-                const float v = acc[i][j][e] * xs;
-                if (r < a.zrows)
-                    out[r] = a.mode ? out[r] + v : v;
-            }
+            for (int e = 0; e < 16; ++e)
+                v[e] = acc[i][j][e] * xs;
+            store_rows16(out, m0 + lb[i] + 4 * p, a.zrows, v, a.mode != 0);
+        }
     }
 }
 
@@ -755,35 +843,33 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             float *pp = a.part + ((size_t)(ks * NW + (PAIR ? i : 0)) * a.part_rows + orow) * a.zrows;
+            float v[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
-                if (r < a.zrows)
-                    pp[r] = acc[i][e] * xs;
-            }
+            for (int e = 0; e < 16; ++e)
+                v[e] = acc[i][e] * xs;
+            store_rows16(pp, m0 + lb[i] + 4 * p, a.zrows, v, false);
         }
         return;
     }
     float *out = a.c + (size_t)orow * a.ldc + a.col0;
     if (PAIR) {
+        float v[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const uint32_t r = m0 + lb[0] + 8 * (e / 4) + 4 * p + (e % 4);
             const float g = acc[0][e] * xs, uu = acc[NI - 1][e] * xs;
-            if (r < a.zrows)
-                out[r] = g / (1.0f + expf(-g)) * uu;
+            v[e] = g / (1.0f + expf(-g)) * uu;
         }
+        store_rows16(out, m0 + lb[0] + 4 * p, a.zrows, v, false);
         return;
     }
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
+    for (int i = 0; i < NI; ++i) {
+        float v[16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t r = m0 + lb[i] + 8 * (e / 4) + 4 * p + (e % 4);
-            const float v = acc[i][e] * xs;
-            if (r < a.zrows)
-                out[r] = a.mode ? out[r] + v : v;
-        }
+        for (int e = 0; e < 16; ++e)
+            v[e] = acc[i][e] * xs;
+        store_rows16(out, m0 + lb[i] + 4 * p, a.zrows, v, a.mode != 0);
+    }
 }
 
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32(const GemmArgs a)
@@ -926,7 +1012,8 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
     if (t0 >= a.T)
         return;
     const uint32_t G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64, stride = dim + 2 * hdkv;
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, lh = lane >> 5;
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
+                   lh = lane >> 5;
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_K * FA_KROW];
     __shared__ __attribute__((aligned(16))) _Float16 Vt[2][64 * FA_VROW];
     const bool active = wave < G;

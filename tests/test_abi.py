@@ -42,6 +42,11 @@ def test_argument_errors_are_status_codes(lfm):
     hp = lfm.make_hparams()
     hp.conv_l_cache = 4
     assert L.lfm_engine_create(C.byref(hp), 0, C.byref(e)) == lfm.LFM_EINVAL
+    # 32-bit byte offsets into the binary16 activation copies bound T x in_dim; the
+    # check comes before any device work (the pointers are never dereferenced)
+    fake = C.c_void_p(256)
+    assert L.lfm_q6k_gemm(fake, 64, 2048, fake, 1 << 20, fake, None) == lfm.LFM_EINVAL
+    assert b"2 GiB" in L.lfm_last_error()
     hp = lfm.make_hparams()
     if lfm.device_count() == 0:
         assert L.lfm_engine_create(C.byref(hp), 0, C.byref(e)) == lfm.LFM_EDEVICE
