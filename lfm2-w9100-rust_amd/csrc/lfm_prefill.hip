@@ -197,6 +197,44 @@ __device__ __forceinline__ void lds_dma_stage(__amdgpu_buffer_rsrc_t rh, __amdgp
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (__attribute__((address_space(3))) void *)&bl[u0], 16, boff[v] + k, 0, 0, 0);
     }
 }
+// Keeps the loads on either side in program order (for counted waits that rely on
+// loads retiring in issue order): a compiler memory barrier and a scheduling barrier.
+__device__ __forceinline__ void issue_fence()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+// A small-call stage's eight B fragments: hi and lo of k-steps 0..3, 16 bytes at
+// byte offsets 1024 kq (hi) and 4096 + 1024 kq (lo) from the lane's address.  Issued
+// in one asm statement, so that the compiler's wait insertion, which cannot tell
+// these reads from reads of the tiles in flight once more than eight tile loads are
+// in the code, does not make them wait for those loads; lds_frags_wait completes
+// them (the stage's tile itself has landed: the barrier before the stage follows a
+// wait for it).
+__device__ __forceinline__ void lds_frags_issue(uint32_t addr, half8 (&h)[4], half8 (&l)[4])
+{
+    asm volatile("ds_read_b128 %0, %8\n\t"
+                 "ds_read_b128 %1, %8 offset:1024\n\t"
+                 "ds_read_b128 %2, %8 offset:2048\n\t"
+                 "ds_read_b128 %3, %8 offset:3072\n\t"
+                 "ds_read_b128 %4, %8 offset:4096\n\t"
+                 "ds_read_b128 %5, %8 offset:5120\n\t"
+                 "ds_read_b128 %6, %8 offset:6144\n\t"
+                 "ds_read_b128 %7, %8 offset:7168"
+                 : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(l[0]), "=&v"(l[1]), "=&v"(l[2]),
+                   "=&v"(l[3])
+                 : "v"(addr));
+}
+__device__ __forceinline__ void lds_frags_wait(half8 (&h)[4], half8 (&l)[4])
+{
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(h[0]), "+v"(h[1]), "+v"(h[2]), "+v"(h[3]), "+v"(l[0]), "+v"(l[1]), "+v"(l[2]), "+v"(l[3]));
+}
+// 32-bit LDS address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
 __device__ __forceinline__ half8 lds_frag(const _Float16 *__restrict__ b, uint32_t off)
 {
     return *reinterpret_cast<const half8 *>(b + off);
@@ -228,15 +266,27 @@ struct AChunk {
 // Lane `lane` (row lane % 32 of the tile, chunk parity lane / 32) of tile-block tb
 // of the Q6Tiles planes at wb (ntb tile-blocks): chunks 4h + p and 4h + 2 + p of
 // its row, i.e. half h of the block (5 loads: ql 1 KB and qh 512 B contiguous per
-// wave and chunk pair, both chunks' scale groups as one 8-byte load).
+// wave and chunk pair, both chunks' scale groups as one 8-byte load).  STREAM: the
+// ql / qh bytes are read once per call (small calls), so they are loaded
+// non-temporally and do not displace the activations from the caches.
+template <bool STREAM = false>
 __device__ __forceinline__ void load_tile_chunks(const uint8_t *wb, size_t ntb, size_t tb, uint32_t h,
                                                  uint32_t lane, AChunk (&A)[2])
 {
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
         const uint32_t q = 2 * h + ch;
-        A[ch].ql = *reinterpret_cast<const uint4 *>(wb + tb * TILE_QL + q * 1024 + lane * 16);
-        A[ch].qh = *reinterpret_cast<const uint2 *>(wb + ntb * TILE_QL + tb * TILE_QH + q * 512 + lane * 8);
+        const uint8_t *pl = wb + tb * TILE_QL + q * 1024 + lane * 16;
+        const uint8_t *ph = wb + ntb * TILE_QL + tb * TILE_QH + q * 512 + lane * 8;
+        if (STREAM) {
+            const u32x4_t l = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(pl));
+            const u32x2_t hh = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(ph));
+            A[ch].ql = make_uint4(l.x, l.y, l.z, l.w);
+            A[ch].qh = make_uint2(hh.x, hh.y);
+        } else {
+            A[ch].ql = *reinterpret_cast<const uint4 *>(pl);
+            A[ch].qh = *reinterpret_cast<const uint2 *>(ph);
+        }
     }
     const uint2 sc = *reinterpret_cast<const uint2 *>(wb + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + h * 256 +
                                                       (lane & 31) * 8);
@@ -663,8 +713,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         return;
     const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
     const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
-    const _Float16 *xh = reinterpret_cast<const _Float16 *>(a.x_hi);
-    const _Float16 *xl = reinterpret_cast<const _Float16 *>(a.x_lo);
+    const __amdgpu_buffer_rsrc_t xh = act_rsrc(a.x_hi), xl = act_rsrc(a.x_lo);
     // the wave index as a wave-uniform value, so that the row-tile and weight
     // addresses derived from it stay in scalar registers
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -683,27 +732,25 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // 4 KB of lo, contiguous.  The four waves load a stage into one LDS buffer
     // (wave w: k-pieces 2w, 2w + 1, i.e. kilobyte w of each half; lanes past the
     // tile's last column re-read that column, so an expert tile of ~8 tokens reads
-    // ~8 rows' bytes), double-buffered with one barrier per stage, and read their
-    // MFMA B fragments from there.
+    // ~8 rows' bytes) and read their MFMA B fragments from there.  Byte offsets stay
+    // below 2^31 (the host bounds the activation copies).
     const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
-    const size_t bsrc = (size_t)lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8;
-    __shared__ __attribute__((aligned(16))) _Float16 Bsh[2][2][8 * 256];
+    const uint32_t bsrc = 2 * (lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8);
+    // four stage buffers, hi then lo (stage s in buffer s & 3), each its own array
+    __shared__ __attribute__((aligned(16))) _Float16 B0[2 * 8 * 256], B1[2 * 8 * 256], B2[2 * 8 * 256],
+        B3[2 * 8 * 256];
+    typedef AChunk BlockW[2][NI][2]; // a block's weights: [half][row tile][chunk]
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            load_tile_chunks(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
+            load_tile_chunks<true>(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
-    // stage st's tile into LDS buffer st & 1 (this wave's two 16-byte pieces per lane)
-    auto loadB = [&](uint32_t st) {
-        const uint32_t buf = st & 1;
-        const size_t o = bsrc + ((size_t)kb0 * 4 + st) * (TK / 8) * 256;
-        __builtin_amdgcn_global_load_lds((const void *)(xh + o),
-                                         (__attribute__((address_space(3))) void *)&Bsh[buf][0][wave * 512],
-                                         16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void *)(xl + o),
-                                         (__attribute__((address_space(3))) void *)&Bsh[buf][1][wave * 512],
-                                         16, 0, 0);
+    // stage st's tile into buffer dst (this wave's two 16-byte pieces per lane)
+    auto loadB = [&](uint32_t st, _Float16 *__restrict__ dst) {
+        const uint32_t o = bsrc + (kb0 * 4 + st) * TK * 32 * 2;
+        lds_dma16(xh, o, &dst[wave * 512]);
+        lds_dma16(xl, o, &dst[8 * 256 + wave * 512]);
     };
     // this lane's A rows' block scales d, block kb of the slice, as binary16 bits
     // (converted where used, so the load does not wait for the weights issued before it)
@@ -726,7 +773,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             acc[i][e] *= __shfl(v, 8 * (e / 4) + 4 * p + (e % 4), 64);
     };
     float u[NI], dcur[NI];
-    uint32_t dbits[NI], dnext[NI];
+    uint32_t dnext[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
         u[i] = 1.0f, dnext[i] = 0;
@@ -740,96 +787,125 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                 by_row(i, r);
         }
     };
-    const uint32_t nst = nbl * 4, nhb = nbl * 2;
-    AChunk A[NI][2], An[NI][2];
-    loadA(0, A);
-    loadD(0, dbits);
-    loadB(0);
-    __builtin_amdgcn_s_waitcnt(0); // stage 0's tile (and the first weights) have landed
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-        dcur[i] = half_bits_to_float(dbits[i]);
-    enter_block(true);
-    for (uint32_t hb = 0; hb < nhb; ++hb) {
-        if ((hb & 1) == 0 && hb > 0) {
+    const uint32_t nst = nbl * 4;
+    bool zero[NI];
+    // Stage s = 4 kb + j.  Issue order per block, so that the loads waited for at
+    // each stage's end leave everything issued after them in flight (loads retire
+    // in issue order): stage j first loads stage s + 3's tile (into the buffer the
+    // last barrier freed), then at j = 0 the next block's first half of the weights
+    // and its scales, at j = 2 its second half.  The weights thus have a block of
+    // stages to arrive and the tiles three stages.  The buffers arrive as restrict-
+    // qualified pointers, so the compiler sees that the stage's LDS reads do not
+    // touch the tile in flight.
+    auto stage = [&](uint32_t kb, int j, const _Float16 *__restrict__ rb, _Float16 *__restrict__ nbuf,
+                     BlockW &W, BlockW &N) {
+        const uint32_t st = kb * 4 + j;
+        const bool more = kb + 1 < nbl; // a next block exists
+        if (j == 0) {
 #pragma unroll
             for (int i = 0; i < NI; ++i)
                 dcur[i] = half_bits_to_float(dnext[i]);
-            enter_block(false);
+            enter_block(kb == 0);
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+                zero[i] = dcur[i] == 0.f;
         }
-        bool zero[NI];
+        issue_fence();
+        if (st + 3 < nst)
+            loadB(st + 3, nbuf);
+        issue_fence();
+        if ((j == 0 || j == 2) && more) {
+            loadA(2 * (kb + 1) + (j >> 1), N[j >> 1]);
+            if (j == 0)
+                loadD(kb + 1, dnext);
+        }
+        issue_fence();
+        const int q = j & 1;
+        AChunk (&A)[NI][2] = W[j >> 1];
+        half8 afc[NI], bch[4], bcl[4];
+        // k-step kq reads k-piece 2 kq + p of row lr
+        lds_frags_issue(lds_addr(rb) + (p * 256 + lr * 8) * 2, bch, bcl);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            zero[i] = dcur[i] == 0.f;
+            afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+        lds_frags_wait(bch, bcl);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t st = hb * 2 + q;
-            // Loads retire in issue order: the next stage's activations go first, so
-            // waiting for them does not wait for the next half block's weights and
-            // scales, issued after them and used two stages later.
-            if (st + 1 < nst)
-                loadB(st + 1); // into buffer 1 - q: every wave finished it before the last barrier
-            if (q == 0) {
-                __builtin_amdgcn_sched_barrier(0);
-                if (hb + 1 < nhb)
-                    loadA(hb + 1, An);
-                if ((hb & 1) == 0 && hb + 2 < nhb)
-                    loadD((hb >> 1) + 1, dnext);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            half8 afc[NI], bch[4], bcl[4];
+        for (int kq = 0; kq < 4; ++kq) {
+            half8 afn[NI];
 #pragma unroll
-            for (int kq = 0; kq < 4; ++kq) { // k-step kq reads k-piece 2 kq + p of row lr
-                bch[kq] = *reinterpret_cast<const half8 *>(&Bsh[q][0][(2 * kq + p) * 256 + lr * 8]);
-                bcl[kq] = *reinterpret_cast<const half8 *>(&Bsh[q][1][(2 * kq + p) * 256 + lr * 8]);
+            for (int i = 0; i < NI; ++i)
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bch[kq], acc[i], 0, 0, 0);
+            if (kq < 3) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i)
+                    afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), zero[i]);
             }
 #pragma unroll
             for (int i = 0; i < NI; ++i)
-                afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
-#pragma unroll
-            for (int kq = 0; kq < 4; ++kq) {
-                half8 afn[NI];
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bcl[kq], acc[i], 0, 0, 0);
+            if (kq < 3) {
 #pragma unroll
                 for (int i = 0; i < NI; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bch[kq], acc[i], 0, 0, 0);
-                if (kq < 3) {
-#pragma unroll
-                    for (int i = 0; i < NI; ++i)
-                        afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), zero[i]);
-                }
-#pragma unroll
-                for (int i = 0; i < NI; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afc[i], bcl[kq], acc[i], 0, 0, 0);
-                if (kq < 3) {
-#pragma unroll
-                    for (int i = 0; i < NI; ++i)
-                        afc[i] = afn[i];
-                }
+                    afc[i] = afn[i];
             }
-            if (st + 1 < nst) {
-                // The next stage's tile has landed and every wave is done with buffer
-                // q.  Loads retire in issue order and the tile was issued before the
-                // next half block's weights (5 loads per tile) and block scales:
-                // waiting until at most 5 NI loads are outstanding leaves those weights
-                // in flight.
-                asm volatile("" ::: "memory");
-                if (q == 0 && hb + 1 < nhb)
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(5 * NI));
+        }
+        if (st + 1 < nst) {
+            // Stage st + 1's tile has landed (and with it the weights and scales it
+            // needs, all issued before it) and every wave is done with buffer j.  The
+            // loads issued after that tile stay in flight: the next two tiles (2
+            // loads each) and the weights issued at the last j = 0 or 2 stages (5 NI
+            // per half block, NI scales with the first half).  Near the slice's end,
+            // where fewer were issued, the counts below shrink to what was issued.
+            asm volatile("" ::: "memory");
+            if (j == 0 || j == 2) {
+                if (more)
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 11 * NI));
+                else if (j == 0)
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI));
                 else
                     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
+            } else if (j == 1) {
+                if (more)
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 6 * NI));
+                else
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(2));
+            } else {
+                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI)); // j = 3 ends a block that has a next
             }
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
         }
-        if (hb + 1 < nhb) {
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-#pragma unroll
-                for (int ch = 0; ch < 2; ++ch)
-                    A[i][ch] = An[i][ch];
-        }
+    };
+    auto block = [&](uint32_t kb, BlockW &W, BlockW &N) {
+        stage(kb, 0, B0, B3, W, N);
+        stage(kb, 1, B1, B0, W, N);
+        stage(kb, 2, B2, B1, W, N);
+        stage(kb, 3, B3, B2, W, N);
+    };
+    // Prologue: what stages -4 .. -1 of a block before the first would have issued.
+    BlockW S0, S1;
+    loadA(0, S0[0]);
+    loadD(0, dnext);
+    issue_fence();
+    loadB(0, B0);
+    loadB(1, B1);
+    issue_fence();
+    loadA(1, S0[1]);
+    issue_fence();
+    loadB(2, B2);
+    issue_fence();
+    // the first tile, the first half block's weights and the first scales have landed
+    // (a bare barrier: a fence would wait for every load)
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    uint32_t kb = 0;
+    for (; kb + 1 < nbl; kb += 2) {
+        block(kb, S0, S1);
+        block(kb + 1, S1, S0);
     }
+    if (kb < nbl)
+        block(kb, S0, S1);
 #pragma unroll
     for (int i = 0; i < NI; ++i)
         by_row(i, u[i]);
