@@ -106,7 +106,7 @@ struct Shape {
 
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
-    hipFunction_t split_rows, gemm_q6, conv_prefill, conv_state, rope_kv_prefill, attn_prefill,
+    hipFunction_t split_rows, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
         tile_pack;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
@@ -231,7 +231,7 @@ static int get_kernels(Kernels **out)
         hipFunction_t *f;
         const char *name;
     } pfns[] = {{&k->split_rows, "k_split_rows"},       {&k->gemm_q6, "k_gemm_q6"},
-                {&k->conv_prefill, "k_conv_prefill"},   {&k->conv_state, "k_conv_state"},
+                {&k->conv_prefill, "k_conv_prefill"},
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
                 {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_prefill, "k_router_prefill"},
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
@@ -597,9 +597,13 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 // at least one Q6_K block, the partials within `part_cap` floats of `part`) and
 // k_gemm_reduce adds the slices in order.  part_rows: output rows the GEMM can
 // write (T, or 4T for expert slots); n_used: ranks per token of the expert slots.
+// `deferred` (ungrouped, non-pair calls): with a K split the reduce is left to the
+// caller, which gets the slice count there (1: the kernel wrote c itself; S > 1: the
+// S slices of part, each part_rows x zrows).
 static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
                        uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches,
-                       const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr)
+                       const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr,
+                       uint32_t *deferred = nullptr)
 {
     if (combined)
         *combined = false;
@@ -616,6 +620,8 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     }
     hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
                             : (pair ? K->gemm_swiglu : K->gemm_q6);
+    if (deferred)
+        *deferred = S;
     if (S == 1) {
         RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
         *dispatches += 1;
@@ -627,6 +633,10 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     g.part_rows = part_rows;
     grid.z = nz * S;
     RC(launch_t(f, grid, GEMM_THREADS, 0, s, g));
+    if (deferred) {
+        *dispatches += 1;
+        return LFM_OK;
+    }
     if (combine) { // grouped down projection: slices and the rank combine in one pass
         ReduceCombineArgs rc{part, combine->wsel, combine->x, S, combine->T, combine->dim, combine->n_used};
         RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
@@ -795,6 +805,7 @@ struct lfm_engine {
     // batched prefill buffers (capacity: ctx tokens per call)
     struct {
         float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr, *part = nullptr;
+        float *cstate = nullptr; // the short conv's new state, until the next split copies it
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
         uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr, *pos = nullptr;
@@ -1441,6 +1452,7 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));
+        HIPCHK(hipMalloc(&e->pf.cstate, (size_t)dim * 2 * 4));
         HIPCHK(hipMalloc(&e->pf.logits, TC * E * 4));
         HIPCHK(hipMalloc(&e->pf.wsel, TC * 4 * 4));
         HIPCHK(hipMalloc(&e->pf.sel, TC * 4 * 4));
@@ -1481,7 +1493,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
-                    e->pf.slot, e->pf.pos};
+                    e->pf.slot, e->pf.pos, e->pf.cstate};
     for (void *p : bufs)
         if (p)
             (void)hipFree(p);
@@ -1542,18 +1554,22 @@ static SplitArgs split_args(lfm_engine *e, const float *x, const float *norm, ui
 }
 
 static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
-                    uint32_t T, bool grouped = false, uint32_t spr = 1)
+                    uint32_t T, bool grouped = false, uint32_t spr = 1, const float *copy_src = nullptr,
+                    float *copy_dst = nullptr, uint32_t copy_n = 0)
 {
     if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
         return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
-    const SplitArgs a = split_args(e, x, norm, rows, K, T, grouped, spr);
+    SplitArgs a = split_args(e, x, norm, rows, K, T, grouped, spr);
+    a.copy_src = copy_src;
+    a.copy_dst = copy_dst;
+    a.copy_n = copy_n;
     RC(launch(e->K->split_rows, dim3(rows), 0, e->stream, a));
     e->dispatches += 1;
     return LFM_OK;
 }
 
 static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
-                   uint32_t mode)
+                   uint32_t mode, uint32_t *deferred = nullptr)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -1567,7 +1583,8 @@ static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32
     g.ldc = ldc;
     g.col0 = col0;
     g.mode = mode;
-    return launch_gemm(e->K, e->stream, g, false, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches);
+    return launch_gemm(e->K, e->stream, g, false, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches,
+                       nullptr, nullptr, deferred);
 }
 
 // Gate and up projections of a SwiGLU FFN in one launch: c = silu(Wg x) * (Wu x)
@@ -1629,14 +1646,16 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
     const uint32_t dim = hp.dim, kv = hp.kv_heads[l];
     RC(pf_split(e, e->pf.x, f32(e, "blk.%u.attn_norm.weight", l), T, dim, T));
     if (kv == 0) {
-        RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0));
-        ConvPrefillArgs c{e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l], e->pf.y, T,
-                          dim};
+        // in_proj; with a K split the conv adds the slices itself (no reduce launch)
+        uint32_t S = 1;
+        RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0, &S));
+        ConvPrefillArgs c{S > 1 ? e->pf.part : e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l],
+                          e->pf.cstate, e->pf.y, T, dim, S};
         RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
-        RC(launch(e->K->conv_state, dim3((dim + 255) / 256), 0, e->stream, c));
-        RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
+        // the split of y also moves the new conv state into place
+        RC(pf_split(e, e->pf.y, nullptr, T, dim, T, false, 1, e->pf.cstate, e->conv[l], 2 * dim));
         RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
-        e->dispatches += 2;
+        e->dispatches += 1;
         return LFM_OK;
     }
     const uint32_t hdkv = 64 * kv, w = dim + 2 * hdkv;

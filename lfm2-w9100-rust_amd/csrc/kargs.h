@@ -224,6 +224,12 @@ struct SplitArgs {
     // sel[s], index pos[s] in its token list, rpe rows reserved per expert)
     const uint32_t *sel, *pos;
     uint32_t spr, n_used, rpe;
+    // nullable: the workgroups also copy copy_n floats (a multiple of 4, 16-byte
+    // aligned) from copy_src to copy_dst (the short conv's new state, written by the
+    // kernel before this one)
+    const float *copy_src;
+    float *copy_dst;
+    uint32_t copy_n;
 };
 
 // Q6_K weights in 32-row tiles, the prefill GEMMs' copy (the matvecs read the
@@ -294,11 +300,13 @@ struct ReduceCombineArgs { // x[t] += sum_r w[t][r] * (sum_s part[s][t*4 + r]), 
 };
 
 struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t
-    const float *bcx;     // [T][3*dim] in_proj rows B, C, X
+    const float *bcx;     // [ksplit][T][3*dim] in_proj rows B, C, X (ksplit > 1: the
+                          // split-K partial sums, added here in slice order)
     const float *conv_w;  // [dim][3]
-    float *state;         // [dim][2] in: before the chunk, out: after it
+    const float *state;   // [dim][2] before the chunk
+    float *state_next;    // [dim][2] after it (copied over `state` by the next split)
     float *y;             // [T][dim]
-    uint32_t T, dim;
+    uint32_t T, dim, ksplit;
 };
 
 struct RopeKvArgs {       // per token: q/k head norm + RoPE, K/V to the binary16 cache

@@ -30,6 +30,44 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
     lo = (_Float16)(x - (float)hi);
 }
 
+// Sums over the S slices of split-K partials, in slice order: v = p_0, then
+// v += p_s.  The loads of a batch of slices are all issued before the first add
+// (indexes clamped into range, the extra values unused; the batch is the smallest
+// of 1, 2, 4, 8 that covers S, or 8); a load-add loop waited for each slice in
+// turn.  NV sums share the batches: value n of slice s is at p + s * step + off[n].
+template <int NV, int B>
+__device__ __forceinline__ void slice_sums_b(const float *p, size_t step, uint32_t S, const size_t (&off)[NV],
+                                             float (&v)[NV])
+{
+    for (uint32_t s0 = 0; s0 < S; s0 += B) {
+        float q[NV][B];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int n = 0; n < NV; ++n)
+                q[n][j] = p[(size_t)min(s0 + j, S - 1) * step + off[n]];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int n = 0; n < NV; ++n)
+                if (s0 + j < S)
+                    v[n] = s0 + j == 0 ? q[n][j] : v[n] + q[n][j];
+    }
+}
+template <int NV>
+__device__ __forceinline__ void slice_sums(const float *p, size_t step, uint32_t S, const size_t (&off)[NV],
+                                           float (&v)[NV])
+{
+    if (S <= 1) // uniform
+        slice_sums_b<NV, 1>(p, step, S, off, v);
+    else if (S <= 2)
+        slice_sums_b<NV, 2>(p, step, S, off, v);
+    else if (S <= 4)
+        slice_sums_b<NV, 4>(p, step, S, off, v);
+    else
+        slice_sums_b<NV, 8>(p, step, S, off, v);
+}
+
 // RMSNorm (optional) of T rows of x [T][K], then a binary16 hi/lo split of
 // x / scale with scale = 2^(e - 14) for max|x| = m * 2^e (so |x / scale| < 2^14).
 // One workgroup per token row; K is a multiple of 256 up to 8192 (the engine's
@@ -40,11 +78,12 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
 // 16 contiguous bytes).
 #define SPLIT_NP 4 // pieces per thread: K <= 256 * 8 * SPLIT_NP
 
-// Pieces v of row t (np of them valid for this thread), RMS-normed here when
-// a.norm_w is set, split into hi / lo of v / scale (scale[t] written): into row
-// t (SPLIT_ROWMAJOR) or into the nl logical rows L[j] of the token-blocked layout.
-__device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8], const uint32_t *L,
-                                             uint32_t nl)
+// Pieces v of row t (np of them valid for this thread), RMS-normed here with the
+// matching pieces nw of the norm weight when a.norm_w is set, split into hi / lo of
+// v / scale (scale[t] written): into row t (SPLIT_ROWMAJOR) or into the nl logical
+// rows L[j] of the token-blocked layout.
+__device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8],
+                                             const float (&nw)[SPLIT_NP][8], const uint32_t *L, uint32_t nl)
 {
     const uint32_t tid = threadIdx.x, npc = a.K >> 3;
     __shared__ float red[4], redm[4];
@@ -65,12 +104,9 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
         for (int i = 0; i < SPLIT_NP; ++i) {
             const uint32_t pc = tid + WG_THREADS * i;
             if (pc < npc) {
-                const float4 n0 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc);
-                const float4 n1 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc + 4);
-                const float nw[8] = {n0.x, n0.y, n0.z, n0.w, n1.x, n1.y, n1.z, n1.w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    v[i][j] = v[i][j] * inv * nw[j];
+                    v[i][j] = v[i][j] * inv * nw[i][j];
             }
         }
     }
@@ -118,25 +154,33 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
     }
 }
 
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
+template <bool NORM>
+__device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
 {
-    const uint32_t t = blockIdx.x;
-    if (t >= a.T)
-        return;
     const uint32_t tid = threadIdx.x, npc = a.K >> 3;
     const float *x = a.x + (size_t)t * a.K;
-    float v[SPLIT_NP][8];
+    // the norm weight's pieces are loaded with the row's, not after the sum of squares
+    float v[SPLIT_NP][8], nw[SPLIT_NP][8];
 #pragma unroll
     for (int i = 0; i < SPLIT_NP; ++i) {
         const uint32_t pc = tid + WG_THREADS * i;
-        float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+        float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0, n0 = x0, n1 = x0;
         if (pc < npc) {
             x0 = *reinterpret_cast<const float4 *>(x + 8 * pc);
             x1 = *reinterpret_cast<const float4 *>(x + 8 * pc + 4);
+            if (NORM) {
+                n0 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc);
+                n1 = *reinterpret_cast<const float4 *>(a.norm_w + 8 * pc + 4);
+            }
         }
         v[i][0] = x0.x, v[i][1] = x0.y, v[i][2] = x0.z, v[i][3] = x0.w;
         v[i][4] = x1.x, v[i][5] = x1.y, v[i][6] = x1.z, v[i][7] = x1.w;
+        nw[i][0] = n0.x, nw[i][1] = n0.y, nw[i][2] = n0.z, nw[i][3] = n0.w;
+        nw[i][4] = n1.x, nw[i][5] = n1.y, nw[i][6] = n1.z, nw[i][7] = n1.w;
     }
+    if (a.copy_src) // uniform: one float4 per thread of the first copy_n / 1024 rows' workgroups
+        for (uint32_t u = t * WG_THREADS + tid; u < a.copy_n / 4; u += a.T * WG_THREADS)
+            reinterpret_cast<float4 *>(a.copy_dst)[u] = reinterpret_cast<const float4 *>(a.copy_src)[u];
     uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
     if (a.mode == SPLIT_GROUPED) { // uniform
         nl = 0;
@@ -146,7 +190,18 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
                 L[nl++] = a.sel[s] * a.rpe + a.pos[s];
         }
     }
-    split_pieces(a, t, v, L, nl);
+    split_pieces(a, t, v, nw, L, nl);
+}
+
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
+{
+    const uint32_t t = blockIdx.x;
+    if (t >= a.T)
+        return;
+    if (a.norm_w) // uniform
+        split_rows_body<true>(a, t);
+    else
+        split_rows_body<false>(a, t);
 }
 
 // s_waitcnt immediate (gfx9 encoding): vector-memory count <= n, LDS/scalar count 0,
@@ -976,25 +1031,27 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_reduce(const Gem
         return;
     const size_t slice = (size_t)a.part_rows * a.zrows, at = (size_t)orow * a.zrows + r;
     float *out = a.c + (size_t)orow * a.ldc + a.col0 + r;
-    if (a.pair) {
-        float g = a.part[at], u = a.part[slice + at];
-        for (uint32_t s = 1; s < a.ksplit; ++s) {
-            g += a.part[2 * s * slice + at];
-            u += a.part[(2 * s + 1) * slice + at];
-        }
+    if (a.pair) { // slice s holds the gate sums at 2s, the up sums at 2s + 1
+        float gu[2] = {0.f, 0.f};
+        slice_sums<2>(a.part + at, 2 * slice, a.ksplit, {0, slice}, gu);
+        const float g = gu[0], u = gu[1];
         *out = g / (1.0f + expf(-g)) * u;
         return;
     }
-    float v = a.part[at];
-    for (uint32_t s = 1; s < a.ksplit; ++s)
-        v += a.part[s * slice + at];
-    *out = a.mode ? *out + v : v;
+    const float old = *out; // issued with the slices (unused unless accumulating)
+    float v[1] = {0.f};
+    slice_sums<1>(a.part + at, slice, a.ksplit, {0}, v);
+    *out = a.mode ? old + v[0] : v[0];
 }
 // ------------------------------------------------------------------ short conv
 // The LFM2 short conv keeps only the previous two values of bx = B*X, so each
 // (t, ch) output depends on inputs t-2, t-1, t only: the T tokens of a chunk are
 // computed in parallel with the reference's per-element operation order
 // (lfm.rs:464-533: co = ((0 + s0*w0) + s1*w1) + bx*w2, y = C*co, no contraction).
+// With a split-K in_proj the kernel adds its partial sums itself (each B and X
+// value is read by the three tokens that use it), in slice order as
+// k_gemm_reduce would.  The new state (bx[T-2], bx[T-1]), or (s1, bx[0]) for T = 1,
+// goes to state_next: workgroups of the first tokens may still read the old one.
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_prefill(const ConvPrefillArgs a)
 {
 #pragma clang fp contract(off)
@@ -1002,34 +1059,34 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_prefill(const Co
     const uint32_t t = blockIdx.y;
     if (ch >= a.dim || t >= a.T)
         return;
-    const uint32_t D3 = 3 * a.dim;
-    auto bx_at = [&](int tt) -> float {
-        if (tt >= 0)
-            return a.bcx[(size_t)tt * D3 + ch] * a.bcx[(size_t)tt * D3 + 2 * a.dim + ch];
-        return a.state[ch * 2 + (tt == -2 ? 0 : 1)];
-    };
-    const float s0 = bx_at((int)t - 2), s1 = bx_at((int)t - 1), bx = bx_at((int)t);
+    const size_t D3 = 3 * (size_t)a.dim, slice = (size_t)a.T * D3;
+    // B and X of tokens t-2, t-1, t (clamped to token 0: values for t < 2 come from
+    // the state), C of token t, all slices' loads issued together
+    const uint32_t t2 = t >= 2 ? t - 2 : 0, t1 = t >= 1 ? t - 1 : 0;
+    float v[7];
+    const size_t base = ch;
+    slice_sums<7>(a.bcx + base, slice, a.ksplit,
+                  {t2 * D3, t2 * D3 + 2 * a.dim, t1 * D3, t1 * D3 + 2 * a.dim, t * D3, t * D3 + 2 * a.dim,
+                   t * D3 + a.dim},
+                  v);
+    float st0 = 0.f, st1 = 0.f;
+    if (t < 2) { // uniform
+        st0 = a.state[ch * 2];
+        st1 = a.state[ch * 2 + 1];
+    }
+    const float bx = v[4] * v[5];
+    const float s0 = t >= 2 ? v[0] * v[1] : t == 1 ? st1 : st0;
+    const float s1 = t >= 1 ? v[2] * v[3] : st1;
     const float *w3 = a.conv_w + ch * 3;
     float co = 0.0f;
     co = co + s0 * w3[0];
     co = co + s1 * w3[1];
     co = co + bx * w3[2];
-    a.y[(size_t)t * a.dim + ch] = a.bcx[(size_t)t * D3 + a.dim + ch] * co;
-}
-
-// New conv state after the chunk: (bx[T-2], bx[T-1]) (or (s1, bx[0]) for T = 1).
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_state(const ConvPrefillArgs a)
-{
-#pragma clang fp contract(off)
-    const uint32_t ch = blockIdx.x * WG_THREADS + threadIdx.x;
-    if (ch >= a.dim)
-        return;
-    const uint32_t D3 = 3 * a.dim;
-    const float last = a.bcx[(size_t)(a.T - 1) * D3 + ch] * a.bcx[(size_t)(a.T - 1) * D3 + 2 * a.dim + ch];
-    const float prev = a.T >= 2 ? a.bcx[(size_t)(a.T - 2) * D3 + ch] * a.bcx[(size_t)(a.T - 2) * D3 + 2 * a.dim + ch]
-                                : a.state[ch * 2 + 1];
-    a.state[ch * 2] = prev;
-    a.state[ch * 2 + 1] = last;
+    a.y[(size_t)t * a.dim + ch] = v[6] * co;
+    if (t + 1 == a.T) {
+        a.state_next[ch * 2] = s1;
+        a.state_next[ch * 2 + 1] = bx;
+    }
 }
 
 // ------------------------------------------------------------------ attention
@@ -1513,16 +1570,21 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_reduce_combine(const 
     if (k >= a.dim || t >= a.T)
         return;
     const size_t slice = (size_t)a.T * 4 * a.dim;
-    float sm = 0.0f;
-    for (uint32_t r = 0; r < a.n_used; ++r) {
-        const size_t at = ((size_t)t * 4 + r) * a.dim + k;
-        float d = a.part[at];
-        for (uint32_t s = 1; s < a.ksplit; ++s)
-            d += a.part[s * slice + at];
-        sm = sm + d * a.wsel[(size_t)t * 4 + r];
-    }
     float *x = a.x + (size_t)t * a.dim + k;
-    *x = *x + sm;
+    const float x0 = *x;
+    float w[4], d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        w[r] = a.wsel[(size_t)t * 4 + r];
+    // the four ranks' slices together (ranks >= n_used are read and not used)
+    const size_t D = a.dim;
+    slice_sums<4>(a.part + (size_t)t * 4 * a.dim + k, slice, a.ksplit, {0, D, 2 * D, 3 * D}, d);
+    float sm = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (r < (int)a.n_used)
+            sm = sm + d[r] * w[r];
+    *x = x0 + sm;
 }
 
 // Token embeddings of T ids (lfm.rs:310-320): row ids[t] of the Q6_K table,
