@@ -1659,10 +1659,12 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         return LFM_OK;
     }
     const uint32_t hdkv = 64 * kv, w = dim + 2 * hdkv;
-    RC(pf_gemm(e, e->qkvt[l], T, e->pf.bcx, w, 0, 0)); // rows q | k | v = columns of bcx
-    RopeKvArgs r{e->pf.bcx, f32(e, "blk.%u.attn_q_norm.weight", l),
+    // rows q | k | v = columns of bcx; with a K split the rope kernel adds the slices
+    uint32_t S = 1;
+    RC(pf_gemm(e, e->qkvt[l], T, e->pf.bcx, w, 0, 0, &S));
+    RopeKvArgs r{e->pf.bcx, S > 1 ? e->pf.part : e->pf.bcx, f32(e, "blk.%u.attn_q_norm.weight", l),
                  f32(e, "blk.%u.attn_k_norm.weight", l), e->rope, hp.eps, e->kc[l], e->vc[l], T,
-                 start, hp.heads, kv, e->ctx};
+                 start, hp.heads, kv, e->ctx, S};
     RC(launch(e->K->rope_kv_prefill, dim3(T), 0, e->stream, r));
     AttnPrefillArgs at{e->pf.bcx, e->kc[l], e->vc[l], e->pf.y, 1.0f / sqrtf((float)hp.head_dim), T,
                        start, hp.heads, kv, e->ctx, nullptr, 0};

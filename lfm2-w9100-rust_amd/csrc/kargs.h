@@ -310,11 +310,13 @@ struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t
 };
 
 struct RopeKvArgs {       // per token: q/k head norm + RoPE, K/V to the binary16 cache
-    float *qkv;           // [T][dim + 2*hdkv], q rotated in place
+    float *qkv;           // [T][dim + 2*hdkv], the rotated q written here
+    const float *src;     // [ksplit][T][dim + 2*hdkv] the projection (ksplit > 1: its
+                          // split-K partial sums, added here in slice order; may be qkv)
     const float *q_norm, *k_norm, *rope;
     float eps;
     uint16_t *kcache, *vcache;  // [kv][ctx][64]
-    uint32_t T, start, heads, kv, ctx;
+    uint32_t T, start, heads, kv, ctx, ksplit;
 };
 
 struct AttnPrefillArgs {  // causal GQA attention of T queries at positions start + t

@@ -33,8 +33,9 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo)
 // Sums over the S slices of split-K partials, in slice order: v = p_0, then
 // v += p_s.  The loads of a batch of slices are all issued before the first add
 // (indexes clamped into range, the extra values unused; the batch is the smallest
-// of 1, 2, 4, 8 that covers S, or 8); a load-add loop waited for each slice in
-// turn.  NV sums share the batches: value n of slice s is at p + s * step + off[n].
+// of 1, 2, 4, 8 that covers S, or 8, or at most BMAX); a load-add loop waited for
+// each slice in turn.  NV sums share the batches: value n of slice s is at p + s *
+// step + off[n].
 template <int NV, int B>
 __device__ __forceinline__ void slice_sums_b(const float *p, size_t step, uint32_t S, const size_t (&off)[NV],
                                              float (&v)[NV])
@@ -54,15 +55,15 @@ __device__ __forceinline__ void slice_sums_b(const float *p, size_t step, uint32
                     v[n] = s0 + j == 0 ? q[n][j] : v[n] + q[n][j];
     }
 }
-template <int NV>
+template <int NV, int BMAX = 8>
 __device__ __forceinline__ void slice_sums(const float *p, size_t step, uint32_t S, const size_t (&off)[NV],
                                            float (&v)[NV])
 {
     if (S <= 1) // uniform
         slice_sums_b<NV, 1>(p, step, S, off, v);
-    else if (S <= 2)
+    else if (S <= 2 || BMAX < 4)
         slice_sums_b<NV, 2>(p, step, S, off, v);
-    else if (S <= 4)
+    else if (S <= 4 || BMAX < 8)
         slice_sums_b<NV, 4>(p, step, S, off, v);
     else
         slice_sums_b<NV, 8>(p, step, S, off, v);
@@ -1094,31 +1095,55 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_prefill(const Co
 // Per token: q heads and k heads RMS-normed over head_dim and NEOX-rotated at
 // position start + t (table row), q written back, K and V rounded to binary16 and
 // stored in the cache (lfm.rs:360-393).  One wave per head.
+// Wave w takes q heads w + 4i (heads <= 32) and kv heads w + 4j (kv <= 8).  Every
+// value it needs (all split-K slices of its q, k and v heads, the norm weights and
+// the position's rotation) is loaded before the first is used: a per-head loop of
+// load, reduce and store waited for each head in turn (the stores may alias the
+// next head's loads).
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_rope_kv_prefill(const RopeKvArgs a)
 {
     const uint32_t t = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (t >= a.T)
         return;
-    const uint32_t dim = a.heads * 64, hdkv = a.kv * 64, pos = a.start + t;
-    float *row = a.qkv + (size_t)t * (dim + 2 * hdkv);
+    const uint32_t dim = a.heads * 64, hdkv = a.kv * 64, W = dim + 2 * hdkv, pos = a.start + t;
+    const size_t rowo = (size_t)t * W;
+    float *row = a.qkv + rowo;
     const float *cs = a.rope + (size_t)pos * 64;
-    for (uint32_t h = wave; h < a.heads + a.kv; h += 4) {
-        const bool isq = h < a.heads;
-        float v = row[(isq ? 0 : dim) + (isq ? h : h - a.heads) * 64 + lane];
-        const float ss = wave_sum(v * v);
+    const uint32_t p = lane & 31;
+    const float c = cs[2 * p], s = cs[2 * p + 1], qw = a.q_norm[lane], kw = a.k_norm[lane];
+    size_t off[12];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        off[i] = min(wave + 4 * i, a.heads - 1) * 64 + lane;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t kh = min(wave + 4 * j, a.kv - 1);
+        off[8 + j] = dim + kh * 64 + lane;
+        off[10 + j] = dim + hdkv + kh * 64 + lane;
+    }
+    float v[12];
+    slice_sums<12, 4>(a.src + rowo, (size_t)a.T * W, a.ksplit, off, v);
+    auto norm_rope = [&](float x, float w) {
+        const float ss = wave_sum(x * x);
         const float inv = 1.0f / sqrtf(ss / 64.0f + a.eps);
-        v *= inv * (isq ? a.q_norm : a.k_norm)[lane];
-        const float other = __shfl_xor(v, 32, 64);
-        const uint32_t p = lane & 31;
-        const float c = cs[2 * p], s = cs[2 * p + 1];
-        const float r = lane < 32 ? v * c - other * s : other * s + v * c;
-        if (isq) {
-            row[h * 64 + lane] = r;
-        } else {
-            const uint32_t kh = h - a.heads;
-            const size_t off = ((size_t)kh * a.ctx + pos) * 64 + lane;
-            a.kcache[off] = __builtin_bit_cast(uint16_t, (_Float16)r);
-            a.vcache[off] = __builtin_bit_cast(uint16_t, (_Float16)row[dim + hdkv + kh * 64 + lane]);
+        x *= inv * w;
+        const float other = __shfl_xor(x, 32, 64);
+        return lane < 32 ? x * c - other * s : other * s + x * c;
+    };
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t h = wave + 4 * i;
+        if (h < a.heads) // uniform
+            row[h * 64 + lane] = norm_rope(v[i], qw);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t kh = wave + 4 * j;
+        if (kh < a.kv) { // uniform
+            const float r = norm_rope(v[8 + j], kw);
+            const size_t o = ((size_t)kh * a.ctx + pos) * 64 + lane;
+            a.kcache[o] = __builtin_bit_cast(uint16_t, (_Float16)r);
+            a.vcache[o] = __builtin_bit_cast(uint16_t, (_Float16)v[10 + j]);
         }
     }
 }
@@ -1303,15 +1328,38 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge_split(cons
         return;
     const size_t stride = (size_t)a.T * a.heads * 66;
     const float *pb = a.part + ((size_t)t * a.heads + h) * 66;
+    const uint32_t n = a.nsplit;
+    // the ranges in batches of 8, a batch's loads issued before its first use
+    // (indexes clamped, the extra values unused): a load-use loop waited for each
+    // range in turn
     float M = -INFINITY;
-    for (uint32_t s = 0; s < a.nsplit; ++s)
-        M = fmaxf(M, pb[s * stride]);
+    for (uint32_t s0 = 0; s0 < n; s0 += 8) {
+        float m[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            m[j] = pb[(size_t)min(s0 + j, n - 1) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < n)
+                M = fmaxf(M, m[j]);
+    }
     float num = 0.f, den = 0.f;
-    for (uint32_t s = 0; s < a.nsplit; ++s) {
-        const float ms = pb[s * stride];
-        const float f = ms > -INFINITY ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-        den += f * pb[s * stride + 1];
-        num += f * pb[s * stride + 2 + d];
+    for (uint32_t s0 = 0; s0 < n; s0 += 8) {
+        float m[8], l[8], o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float *q = pb + (size_t)min(s0 + j, n - 1) * stride;
+            m[j] = q[0];
+            l[j] = q[1];
+            o[j] = q[2 + d];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < n) {
+                const float f = m[j] > -INFINITY ? __builtin_amdgcn_exp2f(m[j] - M) : 0.f;
+                den += f * l[j];
+                num += f * o[j];
+            }
     }
     a.out[(size_t)t * a.heads * 64 + h * 64 + d] = num / den;
 }
