@@ -207,7 +207,10 @@ int lfm_copy_time(uint64_t bytes, uint32_t reps, float *us_per_copy);
 
 /* Prefill GEMM on the matrix cores: y[t][r] = sum_k W[r][k] * x[t][k] for T
  * activation rows x (f32 [T][in_dim], device) into y (f32 [T][rows], device);
- * the multi-token q6k_prompt path of engine/src/ops.rs:350-373. */
+ * the multi-token q6k_prompt path of engine/src/ops.rs:350-373.  in_dim is a
+ * multiple of 256 up to 8192 and (T + 31) * in_dim * 2 bytes stays below 2 GiB
+ * (the kernels address the binary16 activation copies with 32-bit offsets);
+ * LFM_EINVAL otherwise. */
 int lfm_q6k_gemm(const void *packed_dev, uint64_t rows, uint64_t in_dim, const float *x_dev,
                  uint32_t T, float *y_dev, void *stream);
 
