@@ -600,11 +600,21 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 // `deferred` (ungrouped, non-pair calls): with a K split the reduce is left to the
 // caller, which gets the slice count there (1: the kernel wrote c itself; S > 1: the
 // S slices of part, each part_rows x zrows).
+// Router partials for the next FFN (ungrouped, non-pair, accumulating calls): with
+// a K split the reduce also leaves them (GemmReduceArgs) and *router_done is set.
+struct RouterPart {
+    const float *norm, *w; // the FFN's RMSNorm weight and router rows [n_expert][zrows]
+    float *rpart, *rss;
+    uint32_t n_expert;
+};
+
 static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
                        uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches,
                        const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr,
-                       uint32_t *deferred = nullptr)
+                       uint32_t *deferred = nullptr, const RouterPart *router = nullptr, bool *router_done = nullptr)
 {
+    if (router_done)
+        *router_done = false;
     if (combined)
         *combined = false;
     const bool small = T <= GEMM_TOKENS;
@@ -642,7 +652,17 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
         *combined = true;
     } else {
-        GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used};
+        GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used,
+                         nullptr, nullptr, nullptr, nullptr, 0};
+        if (router && !pair && nz == 1 && g.zrows % 256 == 0 && router->n_expert <= 64) {
+            r.rnorm = router->norm;
+            r.rw = router->w;
+            r.rpart = router->rpart;
+            r.rss = router->rss;
+            r.n_expert = router->n_expert;
+            if (router_done)
+                *router_done = true;
+        }
         RC(launch(K->gemm_reduce, dim3((g.zrows + 255) / 256, part_rows), 0, s, r));
     }
     *dispatches += 2;
@@ -809,6 +829,10 @@ struct lfm_engine {
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
         uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr, *pos = nullptr;
+        // router partial sums left by the out projection's reduce (small calls), and
+        // whether the current layer's were written
+        float *rpart = nullptr, *rss = nullptr;
+        bool router_ready = false;
     } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
@@ -1453,6 +1477,9 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));
         HIPCHK(hipMalloc(&e->pf.cstate, (size_t)dim * 2 * 4));
+        const size_t tsmall = std::min<size_t>(TC, GEMM_TOKENS);
+        HIPCHK(hipMalloc(&e->pf.rpart, tsmall * (dim / 256) * E * 4));
+        HIPCHK(hipMalloc(&e->pf.rss, tsmall * (dim / 256) * 4));
         HIPCHK(hipMalloc(&e->pf.logits, TC * E * 4));
         HIPCHK(hipMalloc(&e->pf.wsel, TC * 4 * 4));
         HIPCHK(hipMalloc(&e->pf.sel, TC * 4 * 4));
@@ -1493,7 +1520,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
-                    e->pf.slot, e->pf.pos, e->pf.cstate};
+                    e->pf.slot, e->pf.pos, e->pf.cstate, e->pf.rpart, e->pf.rss};
     for (void *p : bufs)
         if (p)
             (void)hipFree(p);
@@ -1569,7 +1596,8 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
 }
 
 static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
-                   uint32_t mode, uint32_t *deferred = nullptr)
+                   uint32_t mode, uint32_t *deferred = nullptr, const RouterPart *router = nullptr,
+                   bool *router_done = nullptr)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -1584,7 +1612,7 @@ static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32
     g.col0 = col0;
     g.mode = mode;
     return launch_gemm(e->K, e->stream, g, false, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches,
-                       nullptr, nullptr, deferred);
+                       nullptr, nullptr, deferred, router, router_done);
 }
 
 // Gate and up projections of a SwiGLU FFN in one launch: c = silu(Wg x) * (Wu x)
@@ -1640,6 +1668,20 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6Tiles &w, uint32_t zrows, uint
                        GEMM_PART_BYTES / 4, &e->dispatches, combine, combined);
 }
 
+// The mixer's output projection, added to the residual.  Before a MoE FFN in a
+// small call its reduce also leaves the router partial sums (e->pf.router_ready).
+static int pf_out_proj(lfm_engine *e, uint32_t l, const Q6Tiles &w, uint32_t T)
+{
+    const lfm_hparams &hp = e->hp;
+    e->pf.router_ready = false;
+    if (l >= hp.dense_lead && T <= GEMM_TOKENS) {
+        const RouterPart rp{f32(e, "blk.%u.ffn_norm.weight", l), f32(e, "blk.%u.ffn_gate_inp.weight", l), e->pf.rpart,
+                            e->pf.rss, hp.n_expert};
+        return pf_gemm(e, w, T, e->pf.x, hp.dim, 0, 1, nullptr, &rp, &e->pf.router_ready);
+    }
+    return pf_gemm(e, w, T, e->pf.x, hp.dim, 0, 1);
+}
+
 static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
 {
     const lfm_hparams &hp = e->hp;
@@ -1654,7 +1696,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
         // the split of y also moves the new conv state into place
         RC(pf_split(e, e->pf.y, nullptr, T, dim, T, false, 1, e->pf.cstate, e->conv[l], 2 * dim));
-        RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.out_proj.weight", l), T, e->pf.x, dim, 0, 1));
+        RC(pf_out_proj(e, l, q6tiles(e, "blk.%u.shortconv.out_proj.weight", l), T));
         e->dispatches += 1;
         return LFM_OK;
     }
@@ -1690,7 +1732,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
     }
     RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
-    RC(pf_gemm(e, q6tiles(e, "blk.%u.attn_output.weight", l), T, e->pf.x, dim, 0, 1));
+    RC(pf_out_proj(e, l, q6tiles(e, "blk.%u.attn_output.weight", l), T));
     e->dispatches += 2;
     return LFM_OK;
 }
@@ -1714,15 +1756,25 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
     RouterPrefillArgs ra{x, norm, f32(e, "blk.%u.ffn_gate_inp.weight", l), hp.eps, e->pf.logits, T,
                          dim, E};
     RouteGroupArgs rg{e->pf.logits, f32(e, "blk.%u.exp_probs_b.bias", l), e->pf.sel, e->pf.wsel,
-                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx, e->pf.pos};
-    if (T <= GEMM_TOKENS) // few tokens: one workgroup per (expert, token)
+                      e->pf.counts, e->pf.tok, e->pf.slot, T, E, hp.n_used, e->ctx, e->pf.pos,
+                      nullptr, nullptr, 0, dim, hp.eps};
+    if (e->pf.router_ready) { // the out projection's reduce left the router partials
+        // x is token row `first` of the call's rows (the last layer runs only the last)
+        const size_t first = (size_t)(x - e->pf.x) / dim, nb = dim / 256;
+        rg.rpart = e->pf.rpart + first * nb * E;
+        rg.rss = e->pf.rss + first * nb;
+        rg.nparts = (uint32_t)nb;
+    } else if (T <= GEMM_TOKENS) { // few tokens: one workgroup per (expert, token)
         RC(launch(e->K->router_small, dim3(E, T), 0, e->stream, ra));
-    else
+        e->dispatches += 1;
+    } else {
         RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
+        e->dispatches += 1;
+    }
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
     RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
     RC(pf_split(e, x, norm, T, dim, T, true, 4));
-    e->dispatches += 3;
+    e->dispatches += 2;
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank

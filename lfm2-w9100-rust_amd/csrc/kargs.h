@@ -290,6 +290,14 @@ struct GemmReduceArgs {    // c (+)= sum_s part[s] in slice order; pair: silu(g)
     float *c;
     uint32_t ksplit, pair, part_rows, zrows, ldc, col0, mode;
     uint32_t n_used;       // grouped: out_row = token * 4 + rank, ranks >= n_used unused; 0 = all
+    // Router partials (rw nullable; ungrouped, non-pair, zrows a multiple of 256):
+    // workgroup (b, t), rows 256 b .. 256 b + 255 of token t, leaves the partial dots
+    // sum_r rw[e][r] * (c_new[r] * rnorm[r]) of the n_expert (<= 64) experts at
+    // rpart[(t * nb + b) * n_expert + e] and sum_r c_new[r]^2 at rss[t * nb + b]
+    // (nb = zrows / 256), from which k_route_topk forms the next FFN's logits.
+    const float *rnorm, *rw;
+    float *rpart, *rss;
+    uint32_t n_expert;
 };
 
 struct ReduceCombineArgs { // x[t] += sum_r w[t][r] * (sum_s part[s][t*4 + r]), rank then slice order
@@ -346,7 +354,7 @@ struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)
 };
 
 struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token, rank) list
-    const float *logits, *bias;
+    const float *logits, *bias;  // logits [T][n_expert] (k_route_topk: unless rpart is set)
     uint32_t *sel;        // [T][4] ids
     float *wsel;          // [T][4] weights
     uint32_t *counts;     // [n_expert]
@@ -354,6 +362,11 @@ struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token
     uint32_t *slot;       // [n_expert][list_stride] slot = t*4 + rank
     uint32_t T, n_expert, n_used, list_stride;
     uint32_t *pos;        // [T*4]: index of slot t*4 + rank in its expert's list
+    // k_route_topk with rpart set: logit = (sum_b rpart[t][b][e]) / sqrt((sum_b rss[t][b]) / dim + eps),
+    // b < nparts in order (the router partials of the preceding reduce)
+    const float *rpart, *rss;
+    uint32_t nparts, dim;
+    float eps;
 };
 
 struct CombinePrefillArgs {  // x[t] += sum_r w[t][r] * D[t*4 + r] (rank order)

@@ -1025,9 +1025,69 @@ extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32n1(const Gem
 // Sums the K slices of a split GEMM in slice order and applies its epilogue:
 // c = v, c += v (mode 1), or silu(g) * u for the pair form.  One thread per
 // output element (row blockIdx.x * 256 + tid of output row blockIdx.y).
+// Router partials of the rows a reduce workgroup just finished (GemmReduceArgs):
+// thread (part = tid / 64, expert e = tid % 64) dots the 64 rows of its part with
+// router row e; the four parts are added in order.  The router rows are loaded
+// before the slices are summed.
+struct RouterRows {
+    float4 w[16];
+    float nw; // rnorm of this thread's row
+};
+__device__ __forceinline__ RouterRows router_rows_load(const GemmReduceArgs &a)
+{
+    RouterRows rr;
+    const uint32_t tid = threadIdx.x, e = min(tid & 63, a.n_expert - 1), part = tid >> 6;
+    const float4 *w = reinterpret_cast<const float4 *>(a.rw + (size_t)e * a.zrows + blockIdx.x * 256 + part * 64);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        rr.w[i] = w[i];
+    rr.nw = a.rnorm[blockIdx.x * 256 + tid];
+    return rr;
+}
+__device__ __forceinline__ void router_partials(const GemmReduceArgs &a, const RouterRows &rr, float xn)
+{
+    __shared__ __attribute__((aligned(16))) float xw[256];
+    __shared__ float red[4][64], ssw[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = blockIdx.y;
+    xw[tid] = xn * rr.nw;
+    const float ss = wave_sum(xn * xn);
+    if (lane == 0)
+        ssw[wave] = ss;
+    __syncthreads();
+    const float4 *xv = reinterpret_cast<const float4 *>(xw + wave * 64);
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float4 x4 = xv[i];
+        dot = fmaf(x4.x, rr.w[i].x, dot);
+        dot = fmaf(x4.y, rr.w[i].y, dot);
+        dot = fmaf(x4.z, rr.w[i].z, dot);
+        dot = fmaf(x4.w, rr.w[i].w, dot);
+    }
+    red[wave][lane] = dot;
+    __syncthreads();
+    const size_t blk = (size_t)t * gridDim.x + blockIdx.x;
+    if (tid < a.n_expert)
+        a.rpart[blk * a.n_expert + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+    if (tid == 64)
+        a.rss[blk] = ((ssw[0] + ssw[1]) + ssw[2]) + ssw[3];
+}
+
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_reduce(const GemmReduceArgs a)
 {
     const uint32_t r = blockIdx.x * WG_THREADS + threadIdx.x, orow = blockIdx.y;
+    if (a.rw) { // uniform; every row is in range (zrows is a multiple of 256)
+        const RouterRows rr = router_rows_load(a);
+        const size_t slice = (size_t)a.part_rows * a.zrows, at = (size_t)orow * a.zrows + r;
+        float *out = a.c + (size_t)orow * a.ldc + a.col0 + r;
+        const float old = *out;
+        float v[1] = {0.f};
+        slice_sums<1>(a.part + at, slice, a.ksplit, {0}, v);
+        const float xn = a.mode ? old + v[0] : v[0];
+        *out = xn;
+        router_partials(a, rr, xn);
+        return;
+    }
     if (r >= a.zrows || (a.n_used && orow % 4 >= a.n_used))
         return;
     const size_t slice = (size_t)a.part_rows * a.zrows, at = (size_t)orow * a.zrows + r;
@@ -1525,7 +1585,38 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_topk(const Rout
     r.n_expert = a.n_expert;
     r.n_used = a.n_used;
     r.sel_out = nullptr;
-    const Routed rt = wave_route(r);
+    Routed rt;
+    if (a.rpart) { // uniform: logits from the preceding reduce's router partials
+        const uint32_t e = min(lane, a.n_expert - 1);
+        float dp[8], sp[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint32_t bb = min((uint32_t)b, a.nparts - 1);
+            dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
+            sp[b] = a.rss[(size_t)t * a.nparts + bb];
+        }
+        float dot = 0.f, ss = 0.f;
+        for (uint32_t b0 = 0; b0 < a.nparts; b0 += 8) { // uniform; nparts <= 8 in one pass
+            if (b0 > 0) {
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const uint32_t bb = min(b0 + b, a.nparts - 1);
+                    dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
+                    sp[b] = a.rss[(size_t)t * a.nparts + bb];
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < 8; ++b)
+                if (b0 + b < a.nparts) {
+                    dot = b0 + b == 0 ? dp[b] : dot + dp[b];
+                    ss = b0 + b == 0 ? sp[b] : ss + sp[b];
+                }
+        }
+        const RouteIn in{dot / sqrtf(ss / (float)a.dim + a.eps), a.bias ? a.bias[e] : 0.f};
+        rt = wave_route(r, in);
+    } else {
+        rt = wave_route(r);
+    }
     if (lane < 4) {
         a.sel[(size_t)t * 4 + lane] = rt.id(lane);
         a.wsel[(size_t)t * 4 + lane] = lane < a.n_used ? rt.w(lane) : 0.f;
