@@ -241,7 +241,9 @@ struct SplitArgs {
 // of row r's block in the Q6T planes:
 //   ql [tb][q < 4][l][16 B]  its ql chunk 2q + p
 //   qh [tb][q < 4][l][8 B]   its qh bytes 8 (2q + p) .. + 7
-//   sc [tb][h < 2][r][8 B]   its scale groups 2h, 2h + 1
+//   sc [tb][h < 2][r][8 B]   its scale groups 2h, 2h + 1, each int8 scale stored as
+//                            sc + 128 (128, a zero scale, throughout a block whose d is
+//                            zero: such a block contributes zero weights)
 //   d  [tb][r][2 B]          its d
 // 6720 B per tile-block, 210 B per row and block as in the row-major planes.
 #define TILE_QL 4096u

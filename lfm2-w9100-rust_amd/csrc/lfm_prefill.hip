@@ -377,20 +377,31 @@ extern "C" __global__ __launch_bounds__(64) void k_q6_tile_pack(const TilePackAr
         *reinterpret_cast<uint4 *>(d + tb * TILE_QL + q * 1024 + l * 16) = vl;
         *reinterpret_cast<uint2 *>(d + ntb * TILE_QL + tb * TILE_QH + q * 512 + l * 8) = vh;
     }
+    // scales as sc + 128 (sc ^ 0x80), or 128 throughout when d is +-0
+    const uint16_t vd = ok ? reinterpret_cast<const uint16_t *>(s + nblk * 208)[blk] : (uint16_t)0;
     const uint2 vs = ok ? *reinterpret_cast<const uint2 *>(s + nblk * 192 + blk * 16 + p * 8) : make_uint2(0, 0);
-    *reinterpret_cast<uint2 *>(d + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + p * 256 + r * 8) = vs;
-    if (p == 0) {
-        const uint16_t vd = ok ? reinterpret_cast<const uint16_t *>(s + nblk * 208)[blk] : (uint16_t)0;
+    const bool dz = (vd & 0x7FFFu) == 0;
+    const uint2 vb = dz ? make_uint2(0x80808080u, 0x80808080u) : make_uint2(vs.x ^ 0x80808080u, vs.y ^ 0x80808080u);
+    *reinterpret_cast<uint2 *>(d + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + p * 256 + r * 8) = vb;
+    if (p == 0)
         reinterpret_cast<uint16_t *>(d + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r] = vd;
-    }
+}
+
+// The scales of sub-blocks 2q and 2q + 1 of a chunk as binary16: its scale bytes
+// are sc + 128 (zero throughout a block whose d is zero), so the byte permute that
+// forms 1024 + (sc + 128) and a subtraction of 1152 give sc exactly.
+__device__ __forceinline__ half2v stage_scales(uint32_t sc, int q)
+{
+    const uint32_t v = __builtin_amdgcn_perm(sc, 0x64646464u, q ? 0x01070006u : 0x01050004u);
+    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
 }
 
 // The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in
-// MFMA A-operand order, or zeros when the block scale d is zero.  Exact while
+// MFMA A-operand order; ss = stage_scales of the chunk for stage s / 2.  Exact while
 // |sc * (q6 - 32)| <= 2048, within 1/2 ulp otherwise.
-__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, bool zero)
+__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, half2v ss)
 {
-    const _Float16 scf = zero ? (_Float16)0.0f : (_Float16)(float)(int)(int8_t)(c.sc >> (8 * s));
+    const _Float16 scf = ss[s & 1];
     const half2v sc2 = {scf, scf};
     half2v o[4];
 #pragma unroll
@@ -575,7 +586,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
     AChunk A[2][2], An[2][2];
     uint32_t dnext = 0;
     float dnextf = 0.f;
-    bool zero[2];
+
     // Stage st = 2 hb + q: issue stage st + 1's tile into buffer 1 - q (every wave
     // finished reading it before the last barrier; stages 0 and 1 come from the
     // prologue), then the next half block's weights and block scale at q = 0, then
@@ -600,10 +611,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
             if ((hb & 1) == 0 && hb + 2 < nhb)
                 dnext = loadD((hb >> 1) + 1);
         }
+        // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
+        half2v ss[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch)
+                ss[i][ch] = stage_scales(A[i][ch].sc, q);
         half8 afc[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+            afc[i] = decode_frag(A[i][0], 2 * q, ss[i][0]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) { // k-step ks: sub-block 2q + ks / 2, chunk ks % 2
             const uint32_t kp = ks * 2 + p;
@@ -623,7 +641,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
                 if (j == 1 && ks < 3) {
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
-                        afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), zero[i]);
+                        afn[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), ss[i][(ks + 1) & 1]);
                 }
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
@@ -666,9 +684,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         const uint32_t db = (hb >> 1) & 1;
         if ((hb & 1) == 0 && hb > 0)
             rescale(db);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            zero[i] = dsh[db][vb[i] + lr] == 0.f;
         stage(hb, 0, Bh0, Bl0, Bh1, Bl1);
         stage(hb, 1, Bh1, Bl1, Bh0, Bl0);
         if ((hb & 1) == 0 && hb + 2 < nhb) // landed at the half block's last wait
@@ -844,7 +859,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         }
     };
     const uint32_t nst = nbl * 4;
-    bool zero[NI];
+
     // Stage s = 4 kb + j.  Issue order per block, so that the loads waited for at
     // each stage's end leave everything issued after them in flight (loads retire
     // in issue order): stage j first loads stage s + 3's tile (into the buffer the
@@ -862,9 +877,6 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             for (int i = 0; i < NI; ++i)
                 dcur[i] = half_bits_to_float(dnext[i]);
             enter_block(kb == 0);
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-                zero[i] = dcur[i] == 0.f;
         }
         issue_fence();
         if (st + 3 < nst)
@@ -881,9 +893,16 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         half8 afc[NI], bch[4], bcl[4];
         // k-step kq reads k-piece 2 kq + p of row lr
         lds_frags_issue(lds_addr(rb) + (p * 256 + lr * 8) * 2, bch, bcl);
+        // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
+        half2v ss[NI][2];
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            afc[i] = decode_frag(A[i][0], 2 * q, zero[i]);
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch)
+                ss[i][ch] = stage_scales(A[i][ch].sc, q);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            afc[i] = decode_frag(A[i][0], 2 * q, ss[i][0]);
         lds_frags_wait(bch, bcl);
 #pragma unroll
         for (int kq = 0; kq < 4; ++kq) {
@@ -894,7 +913,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             if (kq < 3) {
 #pragma unroll
                 for (int i = 0; i < NI; ++i)
-                    afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), zero[i]);
+                    afn[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), ss[i][(kq + 1) & 1]);
             }
 #pragma unroll
             for (int i = 0; i < NI; ++i)
