@@ -239,8 +239,13 @@ struct SplitArgs {
 // Q6_K block kb, as four planes over all tiles * nb tile-blocks, each ordered so
 // that lane l = 32 p + r of a wave (row r) loads one contiguous stretch.  In terms
 // of row r's block in the Q6T planes:
-//   ql [tb][q < 4][l][16 B]  its ql chunk 2q + p
-//   qh [tb][q < 4][l][8 B]   its qh bytes 8 (2q + p) .. + 7
+//   ql [tb][q < 4][l][16 B]  code words X0 .. X3 of its chunk 2q + p (l0 = 8 (c % 4)
+//                            in half c / 4 of the block)
+//   qh [tb][q < 4][l][8 B]   code words X4, X5 of that chunk
+//   The chunk's 32 codes are the 4 sub-blocks' codes of l = l0 .. l0 + 7; word
+//   X(2s + w), s < 3, byte b holds l = l0 + 4w + b's sub-block s code in bits 2..7
+//   and bits 2s, 2s + 1 of its sub-block 3 code in bits 0..1 (6 bits per code, as
+//   in the Q6_K planes: k_q6_tile_pack's code_words).
 //   sc [tb][h < 2][r][8 B]   its scale groups 2h, 2h + 1, each int8 scale stored as
 //                            sc + 128 (128, a zero scale, throughout a block whose d is
 //                            zero: such a block contributes zero weights)

@@ -297,25 +297,19 @@ __device__ __forceinline__ half8 lds_frag(const _Float16 *__restrict__ b, uint32
 }
 
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-// Two codes c0, c1 (bytes 0, 1 or 2, 3 of `c`) -> half2 (c - 32) exactly: the
-// byte permute forms binary16 0x64cc = 1024 + c, then 1056 is subtracted.
-__device__ __forceinline__ half2v codes_lo(uint32_t c)
+// Bytes 0, 1 (hi false) or 2, 3 of t, each a 6-bit code c in bits 2..7 -> the
+// binary16 pair 256 + c: the byte permute puts 0x5C (exponent 8) above each byte.
+__device__ __forceinline__ half2v codes256(uint32_t t, bool hi)
 {
-    const uint32_t v = __builtin_amdgcn_perm(c, 0x64646464u, 0x01050004u);
-    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1056.0f, (_Float16)1056.0f};
-}
-__device__ __forceinline__ half2v codes_hi(uint32_t c)
-{
-    const uint32_t v = __builtin_amdgcn_perm(c, 0x64646464u, 0x01070006u);
-    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1056.0f, (_Float16)1056.0f};
+    return __builtin_bit_cast(half2v, __builtin_amdgcn_perm(t, 0x5C5C5C5Cu, hi ? 0x01070006u : 0x01050004u));
 }
 
 // A lane's Q6_K bytes for one half block (128 weights) of one row: the chunks of
-// its two l0 groups (chunk c of the half block covers l0 in [8c', 8c' + 8) of
-// the ql / qh planes): 16 B of low bits, 8 B of high bits and the 4 scales.
+// its two l0 groups (chunk c of the half block covers l0 in [8c', 8c' + 8)), each
+// 32 six-bit codes in six words (the tile copy's code form) and the 4 scales.
 struct AChunk {
-    uint4 ql;
-    uint2 qh;
+    uint4 ql; // code words X0 .. X3
+    uint2 qh; // code words X4, X5
     uint32_t sc;
 };
 
@@ -356,6 +350,22 @@ __device__ __forceinline__ uint32_t tile_d(const uint8_t *wb, size_t ntb, size_t
     return reinterpret_cast<const uint16_t *>(wb + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r];
 }
 
+// The code words of one chunk half w (l = l0 + 4w + b, byte b) from its row-major
+// plane words: A = ql[l], B = ql[l + 32], H = qh[l].  The Q6_K codes of sub-blocks
+// 0..3 are (A & 15) | (H & 3) << 4, (B & 15) | (H >> 2 & 3) << 4, (A >> 4) | (H >> 4
+// & 3) << 4 and (B >> 4) | (H >> 6) << 4 (the element order of q6k.rs's dequant);
+// word s < 3 holds code s in bits 2..7 of each byte and bits 2s, 2s + 1 of code 3
+// in bits 0..1.
+__device__ __forceinline__ void code_words(uint32_t A, uint32_t B, uint32_t H, uint32_t (&X)[3])
+{
+    const uint32_t M4 = 0x0F0F0F0Fu, M2 = 0x30303030u, M1 = 0x03030303u;
+    const uint32_t c0 = (A & M4) | ((H << 4) & M2), c1 = (B & M4) | ((H << 2) & M2);
+    const uint32_t c2 = ((A >> 4) & M4) | (H & M2), c3 = ((B >> 4) & M4) | ((H >> 2) & M2);
+    X[0] = (c0 << 2) | (c3 & M1);
+    X[1] = (c1 << 2) | ((c3 >> 2) & M1);
+    X[2] = (c2 << 2) | ((c3 >> 4) & M1);
+}
+
 // Row-major Q6_K planes -> Q6Tiles (the layout is described with the struct).
 // Workgroup tb (64 lanes, lane l = 32 p + r) writes tile-block tb: rows past the
 // slice's end are zero (d = 0: they contribute zero weights).
@@ -374,8 +384,11 @@ extern "C" __global__ __launch_bounds__(64) void k_q6_tile_pack(const TilePackAr
         const uint32_t c = 2 * q + p;
         const uint4 vl = ok ? *reinterpret_cast<const uint4 *>(s + blk * 128 + c * 16) : make_uint4(0, 0, 0, 0);
         const uint2 vh = ok ? *reinterpret_cast<const uint2 *>(s + nblk * 128 + blk * 64 + c * 8) : make_uint2(0, 0);
-        *reinterpret_cast<uint4 *>(d + tb * TILE_QL + q * 1024 + l * 16) = vl;
-        *reinterpret_cast<uint2 *>(d + ntb * TILE_QL + tb * TILE_QH + q * 512 + l * 8) = vh;
+        uint32_t X0[3], X1[3]; // chunk halves w = 0, 1
+        code_words(vl.x, vl.z, vh.x, X0);
+        code_words(vl.y, vl.w, vh.y, X1);
+        *reinterpret_cast<uint4 *>(d + tb * TILE_QL + q * 1024 + l * 16) = make_uint4(X0[0], X1[0], X0[1], X1[1]);
+        *reinterpret_cast<uint2 *>(d + ntb * TILE_QL + tb * TILE_QH + q * 512 + l * 8) = make_uint2(X0[2], X1[2]);
     }
     // scales as sc + 128 (sc ^ 0x80), or 128 throughout when d is +-0
     const uint16_t vd = ok ? reinterpret_cast<const uint16_t *>(s + nblk * 208)[blk] : (uint16_t)0;
@@ -387,37 +400,55 @@ extern "C" __global__ __launch_bounds__(64) void k_q6_tile_pack(const TilePackAr
         reinterpret_cast<uint16_t *>(d + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r] = vd;
 }
 
-// The scales of sub-blocks 2q and 2q + 1 of a chunk as binary16: its scale bytes
-// are sc + 128 (zero throughout a block whose d is zero), so the byte permute that
-// forms 1024 + (sc + 128) and a subtraction of 1152 give sc exactly.
-__device__ __forceinline__ half2v stage_scales(uint32_t sc, int q)
+// The scales of sub-blocks 2q and 2q + 1 of a chunk as binary16 (sc) and -288
+// times them (bias): its scale bytes are sc + 128 (zero throughout a block whose d
+// is zero), so the byte permute that forms 1024 + (sc + 128) and a subtraction of
+// 1152 give sc exactly; 288 sc = 9 sc * 32 is exact too (|9 sc| <= 1152).
+struct StageScales {
+    half2v sc, bias;
+};
+__device__ __forceinline__ StageScales stage_scales(uint32_t sc, int q)
 {
     const uint32_t v = __builtin_amdgcn_perm(sc, 0x64646464u, q ? 0x01070006u : 0x01050004u);
-    return __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
+    const half2v s = __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
+    return {s, s * (half2v){(_Float16)-288.0f, (_Float16)-288.0f}};
 }
 
-// The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in
-// MFMA A-operand order; ss = stage_scales of the chunk for stage s / 2.  Exact while
-// |sc * (q6 - 32)| <= 2048, within 1/2 ulp otherwise.
-__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, half2v ss)
+// The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in MFMA
+// A-operand order; ss = stage_scales of the chunk for stage s / 2.  Each is one
+// fused multiply-add of the code pair's 256 + c: (256 + c) sc - 288 sc, rounded
+// once, i.e. exact while |sc * (q6 - 32)| <= 2048 and within 1/2 ulp otherwise.
+// Sub-blocks 0..2 mask their code word; sub-block 3 gathers its code's three bit
+// pairs from the other words.
+__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, _Float16 scf, _Float16 bf)
 {
-    const _Float16 scf = ss[s & 1];
-    const half2v sc2 = {scf, scf};
+    const half2v sc2 = {scf, scf}, b2 = {bf, bf};
     half2v o[4];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
-        const uint32_t Aw = w ? c.ql.y : c.ql.x, Bw = w ? c.ql.w : c.ql.z, H = w ? c.qh.y : c.qh.x;
-        uint32_t cc;
+        const uint32_t X0 = w ? c.ql.y : c.ql.x, X1 = w ? c.ql.w : c.ql.z, X2 = w ? c.qh.y : c.qh.x;
+        const uint32_t M1 = 0x03030303u;
+        uint32_t t;
         switch (s) {
-        case 0: cc = (Aw & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u); break;
-        case 1: cc = (Bw & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u); break;
-        case 2: cc = ((Aw >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u); break;
-        default: cc = ((Bw >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u); break;
+        case 0: t = X0 & ~(M1); break;
+        case 1: t = X1 & ~(M1); break;
+        case 2: t = X2 & ~(M1); break;
+        default: t = (((((X2 & M1) << 2) | (X1 & M1)) << 2) | (X0 & M1)) << 2; break;
         }
-        o[2 * w] = codes_lo(cc) * sc2;
-        o[2 * w + 1] = codes_hi(cc) * sc2;
+        o[2 * w] = __builtin_elementwise_fma(codes256(t, false), sc2, b2);
+        o[2 * w + 1] = __builtin_elementwise_fma(codes256(t, true), sc2, b2);
     }
     return (half8){o[0][0], o[0][1], o[1][0], o[1][1], o[2][0], o[2][1], o[3][0], o[3][1]};
+}
+__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, const StageScales &ss)
+{
+    return decode_frag(c, s, ss.sc[s & 1], ss.bias[s & 1]);
+}
+// The same with the bias formed here (one multiply more per fragment, no
+// register held for it across the stage).
+__device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, half2v sc)
+{
+    return decode_frag(c, s, sc[s & 1], sc[s & 1] * (_Float16)-288.0f);
 }
 
 // C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, zrows) of group
@@ -617,7 +648,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int ch = 0; ch < 2; ++ch)
-                ss[i][ch] = stage_scales(A[i][ch].sc, q);
+                ss[i][ch] = stage_scales(A[i][ch].sc, q).sc;
         half8 afc[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -894,7 +925,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         // k-step kq reads k-piece 2 kq + p of row lr
         lds_frags_issue(lds_addr(rb) + (p * 256 + lr * 8) * 2, bch, bcl);
         // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
-        half2v ss[NI][2];
+        StageScales ss[NI][2];
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll

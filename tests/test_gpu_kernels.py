@@ -177,3 +177,45 @@ def test_gemm_prefill_full_int8_scales(gpu, oracle, T):
         err = rel_l2(y[t], oracle.q6k_matvec(raw, in_dim, rows, x[t]))
         print(f"T={T} token {t}: rel-L2 {err:.2e}")
         assert err <= 4e-4, (t, err)
+
+
+def encode_q6k(codes, scales, d):
+    """GGUF block_q6_K bytes from 6-bit codes [n][256], int8 scales [n][16] and
+    binary16 d [n]: element 128h + l + 32j of a block is code j of l in half h,
+    low 4 bits in ql (j = 0, 1 low nibbles of ql[64h + l], ql[64h + 32 + l]; j = 2, 3
+    their high nibbles), high 2 bits in qh[32h + l] bits 2j, 2j + 1."""
+    n = codes.shape[0]
+    raw = np.zeros((n, 210), dtype=np.uint8)
+    for h in range(2):
+        c = codes[:, 128 * h:128 * h + 128].reshape(n, 4, 32).astype(np.uint8)
+        raw[:, 64 * h:64 * h + 32] = (c[:, 0] & 15) | ((c[:, 2] & 15) << 4)
+        raw[:, 64 * h + 32:64 * h + 64] = (c[:, 1] & 15) | ((c[:, 3] & 15) << 4)
+        raw[:, 128 + 32 * h:160 + 32 * h] = ((c[:, 0] >> 4) | ((c[:, 1] >> 4) << 2) | ((c[:, 2] >> 4) << 4)
+                                            | ((c[:, 3] >> 4) << 6))
+    raw[:, 192:208] = scales.astype(np.int8).view(np.uint8)
+    raw[:, 208:210] = d.astype(np.float16).view(np.uint8).reshape(n, 2)
+    return raw
+
+
+@pytest.mark.parametrize("T,k0", [(256, 0), (64, 0), (64, 192), (8, 100)])
+def test_gemm_prefill_weights_exact(gpu, oracle, T, k0):
+    """Every binary16 weight the matrix-core GEMMs form, bit for bit: row r has
+    scale r - 128 in all sub-blocks, d = 1, and codes (k + r) % 64, so the 256 rows
+    hold every (scale, code) pair; token t is the one-hot vector of column k0 + t,
+    so y[t][r] is weight (r, k0 + t) times 1 with nothing else added, and must
+    equal binary16(sc (q - 32)) rounded to nearest even (exact up to magnitude
+    2048).  The encoding is checked against the oracle's dequant first.  T = 256
+    runs the 128-token tiles, T <= 128 the 32-token tiles."""
+    rows, in_dim = 256, 256
+    k = np.arange(in_dim)
+    codes = (k[None, :] + np.arange(rows)[:, None]) % 64
+    scales = np.repeat((np.arange(rows) - 128)[:, None], 16, axis=1)
+    raw = encode_q6k(codes, scales, np.ones(rows)).reshape(-1)
+    exact = (scales[:, k // 16] * (codes - 32)).astype(np.float64)
+    assert np.array_equal(oracle.dequant_rows(raw, rows, in_dim).astype(np.float64), exact)
+    x = np.zeros((T, in_dim), dtype=np.float32)
+    x[np.arange(T), k0 + np.arange(T)] = 1.0
+    y = gpu.q6k_gemm(gpu.Q6Weight(raw, rows, in_dim), x)
+    want = exact[:, k0:k0 + T].T.astype(np.float16).astype(np.float32)
+    bad = np.argwhere(y.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, [(int(t), int(r), float(y[t, r]), float(want[t, r])) for t, r in bad[:8]]
