@@ -106,7 +106,7 @@ struct Shape {
 
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
-    hipFunction_t split_rows, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
+    hipFunction_t split_rows, split_rows_ext, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
         tile_pack;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
@@ -230,7 +230,8 @@ static int get_kernels(Kernels **out)
     struct {
         hipFunction_t *f;
         const char *name;
-    } pfns[] = {{&k->split_rows, "k_split_rows"},       {&k->gemm_q6, "k_gemm_q6"},
+    } pfns[] = {{&k->split_rows, "k_split_rows"},       {&k->split_rows_ext, "k_split_rows_ext"},
+                {&k->gemm_q6, "k_gemm_q6"},
                 {&k->conv_prefill, "k_conv_prefill"},
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
                 {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_prefill, "k_router_prefill"},
@@ -611,7 +612,8 @@ struct RouterPart {
 static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
                        uint32_t part_rows, uint32_t n_used, float *part, size_t part_cap, uint64_t *dispatches,
                        const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr,
-                       uint32_t *deferred = nullptr, const RouterPart *router = nullptr, bool *router_done = nullptr)
+                       uint32_t *deferred = nullptr, const RouterPart *router = nullptr, bool *router_done = nullptr,
+                       ReduceCombineArgs *defer_combine = nullptr)
 {
     if (router_done)
         *router_done = false;
@@ -649,8 +651,13 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     }
     if (combine) { // grouped down projection: slices and the rank combine in one pass
         ReduceCombineArgs rc{part, combine->wsel, combine->x, S, combine->T, combine->dim, combine->n_used};
-        RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
         *combined = true;
+        if (defer_combine) { // the caller's next split applies it
+            *defer_combine = rc;
+            *dispatches += 1;
+            return LFM_OK;
+        }
+        RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
     } else {
         GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used,
                          nullptr, nullptr, nullptr, nullptr, 0};
@@ -833,6 +840,10 @@ struct lfm_engine {
         // whether the current layer's were written
         float *rpart = nullptr, *rss = nullptr;
         bool router_ready = false;
+        // small calls: the last MoE FFN's combine, left for the next layer's first
+        // split to apply (comb_pending)
+        ReduceCombineArgs comb{};
+        bool comb_pending = false;
     } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
@@ -1580,9 +1591,11 @@ static SplitArgs split_args(lfm_engine *e, const float *x, const float *norm, ui
     return a;
 }
 
+// lists: (grouped, spr 4) form pos and the expert lists in the split itself.
+// A pending combine (small calls) of the rows of x is applied first.
 static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
                     uint32_t T, bool grouped = false, uint32_t spr = 1, const float *copy_src = nullptr,
-                    float *copy_dst = nullptr, uint32_t copy_n = 0)
+                    float *copy_dst = nullptr, uint32_t copy_n = 0, bool lists = false)
 {
     if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
         return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
@@ -1590,7 +1603,25 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
     a.copy_src = copy_src;
     a.copy_dst = copy_dst;
     a.copy_n = copy_n;
-    RC(launch(e->K->split_rows, dim3(rows), 0, e->stream, a));
+    if (lists) {
+        a.tok = e->pf.tok;
+        a.slot = e->pf.slot;
+        a.counts = e->pf.counts;
+        a.list_stride = e->ctx;
+        a.n_expert = e->hp.n_expert;
+    }
+    if (e->pf.comb_pending) {
+        const ReduceCombineArgs &c = e->pf.comb;
+        if (c.x != x || c.T != rows || c.dim != K)
+            return fail(LFM_EINVAL, "split: a pending combine covers other rows");
+        a.cpart = c.part;
+        a.cwsel = c.wsel;
+        a.cx = c.x;
+        a.cksplit = c.ksplit;
+        a.cn_used = c.n_used;
+        e->pf.comb_pending = false;
+    }
+    RC(launch(a.cpart || a.tok ? e->K->split_rows_ext : e->K->split_rows, dim3(rows), 0, e->stream, a));
     e->dispatches += 1;
     return LFM_OK;
 }
@@ -1648,7 +1679,8 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6Tiles &wg, const Q6Tiles &wu, u
 // `tok`, output rows `slot`, counts per expert on the device.
 static int pf_gemm_grouped(lfm_engine *e, const Q6Tiles &w, uint32_t zrows, uint32_t T,
                            const uint32_t *tok, float *c, uint32_t ldc,
-                           const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr)
+                           const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr,
+                           ReduceCombineArgs *defer_combine = nullptr)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
@@ -1665,7 +1697,8 @@ static int pf_gemm_grouped(lfm_engine *e, const Q6Tiles &w, uint32_t zrows, uint
     g.c = c;
     g.ldc = ldc;
     return launch_gemm(e->K, e->stream, g, false, T, e->hp.n_expert, 4 * T, e->hp.n_used, e->pf.part,
-                       GEMM_PART_BYTES / 4, &e->dispatches, combine, combined);
+                       GEMM_PART_BYTES / 4, &e->dispatches, combine, combined, nullptr, nullptr, nullptr,
+                       defer_combine);
 }
 
 // The mixer's output projection, added to the residual.  Before a MoE FFN in a
@@ -1738,7 +1771,9 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
 }
 
 // FFN over T rows starting at x (the last layer runs only the last row).
-static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
+// defer_ok: a split of the same rows follows (another layer), which may apply
+// the MoE combine.
+static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok)
 {
     const lfm_hparams &hp = e->hp;
     const uint32_t dim = hp.dim;
@@ -1772,16 +1807,30 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
         e->dispatches += 1;
     }
     RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
-    RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
-    RC(pf_split(e, x, norm, T, dim, T, true, 4));
-    e->dispatches += 2;
+    e->dispatches += 1;
+    // small calls: the split forms the expert lists itself (no k_route_group)
+    const bool small = T <= GEMM_TOKENS;
+    if (!small) {
+        RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
+        e->dispatches += 1;
+    }
+    RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, small));
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
+    // small calls before another layer: the combine is left to the next layer's
+    // first split (its rows are this call's, x = e->pf.x)
+    const bool defer = small && defer_ok && x == e->pf.x;
     bool combined = false;
     RC(pf_gemm_grouped(e, q6tiles(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,
-                       &combined));
+                       &combined, defer ? &e->pf.comb : nullptr));
+    if (defer) {
+        if (!combined) // one K slice: the down projection wrote d itself
+            e->pf.comb = ReduceCombineArgs{e->pf.d, e->pf.wsel, x, 1, T, dim, hp.n_used};
+        e->pf.comb_pending = true;
+        return LFM_OK;
+    }
     if (!combined)
         RC(launch(e->K->combine_prefill, dim3((dim + 1023) / 1024, T), 0, e->stream, cb)); // 4 k per thread
     e->dispatches += combined ? 0 : 1;
@@ -1793,16 +1842,19 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T)
 static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
 {
     const lfm_hparams &hp = e->hp;
+    e->pf.comb_pending = false;
     EmbedRowsArgs em{q6(e, "token_embd.weight"), e->ids, e->pf.x, T};
     RC(launch(e->K->embed_rows, dim3((T + 3) / 4), 0, e->stream, em));
     e->dispatches += 1;
     for (uint32_t l = 0; l < hp.n_layers; ++l) {
         RC(pf_mixer(e, l, T, start));
         if (l + 1 < hp.n_layers)
-            RC(pf_ffn(e, l, e->pf.x, T));
+            RC(pf_ffn(e, l, e->pf.x, T, true));
         else
-            RC(pf_ffn(e, l, e->pf.x + (size_t)(T - 1) * hp.dim, 1));
+            RC(pf_ffn(e, l, e->pf.x + (size_t)(T - 1) * hp.dim, 1, false));
     }
+    if (e->pf.comb_pending) // cannot happen: the last layer combines itself
+        return fail(LFM_ESTATE, "prefill: a combine was left pending");
     HIPCHK(hipMemcpyAsync(e->x, e->pf.x + (size_t)(T - 1) * hp.dim, hp.dim * 4,
                           hipMemcpyDeviceToDevice, e->stream));
     return LFM_OK;

@@ -222,8 +222,21 @@ struct SplitArgs {
     // token rows of the gate/up input, spr 1: slot rows of the down input); slot s
     // with rank s % 4 < n_used goes to logical row sel[s] * rpe + pos[s] (expert
     // sel[s], index pos[s] in its token list, rpe rows reserved per expert)
-    const uint32_t *sel, *pos;
+    const uint32_t *sel;
+    uint32_t *pos;
     uint32_t spr, n_used, rpe;
+    // SPLIT_GROUPED with tok set (spr 4, T <= 256 rows, n_expert <= 64): pos is
+    // formed here from sel instead of read, together with k_route_group's lists
+    // (tok[e][i] = token, slot[e][i] = token * 4 + rank in token order, counts[e]),
+    // so that no separate grouping launch precedes the split
+    uint32_t *tok, *slot, *counts;
+    uint32_t list_stride, n_expert;
+    // nullable (small calls): before the split, row t of x first gets the down
+    // projection's ranks combined into it as k_reduce_combine does (x += sum_r
+    // cwsel[t][r] (sum_s cpart[s][t*4 + r]), rank then slice order), written back
+    const float *cpart, *cwsel;
+    float *cx;
+    uint32_t cksplit, cn_used;
     // nullable: the workgroups also copy copy_n floats (a multiple of 4, 16-byte
     // aligned) from copy_src to copy_dst (the short conv's new state, written by the
     // kernel before this one)

@@ -155,7 +155,120 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
     }
 }
 
-template <bool NORM>
+// Row t of x plus the down projection's ranks, as k_reduce_combine forms it:
+// d_r = sum of the cksplit slices in slice order, then x + ((0 + d_0 w_0) + d_1 w_1
+// ...) over the used ranks (lfm.rs:645-668, no contraction); the new values are
+// written back to cx.  v holds the row's pieces (thread tid: pieces tid + 256 i).
+__device__ __forceinline__ void combine_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8])
+{
+#pragma clang fp contract(off)
+    const uint32_t tid = threadIdx.x, npc = a.K >> 3;
+    const size_t D = a.K, slice = (size_t)a.T * 4 * D;
+    float w[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        w[r] = a.cwsel[(size_t)t * 4 + r];
+#pragma unroll
+    for (int i = 0; i < SPLIT_NP; ++i) {
+        const uint32_t pc = tid + WG_THREADS * i;
+        if (pc >= npc)
+            continue;
+        const float *pp = a.cpart + (size_t)t * 4 * D + 8 * pc;
+        float d[4][8];
+        for (uint32_t s0 = 0; s0 < a.cksplit; s0 += 2) { // two slices' loads at a time
+            float4 q[2][4][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        q[j][r][h] = *reinterpret_cast<const float4 *>(
+                            pp + (size_t)min(s0 + j, a.cksplit - 1) * slice + r * D + 4 * h);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (s0 + j < a.cksplit) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float qq[8] = {q[j][r][0].x, q[j][r][0].y, q[j][r][0].z, q[j][r][0].w,
+                                             q[j][r][1].x, q[j][r][1].y, q[j][r][1].z, q[j][r][1].w};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            d[r][e] = s0 + j == 0 ? qq[e] : d[r][e] + qq[e];
+                    }
+                }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (r < (int)a.cn_used)
+                    sm = sm + d[r][e] * w[r];
+            v[i][e] = v[i][e] + sm;
+        }
+        float *o = a.cx + (size_t)t * D + 8 * pc;
+        *reinterpret_cast<float4 *>(o) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        *reinterpret_cast<float4 *>(o + 4) = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+    }
+}
+
+// The logical rows of token t's expert slots (SPLIT_GROUPED with tok set): slot r
+// of t (r < n_used) goes to expert e_r = sel[t][r] at index pos_r = the number of
+// earlier tokens that selected e_r (k_route_group's token order), found by every
+// thread i < T testing token i's selection with ballots.  The workgroup also
+// writes its slots' list entries and pos; workgroup 0 writes the counts.
+__device__ __forceinline__ uint32_t route_rows(const SplitArgs &a, uint32_t t, uint32_t (&L)[4])
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ uint32_t wc[4][4], hist[64];
+    uint32_t mine[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        mine[r] = a.sel[(size_t)t * 4 + r];
+    uint32_t ids[4] = {~0u, ~0u, ~0u, ~0u};
+    if (tid < a.T) {
+        const uint4 s4 = *reinterpret_cast<const uint4 *>(a.sel + (size_t)tid * 4);
+        ids[0] = s4.x, ids[1] = s4.y, ids[2] = s4.z, ids[3] = s4.w;
+    }
+    for (uint32_t r = a.n_used; r < 4; ++r)
+        ids[r] = ~0u;
+    if (t == 0) { // uniform
+        if (tid < 64)
+            hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (ids[r] < 64)
+                atomicAdd(&hist[ids[r]], 1u);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bool hit = tid < t && (ids[0] == mine[r] || ids[1] == mine[r] || ids[2] == mine[r] || ids[3] == mine[r]);
+        const uint64_t m = __ballot(hit);
+        if (lane == 0)
+            wc[wave][r] = (uint32_t)__popcll(m);
+    }
+    __syncthreads();
+    if (t == 0 && tid < a.n_expert)
+        a.counts[tid] = hist[tid];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (r < (int)a.n_used) {
+            const uint32_t pr = wc[0][r] + wc[1][r] + wc[2][r] + wc[3][r], e = mine[r];
+            L[r] = e * a.rpe + pr;
+            if (tid == 0) {
+                a.tok[(size_t)e * a.list_stride + pr] = t;
+                a.slot[(size_t)e * a.list_stride + pr] = t * 4 + r;
+                a.pos[(size_t)t * 4 + r] = pr;
+            }
+        }
+    return a.n_used;
+}
+
+// EXT: the small calls' extra duties (a pending combine, the expert lists), in a
+// kernel of their own so that the plain split keeps its registers.
+template <bool NORM, bool EXT>
 __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
 {
     const uint32_t tid = threadIdx.x, npc = a.K >> 3;
@@ -182,8 +295,12 @@ __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
     if (a.copy_src) // uniform: one float4 per thread of the first copy_n / 1024 rows' workgroups
         for (uint32_t u = t * WG_THREADS + tid; u < a.copy_n / 4; u += a.T * WG_THREADS)
             reinterpret_cast<float4 *>(a.copy_dst)[u] = reinterpret_cast<const float4 *>(a.copy_src)[u];
+    if (EXT && a.cpart) // uniform
+        combine_pieces(a, t, v);
     uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
-    if (a.mode == SPLIT_GROUPED) { // uniform
+    if (EXT && a.mode == SPLIT_GROUPED && a.tok) { // uniform
+        nl = route_rows(a, t, L);
+    } else if (a.mode == SPLIT_GROUPED) { // uniform
         nl = 0;
         for (uint32_t j = 0; j < a.spr; ++j) {
             const uint32_t s = t * a.spr + j;
@@ -200,9 +317,20 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const Spli
     if (t >= a.T)
         return;
     if (a.norm_w) // uniform
-        split_rows_body<true>(a, t);
+        split_rows_body<true, false>(a, t);
     else
-        split_rows_body<false>(a, t);
+        split_rows_body<false, false>(a, t);
+}
+
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows_ext(const SplitArgs a)
+{
+    const uint32_t t = blockIdx.x;
+    if (t >= a.T)
+        return;
+    if (a.norm_w) // uniform
+        split_rows_body<true, true>(a, t);
+    else
+        split_rows_body<false, true>(a, t);
 }
 
 // s_waitcnt immediate (gfx9 encoding): vector-memory count <= n, LDS/scalar count 0,
