@@ -415,6 +415,21 @@ __device__ __forceinline__ void lds_frags_wait(half8 (&h)[4], half8 (&l)[4])
                  : "+v"(h[0]), "+v"(h[1]), "+v"(h[2]), "+v"(h[3]), "+v"(l[0]), "+v"(l[1]), "+v"(l[2]), "+v"(l[3]));
 }
 // 32-bit LDS address of a __shared__ object
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+// Stores v at LDS byte address waddr, then reads the 16 floats at raddr + 32 k
+// (k < 4, 4 each) back, in order within the wave, and waits for them.
+__device__ __forceinline__ void lds_rowf(uint32_t waddr, float v, uint32_t raddr, floatx4 (&f)[4])
+{
+    asm volatile("ds_write_b32 %4, %5\n\t"
+                 "ds_read_b128 %0, %6\n\t"
+                 "ds_read_b128 %1, %6 offset:32\n\t"
+                 "ds_read_b128 %2, %6 offset:64\n\t"
+                 "ds_read_b128 %3, %6 offset:96\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3])
+                 : "v"(waddr), "v"(v), "v"(raddr));
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void *p)
 {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
@@ -966,9 +981,10 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // below 2^31 (the host bounds the activation copies).
     const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
     const uint32_t bsrc = 2 * (lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8);
-    // four stage buffers, hi then lo (stage s in buffer s & 3), each its own array
-    __shared__ __attribute__((aligned(16))) _Float16 B0[2 * 8 * 256], B1[2 * 8 * 256], B2[2 * 8 * 256],
-        B3[2 * 8 * 256];
+    // six stage buffers of 8 KB, hi then lo (stage s in buffer s % 6); every LDS
+    // read of them is in assembly, so the compiler adds no waits for the tiles in
+    // flight and the buffer can be picked at run time
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[6][2 * 8 * 256];
     typedef AChunk BlockW[2][NI][2]; // a block's weights: [half][row tile][chunk]
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
@@ -976,9 +992,10 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         for (int i = 0; i < NI; ++i)
             load_tile_chunks<true>(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb, h, lane, A[i]);
     };
-    // stage st's tile into buffer dst (this wave's two 16-byte pieces per lane)
-    auto loadB = [&](uint32_t st, _Float16 *__restrict__ dst) {
+    // stage st's tile into its buffer (this wave's two 16-byte pieces per lane)
+    auto loadB = [&](uint32_t st) {
         const uint32_t o = bsrc + (kb0 * 4 + st) * TK * 32 * 2;
+        _Float16 *dst = Bs[st % 6];
         lds_dma16(xh, o, &dst[wave * 512]);
         lds_dma16(xl, o, &dst[8 * 256 + wave * 512]);
     };
@@ -996,11 +1013,20 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         for (int e = 0; e < 16; ++e)
             acc[i][e] = 0.f;
     // accumulator element e of a lane is row 8 (e / 4) + 4p + e % 4 of its tile,
-    // whose scale lives in lane (that row)
+    // whose factor v lives in lane (that row) % 32: the wave passes the 32 factors
+    // through its own LDS slots (one store, four 16-byte reads of 4 rows each,
+    // in order within the wave) instead of 16 lane shuffles
+    // (in assembly: the compiler would wait for the activation tiles in flight
+    // before reading an LDS array it cannot tell apart from their buffers)
+    __shared__ __attribute__((aligned(16))) float rowf[4][NI][32];
     auto by_row = [&](int i, float v) {
+        floatx4 f[4]; // lanes lr and lr + 32 store the same value
+        lds_rowf(lds_addr(&rowf[wave][i][lr]), v, lds_addr(&rowf[wave][i][4 * p]), f);
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-            acc[i][e] *= __shfl(v, 8 * (e / 4) + 4 * p + (e % 4), 64);
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][4 * k + j] *= f[k][j];
     };
     float u[NI], dcur[NI];
     uint32_t dnext[NI];
@@ -1019,16 +1045,14 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     };
     const uint32_t nst = nbl * 4;
 
-    // Stage s = 4 kb + j.  Issue order per block, so that the loads waited for at
-    // each stage's end leave everything issued after them in flight (loads retire
-    // in issue order): stage j first loads stage s + 3's tile (into the buffer the
-    // last barrier freed), then at j = 0 the next block's first half of the weights
-    // and its scales, at j = 2 its second half.  The weights thus have a block of
-    // stages to arrive and the tiles three stages.  The buffers arrive as restrict-
-    // qualified pointers, so the compiler sees that the stage's LDS reads do not
-    // touch the tile in flight.
-    auto stage = [&](uint32_t kb, int j, const _Float16 *__restrict__ rb, _Float16 *__restrict__ nbuf,
-                     BlockW &W, BlockW &N) {
+    // Stage s = 4 kb + j.  The workgroup meets at a barrier after odd stages only:
+    // an even stage issues the tiles of stages s + 4 and s + 5 into the buffers of
+    // stages s - 2 and s - 1, which every wave left before the last barrier.  Then
+    // at j = 0 the next block's first half of the weights and its scales, at j = 2
+    // its second half.  Loads retire in issue order, so each odd stage's wait for
+    // the tiles and weights of the next two stages leaves everything issued after
+    // them in flight: the weights have three stages to arrive, the tiles four.
+    auto stage = [&](uint32_t kb, int j, BlockW &W, BlockW &N) {
         const uint32_t st = kb * 4 + j;
         const bool more = kb + 1 < nbl; // a next block exists
         if (j == 0) {
@@ -1038,8 +1062,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             enter_block(kb == 0);
         }
         issue_fence();
-        if (st + 3 < nst)
-            loadB(st + 3, nbuf);
+        if ((j & 1) == 0) {
+            if (st + 4 < nst)
+                loadB(st + 4);
+            if (st + 5 < nst)
+                loadB(st + 5);
+        }
         issue_fence();
         if ((j == 0 || j == 2) && more) {
             loadA(2 * (kb + 1) + (j >> 1), N[j >> 1]);
@@ -1051,7 +1079,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         AChunk (&A)[NI][2] = W[j >> 1];
         half8 afc[NI], bch[4], bcl[4];
         // k-step kq reads k-piece 2 kq + p of row lr
-        lds_frags_issue(lds_addr(rb) + (p * 256 + lr * 8) * 2, bch, bcl);
+        lds_frags_issue(lds_addr(Bs[st % 6]) + (p * 256 + lr * 8) * 2, bch, bcl);
         // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
         StageScales ss[NI][2];
 #pragma unroll
@@ -1083,26 +1111,20 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                     afc[i] = afn[i];
             }
         }
-        if (st + 1 < nst) {
-            // Stage st + 1's tile has landed (and with it the weights and scales it
-            // needs, all issued before it) and every wave is done with buffer j.  The
-            // loads issued after that tile stay in flight: the next two tiles (2
-            // loads each) and the weights issued at the last j = 0 or 2 stages (5 NI
-            // per half block, NI scales with the first half).  Near the slice's end,
-            // where fewer were issued, the counts below shrink to what was issued.
+        if ((j & 1) && st + 1 < nst) {
+            // Stages st + 1 and st + 2 have their tiles and weights, and every wave is
+            // done with buffers st - 1 and st.  Still in flight (issued after what is
+            // waited for): j = 1: the tiles of stage st - 1 (4 loads) and the next
+            // block's first half + scales (6 NI) issued there; j = 3: the tiles of
+            // stage st - 1 and the next block's second half (5 NI).  Without a next
+            // block nothing was issued at stage st - 1, and the last stages wait for
+            // all.
             asm volatile("" ::: "memory");
-            if (j == 0 || j == 2) {
-                if (more)
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 11 * NI));
-                else if (j == 0)
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI));
-                else
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
-            } else if (j == 1) {
+            if (j == 1) {
                 if (more)
                     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 6 * NI));
                 else
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(2));
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
             } else {
                 __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI)); // j = 3 ends a block that has a next
             }
@@ -1111,25 +1133,27 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         }
     };
     auto block = [&](uint32_t kb, BlockW &W, BlockW &N) {
-        stage(kb, 0, B0, B3, W, N);
-        stage(kb, 1, B1, B0, W, N);
-        stage(kb, 2, B2, B1, W, N);
-        stage(kb, 3, B3, B2, W, N);
+        stage(kb, 0, W, N);
+        stage(kb, 1, W, N);
+        stage(kb, 2, W, N);
+        stage(kb, 3, W, N);
     };
-    // Prologue: what stages -4 .. -1 of a block before the first would have issued.
+    // Prologue: what stages -4 .. -1 of a block before the first would have issued
+    // (tiles 0, 1 and the first half block of weights with the scales at -4, tiles
+    // 2, 3 and the second half at -2), then the wait and barrier of stage -1.
     BlockW S0, S1;
+    loadB(0);
+    if (1 < nst)
+        loadB(1);
+    issue_fence();
     loadA(0, S0[0]);
     loadD(0, dnext);
     issue_fence();
-    loadB(0, B0);
-    loadB(1, B1);
+    loadB(2);
+    loadB(3);
     issue_fence();
     loadA(1, S0[1]);
     issue_fence();
-    loadB(2, B2);
-    issue_fence();
-    // the first tile, the first half block's weights and the first scales have landed
-    // (a bare barrier: a fence would wait for every load)
     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
