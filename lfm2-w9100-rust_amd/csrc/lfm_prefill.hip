@@ -931,7 +931,7 @@ k_gemm_q6_swiglu(const GemmArgs a)
 // so there is no LDS tile and no barrier, and each wave waits only for the
 // loads its next instructions use.  Same arithmetic per (row, token) as
 // gemm_body.  NI: 32-row tiles per wave (the pair form: its gate and up tile).
-template <bool PAIR, int NI>
+template <bool PAIR, int NI, int G>
 __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 {
     static_assert(!PAIR || NI == 2, "the pair form holds a gate and an up tile per wave");
@@ -981,10 +981,12 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // below 2^31 (the host bounds the activation copies).
     const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
     const uint32_t bsrc = 2 * (lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8);
-    // six stage buffers of 8 KB, hi then lo (stage s in buffer s % 6); every LDS
-    // read of them is in assembly, so the compiler adds no waits for the tiles in
-    // flight and the buffer can be picked at run time
-    __shared__ __attribute__((aligned(16))) _Float16 Bs[6][2 * 8 * 256];
+    // G + 4 stage buffers of 8 KB, hi then lo (stage s in buffer s % (G + 4));
+    // every LDS read of them is in assembly, so the compiler adds no waits for the
+    // tiles in flight and the buffer can be picked at run time
+    static_assert(G == 2 || G == 4, "a barrier every 2 or 4 stages");
+    constexpr uint32_t NBUF = G + 4;
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[NBUF][2 * 8 * 256];
     typedef AChunk BlockW[2][NI][2]; // a block's weights: [half][row tile][chunk]
     auto loadA = [=](uint32_t half, AChunk (&A)[NI][2]) {
         const uint32_t kb = kb0 + (half >> 1), h = half & 1;
@@ -995,7 +997,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // stage st's tile into its buffer (this wave's two 16-byte pieces per lane)
     auto loadB = [&](uint32_t st) {
         const uint32_t o = bsrc + (kb0 * 4 + st) * TK * 32 * 2;
-        _Float16 *dst = Bs[st % 6];
+        _Float16 *dst = Bs[st % NBUF];
         lds_dma16(xh, o, &dst[wave * 512]);
         lds_dma16(xl, o, &dst[8 * 256 + wave * 512]);
     };
@@ -1045,13 +1047,13 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     };
     const uint32_t nst = nbl * 4;
 
-    // Stage s = 4 kb + j.  The workgroup meets at a barrier after odd stages only:
-    // an even stage issues the tiles of stages s + 4 and s + 5 into the buffers of
-    // stages s - 2 and s - 1, which every wave left before the last barrier.  Then
-    // at j = 0 the next block's first half of the weights and its scales, at j = 2
-    // its second half.  Loads retire in issue order, so each odd stage's wait for
-    // the tiles and weights of the next two stages leaves everything issued after
-    // them in flight: the weights have three stages to arrive, the tiles four.
+    // Stage s = 4 kb + j.  The workgroup meets at a barrier after every G-th stage
+    // only: the first stage of a group issues the tiles of stages s + 4 .. s + 3 + G
+    // into buffers whose stages every wave left before the last barrier.  Then at j
+    // = 0 the next block's first half of the weights and its scales, at j = 2 its
+    // second half.  Loads retire in issue order, so each wait for the tiles and
+    // weights of the coming stages leaves everything issued after them in flight:
+    // the weights have three stages to arrive, the tiles at least four.
     auto stage = [&](uint32_t kb, int j, BlockW &W, BlockW &N) {
         const uint32_t st = kb * 4 + j;
         const bool more = kb + 1 < nbl; // a next block exists
@@ -1062,11 +1064,11 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             enter_block(kb == 0);
         }
         issue_fence();
-        if ((j & 1) == 0) {
-            if (st + 4 < nst)
-                loadB(st + 4);
-            if (st + 5 < nst)
-                loadB(st + 5);
+        if (j % G == 0) {
+#pragma unroll
+            for (int u = 0; u < G; ++u)
+                if (st + 4 + u < nst)
+                    loadB(st + 4 + u);
         }
         issue_fence();
         if ((j == 0 || j == 2) && more) {
@@ -1079,7 +1081,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         AChunk (&A)[NI][2] = W[j >> 1];
         half8 afc[NI], bch[4], bcl[4];
         // k-step kq reads k-piece 2 kq + p of row lr
-        lds_frags_issue(lds_addr(Bs[st % 6]) + (p * 256 + lr * 8) * 2, bch, bcl);
+        lds_frags_issue(lds_addr(Bs[st % NBUF]) + (p * 256 + lr * 8) * 2, bch, bcl);
         // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
         StageScales ss[NI][2];
 #pragma unroll
@@ -1111,7 +1113,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                     afc[i] = afn[i];
             }
         }
-        if ((j & 1) && st + 1 < nst) {
+        if (G == 2 && (j & 1) && st + 1 < nst) {
             // Stages st + 1 and st + 2 have their tiles and weights, and every wave is
             // done with buffers st - 1 and st.  Still in flight (issued after what is
             // waited for): j = 1: the tiles of stage st - 1 (4 loads) and the next
@@ -1131,6 +1133,26 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
         }
+        if (G == 4 && j == 1 && st + 1 < nst) {
+            // the block's second half of the weights has landed (no barrier: the
+            // tiles of stages st + 1, st + 2 came with the last one); in flight: the
+            // 4 tiles (8 loads) and the next block's first half + scales of stage st - 1
+            asm volatile("" ::: "memory");
+            if (more)
+                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(8 + 6 * NI));
+            else
+                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
+            asm volatile("" ::: "memory");
+        }
+        if (G == 4 && j == 3 && st + 1 < nst) {
+            // the next block's tiles, first half of the weights and scales have
+            // landed and every wave is done with this block's buffers; in flight: the
+            // next block's second half (5 NI)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(5 * NI));
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
     };
     auto block = [&](uint32_t kb, BlockW &W, BlockW &N) {
         stage(kb, 0, W, N);
@@ -1139,22 +1161,28 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         stage(kb, 3, W, N);
     };
     // Prologue: what stages -4 .. -1 of a block before the first would have issued
-    // (tiles 0, 1 and the first half block of weights with the scales at -4, tiles
-    // 2, 3 and the second half at -2), then the wait and barrier of stage -1.
+    // (G = 2: tiles 0, 1 and the first half block of weights with the scales at -4,
+    // tiles 2, 3 and the second half at -2; G = 4: tiles 0 .. 3, the first half and
+    // the scales at -4, the second half at -2), then the wait and barrier of stage -1.
     BlockW S0, S1;
     loadB(0);
-    if (1 < nst)
-        loadB(1);
+    loadB(1);
+    if (G == 4) {
+        loadB(2);
+        loadB(3);
+    }
     issue_fence();
     loadA(0, S0[0]);
     loadD(0, dnext);
     issue_fence();
-    loadB(2);
-    loadB(3);
+    if (G == 2) {
+        loadB(2);
+        loadB(3);
+    }
     issue_fence();
     loadA(1, S0[1]);
     issue_fence();
-    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 5 * NI));
+    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0((G == 2 ? 4 : 0) + 5 * NI));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     uint32_t kb = 0;
@@ -1206,14 +1234,15 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     }
 }
 
+// Two 32-row tiles per wave (two workgroups per CU): a barrier once per block.
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32(const GemmArgs a)
 {
-    gemm_small_body<false, 2>(a);
+    gemm_small_body<false, 2, 4>(a);
 }
 
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32(const GemmArgs a)
 {
-    gemm_small_body<true, 2>(a);
+    gemm_small_body<true, 2, 4>(a);
 }
 
 // One 32-row tile per wave (128 rows per workgroup, 144 VGPRs: three waves per
@@ -1221,7 +1250,7 @@ extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32(cons
 // slower for the expert and 6144-row shapes.
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32n1(const GemmArgs a)
 {
-    gemm_small_body<false, 1>(a);
+    gemm_small_body<false, 1, 2>(a); // three workgroups per CU: 6 tile buffers fit their LDS
 }
 
 // Sums the K slices of a split GEMM in slice order and applies its epilogue:
