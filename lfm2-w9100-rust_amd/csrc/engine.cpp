@@ -607,6 +607,7 @@ struct RouterPart {
     const float *norm, *w; // the FFN's RMSNorm weight and router rows [n_expert][zrows]
     float *rpart, *rss;
     uint32_t n_expert;
+    uint32_t *counts; // nullable: zeroed by the reduce (the next split counts into it)
 };
 
 static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_t T, uint32_t nz,
@@ -660,13 +661,14 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         RC(launch(K->reduce_combine, dim3((combine->dim + 255) / 256, combine->T), 0, s, rc));
     } else {
         GemmReduceArgs r{part, g.c, S, pair ? 1u : 0u, part_rows, g.zrows, g.ldc, g.col0, g.mode, n_used,
-                         nullptr, nullptr, nullptr, nullptr, 0};
+                         nullptr, nullptr, nullptr, nullptr, 0, nullptr};
         if (router && !pair && nz == 1 && g.zrows % 256 == 0 && router->n_expert <= 64) {
             r.rnorm = router->norm;
             r.rw = router->w;
             r.rpart = router->rpart;
             r.rss = router->rss;
             r.n_expert = router->n_expert;
+            r.counts = router->counts;
             if (router_done)
                 *router_done = true;
         }
@@ -1591,11 +1593,13 @@ static SplitArgs split_args(lfm_engine *e, const float *x, const float *norm, ui
     return a;
 }
 
-// lists: (grouped, spr 4) form pos and the expert lists in the split itself.
-// A pending combine (small calls) of the rows of x is applied first.
+// lists: (grouped, spr 4) form pos and the expert lists in the split itself;
+// route (with lists): the split also routes each token from the router partials
+// rg names.  A pending combine (small calls) of the rows of x is applied first.
 static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t rows, uint32_t K,
                     uint32_t T, bool grouped = false, uint32_t spr = 1, const float *copy_src = nullptr,
-                    float *copy_dst = nullptr, uint32_t copy_n = 0, bool lists = false)
+                    float *copy_dst = nullptr, uint32_t copy_n = 0, bool lists = false,
+                    const RouteGroupArgs *route = nullptr)
 {
     if (K == 0 || K % 256 || K > 8192) // k_split_rows keeps a row in registers
         return fail(LFM_EINVAL, "split: row width %u must be a multiple of 256 up to 8192", K);
@@ -1609,6 +1613,14 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
         a.counts = e->pf.counts;
         a.list_stride = e->ctx;
         a.n_expert = e->hp.n_expert;
+        if (route) {
+            a.rpart = route->rpart;
+            a.rss = route->rss;
+            a.rbias = route->bias;
+            a.sel_out = route->sel;
+            a.wsel_out = route->wsel;
+            a.nparts = route->nparts;
+        }
     }
     if (e->pf.comb_pending) {
         const ReduceCombineArgs &c = e->pf.comb;
@@ -1709,7 +1721,7 @@ static int pf_out_proj(lfm_engine *e, uint32_t l, const Q6Tiles &w, uint32_t T)
     e->pf.router_ready = false;
     if (l >= hp.dense_lead && T <= GEMM_TOKENS) {
         const RouterPart rp{f32(e, "blk.%u.ffn_norm.weight", l), f32(e, "blk.%u.ffn_gate_inp.weight", l), e->pf.rpart,
-                            e->pf.rss, hp.n_expert};
+                            e->pf.rss, hp.n_expert, e->pf.counts};
         return pf_gemm(e, w, T, e->pf.x, hp.dim, 0, 1, nullptr, &rp, &e->pf.router_ready);
     }
     return pf_gemm(e, w, T, e->pf.x, hp.dim, 0, 1);
@@ -1806,15 +1818,20 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
         e->dispatches += 1;
     }
-    RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
-    e->dispatches += 1;
-    // small calls: the split forms the expert lists itself (no k_route_group)
+    // small calls: the split forms the expert lists itself (no k_route_group), and
+    // with the out projection's router partials (and counts zeroed by its reduce) it
+    // routes each token too (no k_route_topk)
     const bool small = T <= GEMM_TOKENS;
+    const bool self_route = small && e->pf.router_ready && rg.nparts <= 8;
+    if (!self_route) {
+        RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
+        e->dispatches += 1;
+    }
     if (!small) {
         RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
         e->dispatches += 1;
     }
-    RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, small));
+    RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, small, self_route ? &rg : nullptr));
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank

@@ -231,6 +231,17 @@ struct SplitArgs {
     // so that no separate grouping launch precedes the split
     uint32_t *tok, *slot, *counts;
     uint32_t list_stride, n_expert;
+    // nullable (with tok): workgroup t routes token t itself from the preceding
+    // reduce's router partials (rpart / rss, nparts per token; k_route_topk's rule:
+    // logit = dot / sqrt(sum x^2 / K + eps), rbias added for the choice), writes
+    // sel_out / wsel_out, and takes each chosen expert's list index from counts[e]
+    // (zeroed by that reduce) with an atomic add: the lists are then in arrival
+    // order, which changes where a token's row sits in its expert's tile but not
+    // what is computed for it
+    const float *rpart, *rss, *rbias;
+    uint32_t *sel_out;
+    float *wsel_out;
+    uint32_t nparts;
     // nullable (small calls): before the split, row t of x first gets the down
     // projection's ranks combined into it as k_reduce_combine does (x += sum_r
     // cwsel[t][r] (sum_s cpart[s][t*4 + r]), rank then slice order), written back
@@ -318,6 +329,7 @@ struct GemmReduceArgs {    // c (+)= sum_s part[s] in slice order; pair: silu(g)
     const float *rnorm, *rw;
     float *rpart, *rss;
     uint32_t n_expert;
+    uint32_t *counts; // nullable (with rw): workgroup (0, 0) zeroes counts[0 .. n_expert)
 };
 
 struct ReduceCombineArgs { // x[t] += sum_r w[t][r] * (sum_s part[s][t*4 + r]), rank then slice order

@@ -268,6 +268,59 @@ __device__ __forceinline__ uint32_t route_rows(const SplitArgs &a, uint32_t t, u
 
 // EXT: the small calls' extra duties (a pending combine, the expert lists), in a
 // kernel of their own so that the plain split keeps its registers.
+// Routes token t in wave 0 (as k_route_topk does from the router partials) and
+// takes list indexes for its slots by atomic adds on counts; returns the logical
+// rows of its slots as route_rows does.
+__device__ __forceinline__ uint32_t route_self(const SplitArgs &a, uint32_t t, uint32_t (&L)[4])
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    __shared__ uint32_t ids[4], pos[4];
+    if (tid < 64) { // wave 0
+        Route r;
+        r.logits = nullptr;
+        r.bias = a.rbias;
+        r.n_expert = a.n_expert;
+        r.n_used = a.n_used;
+        r.sel_out = nullptr;
+        const uint32_t e = min(lane, a.n_expert - 1);
+        float dp[8], sp[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint32_t bb = min((uint32_t)b, a.nparts - 1);
+            dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
+            sp[b] = a.rss[(size_t)t * a.nparts + bb];
+        }
+        float dot = 0.f, ss = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            if (b < (int)a.nparts) {
+                dot = b == 0 ? dp[b] : dot + dp[b];
+                ss = b == 0 ? sp[b] : ss + sp[b];
+            }
+        const RouteIn in{dot / sqrtf(ss / (float)a.K + a.eps), a.rbias ? a.rbias[e] : 0.f};
+        const Routed rt = wave_route(r, in);
+        if (lane < 4) {
+            const uint32_t id = rt.id(lane);
+            a.sel_out[(size_t)t * 4 + lane] = id;
+            a.wsel_out[(size_t)t * 4 + lane] = lane < a.n_used ? rt.w(lane) : 0.f;
+            ids[lane] = id;
+            if (lane < a.n_used) {
+                const uint32_t pr = atomicAdd(&a.counts[id], 1u);
+                pos[lane] = pr;
+                a.tok[(size_t)id * a.list_stride + pr] = t;
+                a.slot[(size_t)id * a.list_stride + pr] = t * 4 + lane;
+                a.pos[(size_t)t * 4 + lane] = pr;
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (r < (int)a.n_used)
+            L[r] = ids[r] * a.rpe + pos[r];
+    return a.n_used;
+}
+
 template <bool NORM, bool EXT>
 __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
 {
@@ -298,7 +351,9 @@ __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
     if (EXT && a.cpart) // uniform
         combine_pieces(a, t, v);
     uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
-    if (EXT && a.mode == SPLIT_GROUPED && a.tok) { // uniform
+    if (EXT && a.mode == SPLIT_GROUPED && a.tok && a.rpart) { // uniform
+        nl = route_self(a, t, L);
+    } else if (EXT && a.mode == SPLIT_GROUPED && a.tok) { // uniform
         nl = route_rows(a, t, L);
     } else if (a.mode == SPLIT_GROUPED) { // uniform
         nl = 0;
@@ -1321,6 +1376,8 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_gemm_reduce(const Gem
         slice_sums<1>(a.part + at, slice, a.ksplit, {0}, v);
         const float xn = a.mode ? old + v[0] : v[0];
         *out = xn;
+        if (a.counts && blockIdx.x == 0 && orow == 0 && threadIdx.x < a.n_expert)
+            a.counts[threadIdx.x] = 0;
         router_partials(a, rr, xn);
         return;
     }
