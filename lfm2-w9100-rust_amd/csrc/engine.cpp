@@ -108,7 +108,7 @@ struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, split_rows_ext, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
-        tile_pack;
+        tile_pack, gemm_q6_n64;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f;
     Shape matvec, conv, qkv, gateup, head;
@@ -240,7 +240,8 @@ static int get_kernels(Kernels **out)
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
                 {&k->gemm_q6_t32n1, "k_gemm_q6_t32n1"},
                 {&k->attn_merge_split, "k_attn_merge_split"}, {&k->reduce_combine, "k_reduce_combine"}, {&k->router_small, "k_router_prefill_small"},
-                {&k->embed_rows, "k_embed_rows"}, {&k->tile_pack, "k_q6_tile_pack"}};
+                {&k->embed_rows, "k_embed_rows"}, {&k->tile_pack, "k_q6_tile_pack"},
+                {&k->gemm_q6_n64, "k_gemm_q6_n64"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
         if (e != hipSuccess) {
@@ -589,6 +590,7 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 }
 
 #define GEMM_PART_BYTES ((size_t)64 << 20) // split-K partial sums (prefill scratch)
+#define GEMM_N64_BELOW 512u // two 128-token workgroups per CU on 256 CUs
 
 // Launches the matrix-core GEMM g (pair: gate + up + SwiGLU) over T tokens and nz
 // groups.  Up to one 128-token tile (T <= 128, as in 64-token chunked prefill,
@@ -623,7 +625,13 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     const bool small = T <= GEMM_TOKENS;
     // small ungrouped projections of up to 2048 rows: one 32-row tile per wave
     const bool one_tile = small && !pair && nz == 1 && g.zrows <= 2048;
-    dim3 grid = gemm_grid(g.zrows, T, nz, pair || one_tile ? GEMM_ROWS / 2 : GEMM_ROWS, small ? 32 : GEMM_TOKENS);
+    // large single-weight calls whose 128-token grid would not give each CU two
+    // workgroups (few row tiles: the 2048- and 3072-row projections) take 64 tokens
+    // per workgroup
+    const dim3 g128 = gemm_grid(g.zrows, T, nz, GEMM_ROWS, GEMM_TOKENS);
+    const bool n64 = !small && !pair && (uint64_t)g128.x * g128.y * g128.z < GEMM_N64_BELOW;
+    dim3 grid = gemm_grid(g.zrows, T, nz, pair || one_tile ? GEMM_ROWS / 2 : GEMM_ROWS,
+                          small ? 32 : n64 ? GEMM_TOKENS / 2 : GEMM_TOKENS);
     uint32_t S = 1;
     if (part && small) {
         const uint32_t wgs = grid.x * grid.y * grid.z;
@@ -632,7 +640,7 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, part_cap / per));
     }
     hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
-                            : (pair ? K->gemm_swiglu : K->gemm_q6);
+                            : (pair ? K->gemm_swiglu : n64 ? K->gemm_q6_n64 : K->gemm_q6);
     if (deferred)
         *deferred = S;
     if (S == 1) {

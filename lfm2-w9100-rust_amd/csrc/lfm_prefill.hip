@@ -971,6 +971,14 @@ k_gemm_q6(const GemmArgs a)
     gemm_body<false, 4>(a);
 }
 
+// 64 token columns per workgroup: for projections whose 128-column grid would leave
+// CUs without a second workgroup (few row tiles)
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6_n64(const GemmArgs a)
+{
+    gemm_body<false, 2>(a);
+}
+
 extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 k_gemm_q6_swiglu(const GemmArgs a)
 {

@@ -105,14 +105,16 @@ def test_argmax_cases(gpu, oracle):
 @pytest.mark.parametrize("rows,in_dim,T", [(6144, 2048, 200), (130, 256, 7), (1792, 2048, 129),
                                            (2048, 7168, 64), (256, 1792, 1), (2048, 2048, 31),
                                            (512, 1024, 32), (6144, 2048, 33), (1792, 2048, 128),
-                                           (1000, 512, 150), (1000, 512, 40)])
+                                           (1000, 512, 150), (1000, 512, 40), (8192, 256, 2048)])
 def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
     """Matrix-core GEMM (binary16 sc*(q-32) weights, hi/lo activations, fp32 d
     scaling) against the f64 q6k_matvec oracle per token: rel-L2 <= 1e-5.  Calls
     of up to 128 tokens read token-blocked activations (32-row tiles), so the
     tokens on either side of a tile edge are checked too.  The weights are read
     from a copy in 32-row tiles whose rows past the matrix are zero: 130 and
-    1000 rows end inside a tile, with both the 128-token and the 32-token tiles."""
+    1000 rows end inside a tile, with both the large-call and the 32-token tiles.
+    Large calls run 64-token tiles when 128-token ones would make fewer than 512
+    workgroups: 8192 rows x 2048 tokens is the case that runs the 128-token tiles."""
     raw = blocks(rows * in_dim // 256, rows * 7 + T).reshape(-1)
     rng = np.random.default_rng(T)
     x = rng.standard_normal((T, in_dim)).astype(np.float32)
@@ -205,7 +207,8 @@ def test_gemm_prefill_weights_exact(gpu, oracle, T, k0):
     so y[t][r] is weight (r, k0 + t) times 1 with nothing else added, and must
     equal binary16(sc (q - 32)) rounded to nearest even (exact up to magnitude
     2048).  The encoding is checked against the oracle's dequant first.  T = 256
-    runs the 128-token tiles, T <= 128 the 32-token tiles."""
+    runs the large-call kernel (64-token tiles at this size), T <= 128 the 32-token
+    tiles."""
     rows, in_dim = 256, 256
     k = np.arange(in_dim)
     codes = (k[None, :] + np.arange(rows)[:, None]) % 64
