@@ -636,7 +636,10 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     if (part && small) {
         const uint32_t wgs = grid.x * grid.y * grid.z;
         const size_t per = (size_t)(pair ? 2 : 1) * part_rows * g.zrows;
-        S = std::min<uint32_t>(std::max<uint32_t>(1, 1024 / wgs), g.w.nb);
+        // single weights of more than 4096 rows (the 6144-row in_proj) aim at 192: their
+        // partial sums (slices x T x rows floats) cost more than the wider grid gains
+        const uint32_t target = nz == 1 && !pair && g.zrows > 4096 ? 192 : 1024;
+        S = std::min<uint32_t>(std::max<uint32_t>(1, target / wgs), g.w.nb);
         S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, part_cap / per));
     }
     hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
