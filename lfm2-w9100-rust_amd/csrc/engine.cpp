@@ -590,6 +590,7 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 }
 
 #define GEMM_PART_BYTES ((size_t)64 << 20) // split-K partial sums (prefill scratch)
+#define GEMM_PART_SOFT ((size_t)1600000) // small calls' partial sums, floats (6.4 MB)
 #define GEMM_N64_BELOW 512u // two 128-token workgroups per CU on 256 CUs
 
 // Launches the matrix-core GEMM g (pair: gate + up + SwiGLU) over T tokens and nz
@@ -597,7 +598,8 @@ static dim3 gemm_grid(uint32_t rows, uint32_t ntok, uint32_t nz, uint32_t rows_p
 // about 8 tokens per expert) the kernels with 32-token tiles run, the grid is
 // then mostly the weight-row tiles and each workgroup's K loop is a chain of
 // dependent stages, so K is split into slices (about 1024 workgroups, each slice
-// at least one Q6_K block, the partials within `part_cap` floats of `part`) and
+// at least one Q6_K block, the partials within `part_cap` floats of `part` and
+// within GEMM_PART_SOFT floats) and
 // k_gemm_reduce adds the slices in order.  part_rows: output rows the GEMM can
 // write (T, or 4T for expert slots); n_used: ranks per token of the expert slots.
 // `deferred` (ungrouped, non-pair calls): with a K split the reduce is left to the
@@ -636,11 +638,11 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     if (part && small) {
         const uint32_t wgs = grid.x * grid.y * grid.z;
         const size_t per = (size_t)(pair ? 2 : 1) * part_rows * g.zrows;
-        // single weights of more than 4096 rows (the 6144-row in_proj) aim at 192: their
-        // partial sums (slices x T x rows floats) cost more than the wider grid gains
-        const uint32_t target = nz == 1 && !pair && g.zrows > 4096 ? 192 : 1024;
-        S = std::min<uint32_t>(std::max<uint32_t>(1, target / wgs), g.w.nb);
-        S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, part_cap / per));
+        S = std::min<uint32_t>(std::max<uint32_t>(1, 1024 / wgs), g.w.nb);
+        // and at most GEMM_PART_SOFT floats of partial sums: past that, writing and
+        // adding them costs more than the wider grid gains (the 6144-row in_proj at
+        // four slices, the dense gate/up pair unsplit, the dense down at twelve)
+        S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, std::min<size_t>(part_cap, GEMM_PART_SOFT) / per));
     }
     hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
                             : (pair ? K->gemm_swiglu : n64 ? K->gemm_q6_n64 : K->gemm_q6);
