@@ -625,8 +625,9 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     if (combined)
         *combined = false;
     const bool small = T <= GEMM_TOKENS;
-    // small ungrouped projections of up to 2048 rows: one 32-row tile per wave
-    const bool one_tile = small && !pair && nz == 1 && g.zrows <= 2048;
+    // small ungrouped projections of up to 3072 rows (q/k/v, the out projections):
+    // one 32-row tile per wave
+    const bool one_tile = small && !pair && nz == 1 && g.zrows <= 3072;
     // large single-weight calls whose 128-token grid would not give each CU two
     // workgroups (few row tiles: the 2048- and 3072-row projections) take 64 tokens
     // per workgroup

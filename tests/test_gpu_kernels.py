@@ -105,7 +105,8 @@ def test_argmax_cases(gpu, oracle):
 @pytest.mark.parametrize("rows,in_dim,T", [(6144, 2048, 200), (130, 256, 7), (1792, 2048, 129),
                                            (2048, 7168, 64), (256, 1792, 1), (2048, 2048, 31),
                                            (512, 1024, 32), (6144, 2048, 33), (1792, 2048, 128),
-                                           (1000, 512, 150), (1000, 512, 40), (8192, 256, 2048)])
+                                           (1000, 512, 150), (1000, 512, 40), (8192, 256, 2048),
+                                           (3072, 2048, 64), (3200, 512, 64)])
 def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
     """Matrix-core GEMM (binary16 sc*(q-32) weights, hi/lo activations, fp32 d
     scaling) against the f64 q6k_matvec oracle per token: rel-L2 <= 1e-5.  Calls
@@ -114,7 +115,9 @@ def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
     from a copy in 32-row tiles whose rows past the matrix are zero: 130 and
     1000 rows end inside a tile, with both the large-call and the 32-token tiles.
     Large calls run 64-token tiles when 128-token ones would make fewer than 512
-    workgroups: 8192 rows x 2048 tokens is the case that runs the 128-token tiles."""
+    workgroups: 8192 rows x 2048 tokens is the case that runs the 128-token tiles.
+    Small calls of up to 3072 rows run one 32-row tile per wave (3072 rows), wider
+    ones two (3200)."""
     raw = blocks(rows * in_dim // 256, rows * 7 + T).reshape(-1)
     rng = np.random.default_rng(T)
     x = rng.standard_normal((T, in_dim)).astype(np.float32)
