@@ -153,3 +153,34 @@ def test_prefill_chunks_repeat_bit_exact(gpu, real_width):
         outs.append((lg.view(np.uint32).copy(), np.frombuffer(g.snapshot_resident_cache(192), np.uint32).copy()))
     assert np.array_equal(outs[0][0], outs[1][0])
     assert np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_prefill_mixed_chunk_sizes(gpu, oracle, real_width):
+    """One prompt in calls of 1, 127, 128, 129, 3 and 92 tokens: both sides of the
+    128-token line between the split-K small-call GEMMs (one 32-row tile per wave up
+    to 3072 rows, partial sums capped) and the large-call ones (64-token tiles for
+    grids under 512 workgroups, which every projection here is), each call reading
+    the KV and conv state the previous ones left.  The last logits and the resident
+    state match the oracle's token-by-token forward and the engine's whole-prompt
+    call."""
+    hp, tensors = real_width
+    sizes = [1, 127, 128, 129, 3, 92]
+    n = sum(sizes)
+    prompt = [int(t) for t in np.random.default_rng(23).integers(0, hp.vocab, n)]
+    g = gpu_engine(hp, tensors, ctx=512)
+    s = 0
+    for c in sizes:
+        lg = g.forward(prompt[s:s + c], s)
+        s += c
+    o = oracle_engine(oracle, hp, tensors, ctx=512)
+    lo = o.forward(prompt, 0)
+    err = rel_l2(lg, lo)
+    sg = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    so = np.frombuffer(o.snapshot(n), np.float32)
+    serr = rel_l2(sg, so)
+    print(f"mixed chunks {sizes}: logits rel-L2 {err:.3e}, state rel-L2 {serr:.3e}")
+    assert err <= 1e-3
+    assert serr <= 1e-3
+    w = gpu_engine(hp, tensors, ctx=512)
+    lw = w.forward(prompt, 0)
+    assert rel_l2(lg, lw) <= 1e-3
