@@ -432,6 +432,9 @@ def main():
             f"{extra['q6k_matvec_6144x2048']['hbm_gbs']:.0f} GB/s (HBM, 64 rotating copies), "
             f"{extra['q6k_matvec_6144x2048']['cache_resident_gbs']:.0f} GB/s cache-resident")
 
+    # the engine is released here, while the runtime (and a tracer attached to
+    # it) is up, not by its finalizer at interpreter exit
+    eng.close()
     cpu = None
     if not args.no_cpu_baseline:
         log(f"[bench] cpu baseline (oracle) on {cores} threads ...")

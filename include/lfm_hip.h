@@ -156,6 +156,31 @@ int lfm_engine_run_layer(lfm_engine *e, uint32_t layer, float *x, uint32_t pos, 
  * decode step (32 experts, dim 2048), else 0. */
 int lfm_engine_fused_router(const lfm_engine *e, uint32_t layer, int *fused);
 
+/* ---- routing audit (parity tests; no counterpart in the reference) ---------
+ * The routing the reference records per layer and token (lfm.rs:613-637) as
+ * the GPU computed it, so tests compare expert selections and their margins
+ * with the oracle decision by decision.
+ * lfm_engine_route_records copies the decode step's routing records, 144
+ * words per layer (n_layers * 144 words; layer l at l * 144): ids[8], then
+ * weights[8] (float bits), then the router logits [16 + e] and the selection
+ * scores p + bias the kernel ranked the experts by [80 + e] (float bits), for
+ * e < n_expert.  Each decode step (lfm_forward_* of one token, lfm_decode_run,
+ * lfm_engine_run_layer / _run_ffn) rewrites the records of the MoE layers it
+ * runs; dense layers stay zero. */
+int lfm_engine_route_records(lfm_engine *e, uint32_t *words, size_t cap_words);
+/* on = 1 makes every later multi-token (matrix-core) forward keep its routing:
+ * per MoE layer and token row, ids[4], weights[4] and the router logits
+ * [n_expert] the selection was made from.  The first enable allocates the log
+ * on the device (n_layers * ctx * (32 + 4 * n_expert) bytes).
+ * lfm_engine_prefill_routes returns layer `layer`'s log of the last such call:
+ * token rows *first .. *first + *n - 1 (the last layer routes only the last
+ * row), ids[*n][4], w[*n][4] and, when *has_logits, logits[*n][n_expert]
+ * (logits may be NULL).  LFM_ESTATE while the log was never enabled. */
+int lfm_engine_set_route_log(lfm_engine *e, int on);
+int lfm_engine_prefill_routes(lfm_engine *e, uint32_t layer, uint32_t *first, uint32_t *n,
+                              int *has_logits, uint32_t *ids, float *w, float *logits,
+                              size_t cap_rows);
+
 /* Mean duration of the routed MoE gate/up kernel (the largest share of a decode
  * step), timed with HIP events over one graph of `reps` rounds across every MoE
  * layer's routed experts; *bytes_per_launch = its algorithmic HBM bytes. */
@@ -210,7 +235,13 @@ int lfm_copy_time(uint64_t bytes, uint32_t reps, float *us_per_copy);
  * the multi-token q6k_prompt path of engine/src/ops.rs:350-373.  in_dim is a
  * multiple of 256 up to 8192 and (T + 31) * in_dim * 2 bytes stays below 2 GiB
  * (the kernels address the binary16 activation copies with 32-bit offsets);
- * LFM_EINVAL otherwise. */
+ * LFM_EINVAL otherwise.  This op-level entry point builds its scratch on every
+ * call: it allocates the binary16 activation copies, the split-K partial sums
+ * (T <= 128) and a 32-row tile copy of the weight (ceil(rows / 32) * in_dim /
+ * 256 * 6720 bytes), runs the tile pack kernel, waits for `stream` and frees
+ * them, so a caller that loops over it pays for the allocations and the repack
+ * each time.  The engine's prefill keeps its
+ * tile copies from lfm_engine_finalize and never repacks. */
 int lfm_q6k_gemm(const void *packed_dev, uint64_t rows, uint64_t in_dim, const float *x_dev,
                  uint32_t T, float *y_dev, void *stream);
 

@@ -580,6 +580,7 @@ extern "C" int lfm_q6k_matvec_time(const void *packed, uint32_t ncopies, uint64_
 }
 
 // ------------------------------------------------------------------ MFMA GEMM
+#define DECODE_WINDOW 32u // lfm_decode_run: replays per window (two windows queued at most)
 #define GEMM_ROWS 256   // weight rows per GEMM workgroup
 #define GEMM_TOKENS 128 // token columns per GEMM workgroup
 #define GEMM_THREADS 256 // 4 waves of 64 weight rows each
@@ -828,7 +829,18 @@ struct lfm_engine {
     std::string devname;
 
     DevState *st = nullptr;
-    uint32_t *ids = nullptr, *out_tokens = nullptr, *sel = nullptr;
+    uint32_t *ids = nullptr, *out_tokens = nullptr;
+    uint32_t *sel = nullptr;        // routing records, ROUTE_REC_WORDS per layer
+    uint32_t last_route_layer = 0;  // the MoE layer whose record was enqueued last
+    // prefill routing log (lfm_engine_set_route_log): per layer and prompt
+    // position of the last multi-token call, ids[4] and weights[4], plus the
+    // router logits [n_expert] where the call computed them (calls over
+    // GEMM_TOKENS tokens); log_first[l] / log_n[l] give the token rows logged
+    bool route_log = false;
+    uint32_t *log_ids = nullptr;
+    float *log_w = nullptr, *log_logits = nullptr;
+    std::vector<uint32_t> log_first, log_n;
+    std::vector<uint8_t> log_has_logits;
     float *x = nullptr, *y = nullptr, *qkv = nullptr, *sw = nullptr, *rlogits = nullptr,
           *logits = nullptr, *hpart = nullptr, *apart = nullptr;
     float *rpart = nullptr; // fused router expert partial sums [ROUTE_QUADS][ROUTE_PARTS] float4
@@ -864,6 +876,7 @@ struct lfm_engine {
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
     hipGraphExec_t g_layers = nullptr, g_decode = nullptr;
+    hipEvent_t win_ev[2] = {nullptr, nullptr}; // lfm_decode_run's replay window
     uint64_t nodes_layers = 0, nodes_decode = 0;
     uint64_t dispatches = 0;
     bool stepwise_prefill = false; // true: prompts run as one decode step per token
@@ -1208,7 +1221,7 @@ static GateUpArgs moe_gateup_args(lfm_engine *e, uint32_t l)
     g.route.bias = f32(e, "blk.%u.exp_probs_b.bias", l);
     g.route.n_expert = hp.n_expert;
     g.route.n_used = hp.n_used;
-    g.route.sel_out = e->sel;
+    g.route.sel_out = e->sel + (size_t)l * ROUTE_REC_WORDS;
     g.wg = q6(e, "blk.%u.ffn_gate_exps.weight", l);
     g.wu = q6(e, "blk.%u.ffn_up_exps.weight", l);
     g.ff = hp.expert_ff;
@@ -1268,7 +1281,8 @@ static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
     d.wd = q6(e, "blk.%u.ffn_down_exps.weight", l);
     d.sw = e->sw;
     d.route = route;
-    d.route.sel_out = e->sel; // routing stored by the gate/up kernel
+    d.route.sel_out = g.route.sel_out; // the routing record stored by the gate/up kernel
+    e->last_route_layer = l;
     d.x = e->x;
     d.dim = dim;
     d.ff = hp.expert_ff;
@@ -1402,8 +1416,8 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMemset(e->st, 0, sizeof(DevState)));
     HIPCHK(hipMalloc(&e->ids, e->ctx * 4));
     HIPCHK(hipMalloc(&e->out_tokens, e->ctx * 4));
-    HIPCHK(hipMalloc(&e->sel, 16 * 4));
-    HIPCHK(hipMemset(e->sel, 0, 16 * 4));
+    HIPCHK(hipMalloc(&e->sel, (size_t)hp.n_layers * ROUTE_REC_WORDS * 4));
+    HIPCHK(hipMemset(e->sel, 0, (size_t)hp.n_layers * ROUTE_REC_WORDS * 4));
     HIPCHK(hipMalloc(&e->x, dim * 4));
     HIPCHK(hipMalloc(&e->y, dim * 4));
     HIPCHK(hipMalloc(&e->qkv, (dim + 2 * max_hdkv) * 4));
@@ -1443,7 +1457,11 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         e->qkvw[l] = q6view(dst, rows, (uint64_t)nb * 256);
     }
     // The prefill GEMMs read their weights from 32-row tile copies (one contiguous
-    // 1 KB / 512 B stretch per wave and load instead of 32 rows' pieces).
+    // 1 KB / 512 B stretch per wave and load instead of 32 rows' pieces).  The
+    // uploads and the qkv concatenation above are null-stream copies from pageable
+    // memory, which may still be in flight when hipMemcpy returns and are not
+    // ordered with the engine's non-blocking stream: finish them first.
+    HIPCHK(hipDeviceSynchronize());
     e->qkvtdev.assign(hp.n_layers, nullptr);
     e->qkvt.assign(hp.n_layers, Q6Tiles{});
     for (uint32_t l = 0; l < hp.n_layers; ++l)
@@ -1518,6 +1536,8 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipDeviceSynchronize());
     RC(capture(e, false, &e->g_layers, &e->nodes_layers));
     RC(capture(e, true, &e->g_decode, &e->nodes_decode));
+    for (hipEvent_t &ev : e->win_ev)
+        HIPCHK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     e->finalized = true;
     return LFM_OK;
 }
@@ -1533,6 +1553,9 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
         (void)hipGraphExecDestroy(e->g_layers);
     if (e->g_decode)
         (void)hipGraphExecDestroy(e->g_decode);
+    for (hipEvent_t ev : e->win_ev)
+        if (ev)
+            (void)hipEventDestroy(ev);
     for (auto &kv : e->tensors) {
         (void)hipFree(kv.second.dev);
         if (kv.second.tdev)
@@ -1543,7 +1566,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (void *p : e->qkvtdev)
         if (p)
             (void)hipFree(p);
-    void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->x, e->y, e->qkv, e->sw,
+    void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->log_ids, e->log_w, e->log_logits, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
@@ -1633,6 +1656,7 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
             a.rbias = route->bias;
             a.sel_out = route->sel;
             a.wsel_out = route->wsel;
+            a.logit_out = e->route_log ? e->pf.logits : nullptr;
             a.nparts = route->nparts;
         }
     }
@@ -1797,6 +1821,23 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
 }
 
 // FFN over T rows starting at x (the last layer runs only the last row).
+// Prefill routing log: the routing of token rows first .. first + n - 1 at MoE
+// layer l (and their router logits when the call computed them).
+static int log_routes(lfm_engine *e, uint32_t l, uint32_t first, uint32_t n, bool logits)
+{
+    const uint32_t E = e->hp.n_expert;
+    const size_t row = (size_t)l * e->ctx + first;
+    HIPCHK(hipMemcpyAsync(e->log_ids + row * 4, e->pf.sel, (size_t)n * 16, hipMemcpyDeviceToDevice, e->stream));
+    HIPCHK(hipMemcpyAsync(e->log_w + row * 4, e->pf.wsel, (size_t)n * 16, hipMemcpyDeviceToDevice, e->stream));
+    if (logits)
+        HIPCHK(hipMemcpyAsync(e->log_logits + row * E, e->pf.logits, (size_t)n * E * 4, hipMemcpyDeviceToDevice,
+                              e->stream));
+    e->log_first[l] = first;
+    e->log_n[l] = n;
+    e->log_has_logits[l] = logits ? 1 : 0;
+    return LFM_OK;
+}
+
 // defer_ok: a split of the same rows follows (another layer), which may apply
 // the MoE combine.
 static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok)
@@ -1836,7 +1877,9 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
     // with the out projection's router partials (and counts zeroed by its reduce) it
     // routes each token too (no k_route_topk)
     const bool small = T <= GEMM_TOKENS;
-    const bool self_route = small && e->pf.router_ready && rg.nparts <= 8;
+    const bool self_route = small && e->pf.router_ready;
+    if (self_route && rg.nparts > 8) // dim <= 2048 (validate_hparams): at most 8 partials
+        return fail(LFM_EINTERNAL, "prefill router: %u partial sums per token > 8", rg.nparts);
     if (!self_route) {
         RC(launch(e->K->route_topk, dim3((T + 3) / 4), 0, e->stream, rg));
         e->dispatches += 1;
@@ -1846,6 +1889,8 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         e->dispatches += 1;
     }
     RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, small, self_route ? &rg : nullptr));
+    if (e->route_log) // the call's routing is final here (ids, weights, logits)
+        RC(log_routes(e, l, (uint32_t)((x - e->pf.x) / dim), T, true));
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
     RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
@@ -1873,6 +1918,8 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
 static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
 {
     const lfm_hparams &hp = e->hp;
+    if (e->route_log)
+        std::fill(e->log_n.begin(), e->log_n.end(), 0u);
     e->pf.comb_pending = false;
     EmbedRowsArgs em{q6(e, "token_embd.weight"), e->ids, e->pf.x, T};
     RC(launch(e->K->embed_rows, dim3((T + 3) / 4), 0, e->stream, em));
@@ -2000,7 +2047,17 @@ extern "C" int lfm_decode_run(lfm_engine *e, uint32_t first, uint32_t start, uin
     if (first >= e->hp.vocab)
         return fail(LFM_ERANGE, "token out of range: %u >= vocab %u", first, e->hp.vocab);
     RC(set_state(e, first, start, 0, eos));
+    // At most 2 * DECODE_WINDOW replays are queued at once: before the replays
+    // of window w the host waits for the event recorded after window w - 2.
+    // The device stays fed (a whole window is still queued), and a caller or
+    // tool that tracks every queued launch sees a bounded number of them.
     for (uint32_t s = 0; s < steps; ++s) {
+        if (s % DECODE_WINDOW == 0 && s > 0) {
+            hipEvent_t ev = e->win_ev[(s / DECODE_WINDOW) & 1];
+            if (s >= 2 * DECODE_WINDOW)
+                HIPCHK(hipEventSynchronize(ev));
+            HIPCHK(hipEventRecord(ev, e->stream));
+        }
         HIPCHK(hipGraphLaunch(e->g_decode, e->stream));
         e->dispatches += e->nodes_decode;
     }
@@ -2361,10 +2418,69 @@ extern "C" int lfm_engine_last_route(lfm_engine *e, uint32_t *ids, float *w, uin
         return fail(LFM_ERANGE, "route buffers hold %u < %u entries", cap, e->hp.n_used);
     uint32_t h[16];
     HIPCHK(hipStreamSynchronize(e->stream));
-    HIPCHK(hipMemcpy(h, e->sel, sizeof(h), hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(h, e->sel + (size_t)e->last_route_layer * ROUTE_REC_WORDS, sizeof(h),
+                     hipMemcpyDeviceToHost));
     for (uint32_t r = 0; r < e->hp.n_used; ++r) {
         ids[r] = h[r];
         memcpy(&w[r], &h[8 + r], 4);
+    }
+    return LFM_OK;
+}
+
+// The decode step's routing records, one per layer (zero for dense layers and
+// layers not run since finalize).
+extern "C" int lfm_engine_route_records(lfm_engine *e, uint32_t *words, size_t cap_words)
+{
+    RC(need_final(e));
+    const size_t n = (size_t)e->hp.n_layers * ROUTE_REC_WORDS;
+    if (!words || cap_words < n)
+        return fail(LFM_ERANGE, "route record buffer holds %zu < %zu words", cap_words, n);
+    HIPCHK(hipStreamSynchronize(e->stream));
+    HIPCHK(hipMemcpy(words, e->sel, n * 4, hipMemcpyDeviceToHost));
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_set_route_log(lfm_engine *e, int on)
+{
+    RC(need_final(e));
+    if (on && !e->log_ids) {
+        const size_t rows = (size_t)e->hp.n_layers * e->ctx;
+        HIPCHK(hipMalloc(&e->log_ids, rows * 16));
+        HIPCHK(hipMalloc(&e->log_w, rows * 16));
+        HIPCHK(hipMalloc(&e->log_logits, rows * e->hp.n_expert * 4));
+        e->log_first.assign(e->hp.n_layers, 0u);
+        e->log_n.assign(e->hp.n_layers, 0u);
+        e->log_has_logits.assign(e->hp.n_layers, 0);
+    }
+    e->route_log = on != 0;
+    return LFM_OK;
+}
+
+extern "C" int lfm_engine_prefill_routes(lfm_engine *e, uint32_t layer, uint32_t *first, uint32_t *n,
+                                         int *has_logits, uint32_t *ids, float *w, float *logits,
+                                         size_t cap_rows)
+{
+    RC(need_final(e));
+    if (!e->log_ids)
+        return fail(LFM_ESTATE, "routing log is off (lfm_engine_set_route_log)");
+    if (layer >= e->hp.n_layers)
+        return fail(LFM_ERANGE, "layer %u >= %u", layer, e->hp.n_layers);
+    if (!first || !n || !has_logits || !ids || !w)
+        return fail(LFM_EINVAL, "null argument");
+    const uint32_t cnt = e->log_n[layer];
+    if (cap_rows < cnt)
+        return fail(LFM_ERANGE, "buffers hold %zu < %u rows", cap_rows, cnt);
+    *first = e->log_first[layer];
+    *n = cnt;
+    *has_logits = e->log_has_logits[layer];
+    HIPCHK(hipStreamSynchronize(e->stream));
+    const size_t row = (size_t)layer * e->ctx + *first;
+    if (cnt) {
+        HIPCHK(hipMemcpy(ids, e->log_ids + row * 4, (size_t)cnt * 16, hipMemcpyDeviceToHost));
+        HIPCHK(hipMemcpy(w, e->log_w + row * 4, (size_t)cnt * 16, hipMemcpyDeviceToHost));
+        if (*has_logits && logits)
+            HIPCHK(hipMemcpy(logits, e->log_logits + row * e->hp.n_expert, (size_t)cnt * e->hp.n_expert * 4,
+                             hipMemcpyDeviceToHost));
     }
     return LFM_OK;
 }

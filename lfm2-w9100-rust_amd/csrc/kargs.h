@@ -105,11 +105,20 @@ struct Route {
     const float *logits; // nullptr = dense layer (or the fused router below)
     const float *bias;
     uint32_t n_expert, n_used;
-    uint32_t *sel_out;   // written by one wave: ids[8] then weights[8] (float bits)
+    uint32_t *sel_out;   // routing record of the layer (ROUTE_REC_WORDS, see below), one wave writes it
     const float *rpart;  // fused router: expert partial sums, [ROUTE_QUADS][ROUTE_PARTS] float4
     const float *rss;    // fused router: partial sums of x_new^2 [ROUTE_PARTS]
     const float *xw;     // fused router: x_new * w_norm, the FFN's input before 1/rms [width]
 };
+
+// Routing record of one MoE layer in the decode step, written by the gate/up
+// kernel and read by the down projection: ids[8], weights[8] (float bits, the
+// normalized picks), then per expert e < n_expert the router logit at
+// [ROUTE_REC_LOGITS + e] and the selection score p + bias it was ranked by at
+// [ROUTE_REC_SCORES + e] (float bits).  The step keeps one record per layer.
+#define ROUTE_REC_LOGITS 16
+#define ROUTE_REC_SCORES 80
+#define ROUTE_REC_WORDS 144
 
 // Fused router (the model's 32 experts at width 2048): the output projection
 // before the FFN runs ROUTE_PARTS workgroups of ROUTE_ROWS rows; each leaves
@@ -241,6 +250,7 @@ struct SplitArgs {
     const float *rpart, *rss, *rbias;
     uint32_t *sel_out;
     float *wsel_out;
+    float *logit_out;    // nullable: the router logits [T][n_expert] (routing log)
     uint32_t nparts;
     // nullable (small calls): before the split, row t of x first gets the down
     // projection's ranks combined into it as k_reduce_combine does (x += sum_r
@@ -386,7 +396,7 @@ struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)
 };
 
 struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token, rank) list
-    const float *logits, *bias;  // logits [T][n_expert] (k_route_topk: unless rpart is set)
+    const float *logits, *bias;  // logits [T][n_expert] (read by k_route_topk)
     uint32_t *sel;        // [T][4] ids
     float *wsel;          // [T][4] weights
     uint32_t *counts;     // [n_expert]
@@ -394,8 +404,8 @@ struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token
     uint32_t *slot;       // [n_expert][list_stride] slot = t*4 + rank
     uint32_t T, n_expert, n_used, list_stride;
     uint32_t *pos;        // [T*4]: index of slot t*4 + rank in its expert's list
-    // k_route_topk with rpart set: logit = (sum_b rpart[t][b][e]) / sqrt((sum_b rss[t][b]) / dim + eps),
-    // b < nparts in order (the router partials of the preceding reduce)
+    // the router partials of the preceding reduce (rpart[t][b][e], rss[t][b], b < nparts),
+    // handed to the grouped split that routes each token itself; k_route_topk never reads them
     const float *rpart, *rss;
     uint32_t nparts, dim;
     float eps;

@@ -1033,6 +1033,11 @@ __device__ __forceinline__ void gateup_body(const GateUpArgs &a)
                 a.route.sel_out[lane] = lane < 4 ? rw.id(lane) : 0u;
                 a.route.sel_out[8 + lane] = lane < 4 ? __float_as_uint(rw.w(lane)) : 0u;
             }
+            // the record's logits and the scores the picks were ranked by
+            if (lane < a.route.n_expert) {
+                a.route.sel_out[ROUTE_REC_LOGITS + lane] = __float_as_uint(rin.lg);
+                a.route.sel_out[ROUTE_REC_SCORES + lane] = __float_as_uint(route_score(rin));
+            }
         }
         if (halted)
             return;

@@ -299,6 +299,8 @@ __device__ __forceinline__ uint32_t route_self(const SplitArgs &a, uint32_t t, u
             }
         const RouteIn in{dot / sqrtf(ss / (float)a.K + a.eps), a.rbias ? a.rbias[e] : 0.f};
         const Routed rt = wave_route(r, in);
+        if (a.logit_out && lane < a.n_expert)
+            a.logit_out[(size_t)t * a.n_expert + lane] = in.lg;
         if (lane < 4) {
             const uint32_t id = rt.id(lane);
             a.sel_out[(size_t)t * 4 + lane] = id;
@@ -1886,38 +1888,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_topk(const Rout
     r.n_expert = a.n_expert;
     r.n_used = a.n_used;
     r.sel_out = nullptr;
-    Routed rt;
-    if (a.rpart) { // uniform: logits from the preceding reduce's router partials
-        const uint32_t e = min(lane, a.n_expert - 1);
-        float dp[8], sp[8];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const uint32_t bb = min((uint32_t)b, a.nparts - 1);
-            dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
-            sp[b] = a.rss[(size_t)t * a.nparts + bb];
-        }
-        float dot = 0.f, ss = 0.f;
-        for (uint32_t b0 = 0; b0 < a.nparts; b0 += 8) { // uniform; nparts <= 8 in one pass
-            if (b0 > 0) {
-#pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const uint32_t bb = min(b0 + b, a.nparts - 1);
-                    dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
-                    sp[b] = a.rss[(size_t)t * a.nparts + bb];
-                }
-            }
-#pragma unroll
-            for (int b = 0; b < 8; ++b)
-                if (b0 + b < a.nparts) {
-                    dot = b0 + b == 0 ? dp[b] : dot + dp[b];
-                    ss = b0 + b == 0 ? sp[b] : ss + sp[b];
-                }
-        }
-        const RouteIn in{dot / sqrtf(ss / (float)a.dim + a.eps), a.bias ? a.bias[e] : 0.f};
-        rt = wave_route(r, in);
-    } else {
-        rt = wave_route(r);
-    }
+    const Routed rt = wave_route(r);
     if (lane < 4) {
         a.sel[(size_t)t * 4 + lane] = rt.id(lane);
         a.wsel[(size_t)t * 4 + lane] = lane < a.n_used ? rt.w(lane) : 0.f;

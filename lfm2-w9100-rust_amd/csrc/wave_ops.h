@@ -193,6 +193,18 @@ __device__ __forceinline__ int wave_max_i(int v)
 // normalization of route_normalize).  Selection on integer keys of the
 // scores: removed experts and lanes past n_expert take the lowest key, NaN
 // scores the next (below every number), so numbers rank exactly as floats.
+// sigmoid(logit) with the hardware exp2 / reciprocal (a few ulp).
+__device__ __forceinline__ float route_prob(float lg)
+{
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(lg * -1.44269504088896341f));
+}
+
+// The selection score p + bias (lfm.rs:613-622) that the picks are ranked by.
+__device__ __forceinline__ float route_score(const RouteIn in)
+{
+    return route_prob(in.lg) + in.bias;
+}
+
 __device__ __forceinline__ Routed wave_route_ids(const Route &r, const RouteIn in)
 {
     const uint32_t lane = threadIdx.x & 63;
@@ -200,8 +212,7 @@ __device__ __forceinline__ Routed wave_route_ids(const Route &r, const RouteIn i
     float prob = 0.f;
     int key = (int)0x80000000;
     if (valid) {
-        // sigmoid with the hardware exp2 / reciprocal (a few ulp)
-        prob = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(in.lg * -1.44269504088896341f));
+        prob = route_prob(in.lg);
         const float score = prob + in.bias;
         key = score == score ? float_key(score) : (int)0x80000001;
     }

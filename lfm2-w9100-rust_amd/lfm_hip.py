@@ -10,8 +10,10 @@ code object is missing, every call raises.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
+import weakref
 from typing import Iterable, List, Optional, Sequence
 
 import numpy as np
@@ -152,6 +154,10 @@ def lib():
         "lfm_engine_last_route": (i32, [P, pu32, pf32, u32]),
         "lfm_engine_run_layer": (i32, [P, u32, pf32, u32, pf32]),
         "lfm_engine_fused_router": (i32, [P, u32, C.POINTER(C.c_int)]),
+        "lfm_engine_route_records": (i32, [P, pu32, sz]),
+        "lfm_engine_set_route_log": (i32, [P, i32]),
+        "lfm_engine_prefill_routes": (i32, [P, u32, pu32, pu32, C.POINTER(C.c_int), pu32, pf32, pf32,
+                                            sz]),
         "lfm_engine_time_moe_gateup": (i32, [P, u32, pf32, C.POINTER(u64)]),
         "lfm_engine_time_head": (i32, [P, u32, u32, pf32, C.POINTER(u64)]),
         "lfm_dev_alloc": (i32, [sz, C.POINTER(P)]), "lfm_dev_free": (i32, [P]),
@@ -520,6 +526,21 @@ def write_synthetic_gguf(path: str, hp: Hparams, opts: Optional[SynthOpts] = Non
 
 
 # ------------------------------------------------------------------ device buffers
+# Engines and device buffers still open.  They are released at interpreter exit
+# (atexit runs before module teardown), while the HIP runtime and any tool
+# attached to it are still up, rather than by __del__ during teardown.
+_LIVE = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_engines():
+    for e in list(_LIVE):
+        try:
+            e.close()
+        except Exception:
+            pass
+
+
 class DeviceBuffer:
     """Device memory owned by the library's HIP runtime (hipMalloc)."""
 
@@ -528,6 +549,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         _check(lib().lfm_dev_alloc(self.nbytes, C.byref(p)))
         self.ptr = p.value
+        _LIVE.add(self)
 
     @classmethod
     def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
@@ -552,6 +574,9 @@ class DeviceBuffer:
         if self.ptr:
             _check(lib().lfm_dev_free(self.ptr))
             self.ptr = None
+        _LIVE.discard(self)
+
+    close = free
 
     def __del__(self):
         try:
@@ -657,6 +682,7 @@ class GpuEngine:
     def __init__(self, hp: Hparams, device: int = 0, ctx: int = MAX_CTX):
         self._e = C.c_void_p()
         _check(lib().lfm_engine_create(C.byref(hp), device, C.byref(self._e)))
+        _LIVE.add(self)
         self.hp = hp
         self.ctx = ctx
         _check(lib().lfm_engine_set_ctx(self._e, ctx))
@@ -689,6 +715,7 @@ class GpuEngine:
                                           C.byref(h)))
         e = cls.__new__(cls)
         e._e = h
+        _LIVE.add(e)
         e.hp = Hparams()
         _check(lib().lfm_engine_hparams(h, C.byref(e.hp)))
         e.ctx = ctx
@@ -804,6 +831,43 @@ class GpuEngine:
         _check(lib().lfm_engine_last_route(self._e, _u32p(ids), _f32p(w), 8))
         return [int(i) for i in ids[: self.hp.n_used]], w[: self.hp.n_used].copy()
 
+    ROUTE_REC_WORDS = 144
+
+    def route_records(self):
+        """The decode step's routing per layer: {layer: (ids, weights, logits,
+        scores)} for the MoE layers, scores being the p + bias values the
+        kernel ranked the experts by (lfm_engine_route_records)."""
+        hp, W = self.hp, self.ROUTE_REC_WORDS
+        words = np.zeros(hp.n_layers * W, dtype=np.uint32)
+        _check(lib().lfm_engine_route_records(self._e, _u32p(words), words.size))
+        out = {}
+        for l in range(hp.dense_lead, hp.n_layers):
+            r = words[l * W:(l + 1) * W]
+            out[l] = ([int(i) for i in r[:hp.n_used]], r[8:8 + hp.n_used].view(np.float32).copy(),
+                      r[16:16 + hp.n_expert].view(np.float32).copy(),
+                      r[80:80 + hp.n_expert].view(np.float32).copy())
+        return out
+
+    def set_route_log(self, on: bool = True):
+        """Keep the routing of later multi-token forwards (lfm_engine_set_route_log)."""
+        _check(lib().lfm_engine_set_route_log(self._e, int(on)))
+
+    def prefill_routes(self, layer: int):
+        """Routing of layer `layer` in the last multi-token forward:
+        (first row, ids [n][4], weights [n][4], logits [n][n_expert] or None)."""
+        hp = self.hp
+        first, n, has = C.c_uint32(0), C.c_uint32(0), C.c_int(0)
+        cap = self.ctx
+        ids = np.zeros(cap * 4, dtype=np.uint32)
+        w = np.zeros(cap * 4, dtype=np.float32)
+        lg = np.zeros(cap * hp.n_expert, dtype=np.float32)
+        _check(lib().lfm_engine_prefill_routes(self._e, layer, C.byref(first), C.byref(n), C.byref(has),
+                                               _u32p(ids), _f32p(w), _f32p(lg), cap))
+        k = n.value
+        return (first.value, ids[:k * 4].reshape(k, 4)[:, :hp.n_used].copy(),
+                w[:k * 4].reshape(k, 4)[:, :hp.n_used].copy(),
+                lg[:k * hp.n_expert].reshape(k, hp.n_expert).copy() if has.value else None)
+
     def time_moe_gateup(self, reps: int = 10):
         """(us per launch, algorithmic bytes per launch) of the routed gate/up kernel."""
         us, nb = C.c_float(0), C.c_uint64(0)
@@ -818,9 +882,17 @@ class GpuEngine:
         _check(lib().lfm_engine_time_head(self._e, ncopies, reps, C.byref(us), C.byref(nb)))
         return us.value, nb.value
     def close(self):
+        """lfm_engine_destroy: waits for the engine's stream, frees its buffers and graphs."""
         if self._e:
             lib().lfm_engine_destroy(self._e)
             self._e = None
+        _LIVE.discard(self)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     def __del__(self):
         try:

@@ -18,6 +18,15 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: full-size model checks")
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _release_engines():
+    """Engines and device buffers the tests left open are released when the
+    session ends, while the HIP runtime is still up."""
+    yield
+    import lfm_hip
+    lfm_hip._close_live_engines()
+
+
 @pytest.fixture(scope="session")
 def lfm():
     import lfm_hip

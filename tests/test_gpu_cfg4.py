@@ -1,38 +1,36 @@
 """The full token loop at its real size against the oracle: 24 layers (conv
 mixers, GQA attention at layers 2, 6, 10, 14, 18, 21), dense SwiGLU ff 7168 in
 layers 0-1, MoE 32 experts top-4 ff 1792 in layers 2-23, vocab 65536 tied head,
-seeded random Q6_K weights; a 3840-token prompt of uniform ids prefilled in one
-call, then 256 greedy tokens at positions 3840..4095 (ctx 4096).
+seeded random Q6_K weights; a 3840-token prompt of uniform ids, then 256 greedy
+tokens at positions 3840..4095 (ctx 4096).
 
-The reference audits this workload with a teacher-forced, margin-checked run
-(engine/src/bin/teacher_audit.rs:6-17; its qualification ran 3840 + 256,
-validation/qualification.json:93-124).  Running the oracle's own 3840-token
-prefill would take minutes of host work, so the oracle starts from the GPU's
-state instead and checks every step it takes:
+The reference audits this workload teacher-forced, comparing every step's full
+logits and requiring exact greedy tokens (engine/src/bin/teacher_audit.rs:6-17;
+its qualification ran 3840 + 256 with 64-token prefill chunks,
+validation/qualification.json:93-124, bin/api_stream.rs:57-63).  Running the
+oracle's own 3840-token prefill is minutes of host work, so the prompt is
+checked three ways on the GPU and the oracle is brought in where the paths
+disagree:
 
-1. last prompt position: the oracle restored from the GPU's state after the
-   first 3839 prompt tokens computes position 3839; its logits must match the
-   whole-prompt GPU call's (rel-L2 <= 1e-3) and pick the same token when the
-   top-2 margin is clear;
-2. the whole-prompt (matrix-core) state at 3840 must match the state of the same
-   prompt run one decode step per token (rel-L2 <= 1e-3 per layer, outside
-   routing near-ties, below);
-3. the oracle restored at 3840 is teacher-forced with the GPU's 256 tokens:
-   tokens equal wherever the oracle's top-2 margin exceeds 1e-3 * max|logit|,
-   and the resident state at 4096 matches (rel-L2 <= 1e-3 per layer outside
-   routing near-ties).
+* the prompt runs as one matrix-core call (whole), as sixty 64-token calls
+  (chunked, the api_stream path) and as one decode step per token (stepwise,
+  the decode graph's kernels); every routing decision (3840 positions x 22 MoE
+  layers) of each path is logged and compared with the stepwise one;
+* where two paths pick different experts, the oracle restored from the
+  stepwise state at that position computes it: its 4th/5th score margin must
+  be within twice the measured score drifts (tests/route_audit.py);
+* the resident states match per layer (rel-L2 <= 1e-3) outside the positions
+  such a flip touched, and the last logits and next tokens agree;
+* position 3839 by the oracle restored at 3839 against the whole call.
 
-Routing near-ties: expert ids are identical only where the 4th and 5th selection
-scores are apart (the selection contract; the reassociated router sums differ in
-the last bits).  Over 3840 x 22 routing decisions a few fall inside that margin;
-a different expert at one position changes that position's residual, hence its
-K/V in later attention layers and, through the 3-tap convolution, the next few
-positions.  Such positions are found per position (largest K/V difference
-against the state's rms above 1e-2) and come in short runs of consecutive
-positions (the convolution state carries the difference on while it decays).
-At most 1 % of positions may be such; in the decode comparison every run must
-start at, or one position after, an oracle routing margin below 1e-4; and the
-rel-L2 bar applies to the remaining positions.
+The decode half: 256 greedy steps from the whole-prompt state, replayed
+teacher-forced one token per call with their routing records; against the
+oracle teacher-forced from the same state, every step's full logits (rel-L2 <=
+1e-3 where no routing flip touched the step), every routing decision (flips
+only at near-ties within twice the measured drift, drift <= DECODE_DRIFT_CAP),
+tokens equal wherever the oracle's top-2 margin exceeds 1e-3 * max|logit|, and
+the state at 4096.  The decode kernels' own records must also rank exactly by
+the scores they logged.
 """
 import os
 import time
@@ -42,98 +40,39 @@ import pytest
 
 from conftest import rel_l2
 from model_util import top2_margin
+from route_audit import Audit, margin, reach, sigmoid_scores, state_errors, top_ids
 
 pytestmark = pytest.mark.gpu
 
 SEED = 0x9E3779B97F4A7C15
 N_PROMPT, N_DECODE, CTX = 3840, 256, 4096
+# Score drift caps at clean decisions (no flip at the position's lower layers or
+# the two positions before).  Decode vs oracle: both start from the same state
+# at 3840, so only the new positions' arithmetic differs (rel. ~1e-6 per layer).
+# Whole or chunked prompt vs stepwise: two GPU paths over 3840 positions, whose
+# states differ per layer by up to ~1e-4 rel-L2 (binary16 hi + lo products and
+# reassociated sums in the GEMMs, binary16 KV); |d score / d x| <= 0.25 |logit|.
+DECODE_DRIFT_CAP = 1e-5
+PROMPT_DRIFT_CAP = 1e-4
+ORACLE_STEP_CAP = 1e-5  # oracle vs the stepwise kernels from the same state, one position
 
 
 def say(msg):
     print(f"[cfg4] {msg}", flush=True)
 
 
-def layer_errors(hp, a, b, valid):
-    """rel-L2 per layer of two reference-format snapshots (K then V per
-    attention layer, [ch][2] conv state per conv layer)."""
-    fa, fb = np.frombuffer(a, np.float32), np.frombuffer(b, np.float32)
-    assert fa.size == fb.size
-    out, off = [], 0
-    for l in range(hp.n_layers):
-        n = 2 * valid * 64 * hp.kv_heads[l] if hp.kv_heads[l] else 2 * hp.dim
-        out.append(rel_l2(fa[off:off + n], fb[off:off + n]))
-        off += n
-    assert off == fa.size
-    return out
-
-
-OUTLIER_REL = 1e-2  # per position: max |K/V difference| / rms of the layer's state
-OUTLIER_SHARE = 0.01
-NEAR_TIE = 1e-4     # oracle 4th/5th routing score margin that can explain an outlier
-
-
-def attention_positions(hp, a, b, valid):
-    """Per attention layer: (K/V arrays [valid, kv*64] of both snapshots)."""
-    fa, fb = np.frombuffer(a, np.float32), np.frombuffer(b, np.float32)
-    out, off = {}, 0
-    for l in range(hp.n_layers):
-        kv = hp.kv_heads[l]
-        if not kv:
-            off += 2 * hp.dim
-            continue
-        n = valid * 64 * kv
-        ka, kb = fa[off:off + n].reshape(valid, -1), fb[off:off + n].reshape(valid, -1)
-        va, vb = fa[off + n:off + 2 * n].reshape(valid, -1), fb[off + n:off + 2 * n].reshape(valid, -1)
-        out[l] = (np.concatenate([ka, va], axis=1), np.concatenate([kb, vb], axis=1))
-        off += 2 * n
-    return out
-
-
-def outlier_positions(hp, a, b, valid):
-    """Positions whose largest K/V difference (any attention layer) exceeds
-    OUTLIER_REL times that layer's state rms."""
-    bad = np.zeros(valid, dtype=bool)
-    for l, (xa, xb) in attention_positions(hp, a, b, valid).items():
-        rms = np.sqrt(np.mean(xb.astype(np.float64) ** 2))
-        bad |= np.abs(xa - xb).max(axis=1) > OUTLIER_REL * rms
-    return np.flatnonzero(bad)
-
-
-def masked_errors(hp, a, b, valid, drop):
-    """rel-L2 per attention layer over the positions not in `drop`."""
-    keep = np.ones(valid, dtype=bool)
-    keep[drop] = False
-    return {l: rel_l2(xa[keep], xb[keep]) for l, (xa, xb) in attention_positions(hp, a, b, valid).items()}
-
-
-def attention_detail(hp, a, b, valid, label):
-    """For attention layers whose state differs by more than 1e-4: K and V
-    separately, the binary16 ulp distance of the differing elements and where
-    (position, kv head) the largest differences sit."""
-    fa, fb = np.frombuffer(a, np.float32), np.frombuffer(b, np.float32)
-    off = 0
-    for l in range(hp.n_layers):
-        kv = hp.kv_heads[l]
-        if not kv:
-            off += 2 * hp.dim
-            continue
-        n = valid * 64 * kv
-        for part in ("K", "V"):
-            xa, xb = fa[off:off + n], fb[off:off + n]
-            off += n
-            e = rel_l2(xa, xb)
-            if e <= 1e-4:
-                continue
-            ha = xa.astype(np.float16).view(np.int16).astype(np.int32)
-            hb = xb.astype(np.float16).view(np.int16).astype(np.int32)
-            ulp = np.abs(ha - hb)
-            diff = np.abs(xa - xb).reshape(valid, kv, 64)
-            per_pos = diff.max(axis=(1, 2))
-            worst = np.argsort(per_pos)[::-1][:4]
-            say(f"{label} layer {l} {part}: rel-L2 {e:.2e}, |x| max {np.abs(xb).max():.3g} rms "
-                f"{np.sqrt(np.mean(xb.astype(np.float64) ** 2)):.3g}; {np.count_nonzero(ulp)} of {n} "
-                f"differ, ulp hist {np.bincount(np.minimum(ulp, 4))[1:].tolist()}; worst positions "
-                + ", ".join(f"{int(p)}:{per_pos[p]:.3g}" for p in worst))
+def check_flips(audit, label, extra_drift=None):
+    """Every run-starting flip within twice the drift of the clean decisions
+    (plus the oracle's own distance at that decision when given)."""
+    drift = audit.clean_drift()
+    say(f"{label}: {audit.summary()}")
+    for key in audit.first_flips():
+        ids, ref_ids, d, m = audit.rows[key]
+        bar = 2 * (drift + (extra_drift or {}).get(key, 0.0)) + 1e-6
+        say(f"  {label} {audit.kind(key)} flip at position {key[0]} layer {key[1]}: {ids} vs {ref_ids}, "
+            f"margin {m:.2e} (bar {bar:.2e}), drift there {d:.2e}")
+        assert m <= bar, (label, key, m, bar)
+    return drift
 
 
 def test_cfg4_full_size_against_oracle(gpu, oracle):
@@ -141,47 +80,136 @@ def test_cfg4_full_size_against_oracle(gpu, oracle):
     hp = gpu.make_hparams()  # the model's geometry
     assert (hp.n_layers, hp.vocab, hp.dim, hp.n_expert) == (24, 65536, 2048, 32)
     opts = gpu.synth_opts(SEED)
+    moe = list(range(hp.dense_lead, hp.n_layers))
+    descs = {d.name.decode(): d for d in gpu.model_tensor_descs(hp, opts)}
+    bias = {l: gpu.synth_tensor(descs[f"blk.{l}.exp_probs_b.bias"], opts) for l in moe}
     g = gpu.GpuEngine.load_synthetic(hp, opts, ctx=CTX, threads=16)
+    g.set_route_log(True)
     prompt = [int(v) for v in np.random.default_rng(SEED & 0xFFFFFFFF).integers(0, hp.vocab, N_PROMPT)]
     say(f"GPU engine loaded ({time.perf_counter() - t0:.1f} s)")
 
+    def call_routes(out, start):
+        for l in moe:
+            first, ids, _, lg = g.prefill_routes(l)
+            for j in range(len(ids)):
+                out[(start + first + j, l)] = (ids[j], sigmoid_scores(lg[j], bias[l]))
+
+    # whole prompt in one matrix-core call (and the state after 3839 tokens)
     g.forward(prompt[:N_PROMPT - 1], 0)
     s3839 = g.snapshot_resident_cache(N_PROMPT - 1)
     g.reset_session()
     lg = g.forward(prompt, 0)
-    s3840 = g.snapshot_resident_cache(N_PROMPT)
+    s_whole = g.snapshot_resident_cache(N_PROMPT)
+    whole = {}
+    call_routes(whole, 0)
     first = int(oracle.argmax(lg))
-    g.reset_session()
-    g.set_prefill_mode(True)
-    lst = g.forward(prompt, 0)
-    g.set_prefill_mode(False)
-    s3840_step = g.snapshot_resident_cache(N_PROMPT)
-    errs = layer_errors(hp, s3840, s3840_step, N_PROMPT)
-    say(f"whole-prompt vs stepwise: logits rel-L2 {rel_l2(lg, lst):.2e}, state per layer "
-        + " ".join(f"{l}:{e:.1e}" for l, e in enumerate(errs)))
-    attention_detail(hp, s3840, s3840_step, N_PROMPT, "whole vs stepwise")
-    assert rel_l2(lg, lst) <= 1e-3
-    out = outlier_positions(hp, s3840, s3840_step, N_PROMPT)
-    merr = masked_errors(hp, s3840, s3840_step, N_PROMPT, out)
-    say(f"whole vs stepwise: {len(out)} routing-flip positions {out.tolist()[:12]}; attention "
-        f"layers without them <= {max(merr.values()):.2e}")
-    assert len(out) <= OUTLIER_SHARE * N_PROMPT
-    assert max(merr.values()) <= 1e-3, merr
-    assert max(e for l, e in enumerate(errs) if not hp.kv_heads[l]) <= 1e-3, errs
 
-    g.restore_session(N_PROMPT, s3840)
+    # the api_stream path: sixty 64-token forward_token calls
+    g.reset_session()
+    chunk = {}
+    for s0 in range(0, N_PROMPT, 64):
+        nxt_chunk = g.forward_token(prompt[s0:s0 + 64], s0)
+        call_routes(chunk, s0)
+    s_chunk = g.snapshot_resident_cache(N_PROMPT)
+
+    # one decode step per token, with the decode kernels' routing records
+    g.reset_session()
+    step, inconsistent = {}, 0
+    for p in range(N_PROMPT):
+        g.forward_token([prompt[p]], p)
+        for l, (ids, _, _, sc) in g.route_records().items():
+            step[(p, l)] = (ids, sc)
+            inconsistent += ids != top_ids(sc, hp.n_used)
+    lst = g.snapshot_resident_logits()
+    s_step = g.snapshot_resident_cache(N_PROMPT)
+    say(f"whole, chunked and stepwise prompts done ({time.perf_counter() - t0:.1f} s)")
+    assert inconsistent == 0, f"{inconsistent} decode routing records do not rank by their own scores"
+
+    audits = {}
+    for name, rec in (("whole", whole), ("chunked", chunk)):
+        a = Audit(hp.n_used)
+        for key, (ids, sc) in rec.items():
+            a.add(key[0], key[1], ids, sc, *step[key])
+        audits[name] = a
+    assert len(audits["whole"].rows) == (N_PROMPT * (len(moe) - 1) + 1)
+    assert len(audits["chunked"].rows) == N_PROMPT * (len(moe) - 1) + N_PROMPT // 64
+
+    # stepwise state before every run-starting flip, for the oracle
+    need = sorted({p for a in audits.values() for p, _ in a.first_flips()})
+    snaps = {}
+    if need:
+        g.reset_session()
+        g.set_prefill_mode(True)
+        cur = 0
+        for p in need:
+            if p > cur:
+                g.forward(prompt[cur:p], cur)
+            snaps[p] = g.snapshot_resident_cache(p)
+            cur = p
+        g.set_prefill_mode(False)
+
+    # decode: 256 greedy steps from the whole-prompt state, then the same tokens
+    # replayed one per call with the routing records of every step
+    g.restore_session(N_PROMPT, s_whole)
     toks = g.decode_run(first, N_PROMPT, N_DECODE, eos=1 << 31)
     assert len(toks) == N_DECODE
     s4096 = g.snapshot_resident_cache(CTX)
+    g.restore_session(N_PROMPT, s_whole)
+    glog = np.empty((N_DECODE, hp.vocab), dtype=np.float32)
+    grec, feed = [], first
+    for s in range(N_DECODE):
+        glog[s] = g.forward([feed], N_PROMPT + s)
+        grec.append(g.route_records())
+        assert int(oracle.argmax(glog[s])) == toks[s], (s, toks[s])  # the graph's own kernels
+        feed = toks[s]
+    assert g.snapshot_resident_cache(CTX) == s4096
     g.close()
-    say(f"GPU prefill + stepwise + 256 decode done ({time.perf_counter() - t0:.1f} s)")
+    say(f"GPU decode + replay done ({time.perf_counter() - t0:.1f} s)")
 
     oracle.set_threads(min(16, len(os.sched_getaffinity(0))))
     o = oracle.OracleEngine(hp, ctx=CTX, kv_f16=True)
-    for d in gpu.model_tensor_descs(hp, opts):
+    for d in descs.values():
         o.set_tensor(d.name.decode(), int(d.ggml_type), d.shape, gpu.synth_tensor(d, opts, threads=16))
     o.finalize()
     say(f"oracle loaded ({time.perf_counter() - t0:.1f} s)")
+
+    # the oracle at every prompt position where two GPU paths route differently
+    oracle_gap = {}
+    for p in need:
+        o.restore(p, snaps[p])
+        o.forward([prompt[p]], p)
+        for l in moe:
+            if (p, l) not in step:
+                continue
+            oids, _, osc = o.last_route(l)
+            ids, sc = step[(p, l)]
+            gap = float(np.abs(sc.astype(np.float64) - osc).max())
+            assert gap <= ORACLE_STEP_CAP, (p, l, gap)
+            oracle_gap[(p, l)] = gap
+            for name, a in audits.items():
+                if (p, l) in a.first_flips():
+                    ref_m = margin(osc, hp.n_used)
+                    say(f"  oracle at {name} {a.kind((p, l))} flip ({p}, {l}): oracle {oids}, stepwise {ids}, "
+                        f"{name} {a.rows[(p, l)][0]}, oracle margin {ref_m:.2e}, stepwise vs oracle {gap:.2e}")
+                    bar = 2 * (a.clean_drift() + gap) + 1e-6
+                    assert ref_m <= bar, (name, p, l, ref_m, bar)
+    for name, a in audits.items():
+        drift = check_flips(a, f"{name} vs stepwise", oracle_gap)
+        assert drift <= PROMPT_DRIFT_CAP, (name, drift)
+
+    # the prompt states and logits
+    for name, snap in (("whole", s_whole), ("chunked", s_chunk)):
+        errs, dropped = state_errors(hp, snap, s_step, N_PROMPT, audits[name].flips())
+        say(f"{name} vs stepwise state per layer " + " ".join(f"{l}:{e:.1e}" for l, e in errs.items())
+            + f" ({dropped} positions near flips left out)")
+        assert max(errs.values()) <= 1e-3, (name, errs)
+    cw = state_errors(hp, s_chunk, s_whole, N_PROMPT, audits["whole"].flips() + audits["chunked"].flips())[0]
+    assert max(cw.values()) <= 1e-3, cw
+    say(f"whole vs stepwise logits rel-L2 {rel_l2(lg, lst):.2e}; next token whole {first}, "
+        f"chunked {nxt_chunk}")
+    assert rel_l2(lg, lst) <= 1e-3
+    if top2_margin(lg) > 1e-3 * float(np.abs(lg).max()):
+        assert nxt_chunk == first
 
     o.restore(N_PROMPT - 1, s3839)
     lo = o.forward([prompt[-1]], N_PROMPT - 1)
@@ -192,17 +220,18 @@ def test_cfg4_full_size_against_oracle(gpu, oracle):
     if top2_margin(lo) > tol:
         assert first == oracle.argmax(lo)
 
-    o.restore(N_PROMPT, s3840)
-    feed, compared = first, 0
-    moe_layers = list(range(hp.dense_lead, hp.n_layers))
-    margin = np.zeros(N_DECODE)  # smallest 4th/5th routing score margin at each step
+    # decode, teacher-forced from the same state
+    o.restore(N_PROMPT, s_whole)
+    dec = Audit(hp.n_used)
+    feed, compared, lerr = first, 0, np.zeros(N_DECODE)
     for s in range(N_DECODE):
         lo = o.forward([feed], N_PROMPT + s)
-        m = np.inf
-        for l in moe_layers:
-            srt = np.sort(o.last_route(l)[2])[::-1]
-            m = min(m, float(srt[3] - srt[4]))
-        margin[s] = m
+        lerr[s] = rel_l2(glog[s], lo)
+        for l in moe:
+            oids, _, osc = o.last_route(l)
+            ids, _, _, sc = grec[s][l]
+            assert ids == top_ids(sc, hp.n_used), (s, l)
+            dec.add(N_PROMPT + s, l, ids, sc, oids, osc)
         tol = 1e-3 * float(np.abs(lo).max())
         if top2_margin(lo) > tol:
             assert toks[s] == oracle.argmax(lo), (s, toks[s], oracle.argmax(lo))
@@ -212,26 +241,19 @@ def test_cfg4_full_size_against_oracle(gpu, oracle):
             say(f"teacher-forced {s + 1}/{N_DECODE} steps, {compared} margin-clear tokens equal "
                 f"({time.perf_counter() - t0:.1f} s)")
     so = o.snapshot(CTX)
-    errs = layer_errors(hp, s4096, so, CTX)
-    attention_detail(hp, s4096, so, CTX, "decode vs oracle")
     o.close()
-    say(f"{compared}/{N_DECODE} margin-clear tokens equal; state at 4096 per layer "
-        + " ".join(f"{l}:{e:.1e}" for l, e in enumerate(errs)) + f"; {time.perf_counter() - t0:.1f} s")
+    drift = check_flips(dec, "decode vs oracle")
+    assert drift <= DECODE_DRIFT_CAP, drift
+    # the logits of a step read the residual after the last layer (layer 24's input)
+    touched = {p - N_PROMPT for f in dec.flips() for p in reach(hp.n_layers, f)}
+    clean = [s for s in range(N_DECODE) if s not in touched]
+    worst = int(np.argmax(lerr))
+    say(f"per-step logits rel-L2: worst {lerr[worst]:.2e} at step {worst}, worst clean "
+        f"{lerr[clean].max():.2e} ({len(clean)} of {N_DECODE} steps clean); {compared}/{N_DECODE} "
+        f"margin-clear tokens equal")
+    assert lerr[clean].max() <= 1e-3
     assert compared >= N_DECODE * 3 // 4
-    out = outlier_positions(hp, s4096, so, CTX)
-    merr = masked_errors(hp, s4096, so, CTX, out)
-    say(f"decode vs oracle: smallest routing margin {margin.min():.2e} at position "
-        f"{N_PROMPT + int(margin.argmin())}; routing-flip positions "
-        + ", ".join(f"{p} (margin {margin[p - N_PROMPT]:.1e})" for p in out.tolist())
-        + f"; attention layers without them <= {max(merr.values()):.2e}")
-    assert len(out) <= OUTLIER_SHARE * CTX
-    for p in out.tolist():
-        assert p >= N_PROMPT, p  # the prompt positions were restored unchanged
-        if p - 1 in out:
-            continue  # inside a run: carried on by the convolution state
-        # a run starts where a near-tie routed the position (or, for a flip after
-        # the last attention layer, the position before) to another expert
-        window = margin[max(0, p - N_PROMPT - 1):p - N_PROMPT + 1]
-        assert window.min() < NEAR_TIE, (p, window)
-    assert max(merr.values()) <= 1e-3, merr
-    assert max(e for l, e in enumerate(errs) if not hp.kv_heads[l]) <= 1e-3, errs
+    errs, dropped = state_errors(hp, s4096, so, CTX, dec.flips())
+    say("state at 4096 vs oracle per layer " + " ".join(f"{l}:{e:.1e}" for l, e in errs.items())
+        + f" ({dropped} positions near flips left out; {time.perf_counter() - t0:.1f} s)")
+    assert max(errs.values()) <= 1e-3, errs
