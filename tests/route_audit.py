@@ -97,10 +97,23 @@ class Audit:
         ds = [r[2] for k, r in self.rows.items() if r[0] == r[1] and not self.carried(k, fl)]
         return max(ds) if ds else 0.0
 
+    def pre_flip_drift(self):
+        """Largest score difference before the first flip (positions before it,
+        and its own position's lower layers): arithmetic alone, with no flip
+        behind it.  Later clean decisions also see a flip's position through
+        attention, which reads every earlier position's K/V."""
+        fl = self.flips()
+        if not fl:
+            return self.clean_drift()
+        p0, l0 = min(fl)
+        ds = [r[2] for (p, l), r in self.rows.items() if p < p0 or (p == p0 and l < l0)]
+        return max(ds) if ds else 0.0
+
     def summary(self):
         fl = self.flips()
         return (f"{len(self.rows)} decisions, {len(fl)} flips ({len(self.first_flips())} run starts), "
-                f"clean drift {self.clean_drift():.2e}, smallest reference margin "
+                f"clean drift {self.clean_drift():.2e} ({self.pre_flip_drift():.2e} before the first "
+                f"flip), smallest reference margin "
                 f"{min(r[3] for r in self.rows.values()):.2e}")
 
 

@@ -46,15 +46,20 @@ pytestmark = pytest.mark.gpu
 
 SEED = 0x9E3779B97F4A7C15
 N_PROMPT, N_DECODE, CTX = 3840, 256, 4096
-# Score drift caps at clean decisions (no flip at the position's lower layers or
-# the two positions before).  Decode vs oracle: both start from the same state
-# at 3840, so only the new positions' arithmetic differs (rel. ~1e-6 per layer).
+# Score drift caps at clean decisions (no flip reaches them, route_audit.Audit),
+# about 2-3x the largest drift measured on the MI355X.  Decode vs oracle: both
+# start from the same state at 3840; the drift grows with depth (3e-6 at layer
+# 2 to 1.7e-5 at layer 23: the residual carries every layer's rounding) and
+# over the first ~10 steps (the new positions' K/V and conv state), then stays
+# level (1e-5 +- 0.5e-5 to step 255); after a flip every later position also
+# attends to the flipped position's changed K/V.
 # Whole or chunked prompt vs stepwise: two GPU paths over 3840 positions, whose
-# states differ per layer by up to ~1e-4 rel-L2 (binary16 hi + lo products and
-# reassociated sums in the GEMMs, binary16 KV); |d score / d x| <= 0.25 |logit|.
-DECODE_DRIFT_CAP = 1e-5
-PROMPT_DRIFT_CAP = 1e-4
-ORACLE_STEP_CAP = 1e-5  # oracle vs the stepwise kernels from the same state, one position
+# states differ per layer by up to ~6e-5 rel-L2 outside flips (binary16 hi + lo
+# products and reassociated sums in the GEMMs; measured 9.5e-6 and 6.8e-6).
+DECODE_DRIFT_CAP = 3e-5
+DECODE_CARRIED_CAP = 5e-5
+PROMPT_DRIFT_CAP = 3e-5
+ORACLE_STEP_CAP = 1e-5  # oracle vs the stepwise kernels from the same state, one position (3.6e-6)
 
 
 def say(msg):
@@ -173,26 +178,29 @@ def test_cfg4_full_size_against_oracle(gpu, oracle):
     o.finalize()
     say(f"oracle loaded ({time.perf_counter() - t0:.1f} s)")
 
-    # the oracle at every prompt position where two GPU paths route differently
-    oracle_gap = {}
+    # the oracle at every prompt position where two GPU paths route differently:
+    # restored from the stepwise state there, it starts from the stepwise
+    # kernels' own inputs, so their scores agree within ORACLE_STEP_CAP up to
+    # the first layer where they themselves pick differently (a near-tie)
+    ostep = Audit(hp.n_used)
     for p in need:
         o.restore(p, snaps[p])
         o.forward([prompt[p]], p)
         for l in moe:
-            if (p, l) not in step:
-                continue
-            oids, _, osc = o.last_route(l)
-            ids, sc = step[(p, l)]
-            gap = float(np.abs(sc.astype(np.float64) - osc).max())
-            assert gap <= ORACLE_STEP_CAP, (p, l, gap)
-            oracle_gap[(p, l)] = gap
-            for name, a in audits.items():
-                if (p, l) in a.first_flips():
-                    ref_m = margin(osc, hp.n_used)
-                    say(f"  oracle at {name} {a.kind((p, l))} flip ({p}, {l}): oracle {oids}, stepwise {ids}, "
-                        f"{name} {a.rows[(p, l)][0]}, oracle margin {ref_m:.2e}, stepwise vs oracle {gap:.2e}")
-                    bar = 2 * (a.clean_drift() + gap) + 1e-6
-                    assert ref_m <= bar, (name, p, l, ref_m, bar)
+            if (p, l) in step:
+                oids, _, osc = o.last_route(l)
+                ostep.add(p, l, *step[(p, l)], oids, osc)
+    if need:
+        check_flips(ostep, "stepwise vs oracle")
+        assert ostep.clean_drift() <= ORACLE_STEP_CAP, ostep.clean_drift()
+    oracle_gap = {k: r[2] for k, r in ostep.rows.items()}
+    for name, a in audits.items():
+        for key in a.first_flips():
+            ids, oids, gap, ref_m = (a.rows[key][0],) + ostep.rows[key][1:]
+            bar = 2 * (a.clean_drift() + gap) + 1e-6
+            say(f"  oracle at {name} {a.kind(key)} flip {key}: oracle {oids}, stepwise {step[key][0]}, "
+                f"{name} {ids}, oracle margin {ref_m:.2e} (bar {bar:.2e}), stepwise vs oracle {gap:.2e}")
+            assert ref_m <= bar, (name, key, ref_m, bar)
     for name, a in audits.items():
         drift = check_flips(a, f"{name} vs stepwise", oracle_gap)
         assert drift <= PROMPT_DRIFT_CAP, (name, drift)
@@ -243,7 +251,19 @@ def test_cfg4_full_size_against_oracle(gpu, oracle):
     so = o.snapshot(CTX)
     o.close()
     drift = check_flips(dec, "decode vs oracle")
-    assert drift <= DECODE_DRIFT_CAP, drift
+    per_step = np.zeros(N_DECODE)
+    per_layer = {l: 0.0 for l in moe}
+    fl = dec.flips()
+    for (p, l), r in dec.rows.items():
+        if r[0] == r[1] and not dec.carried((p, l), fl):
+            per_step[p - N_PROMPT] = max(per_step[p - N_PROMPT], r[2])
+            per_layer[l] = max(per_layer[l], r[2])
+    say("decode drift per step (every 8th): " + " ".join(f"{s}:{per_step[s]:.1e}" for s in range(0, N_DECODE, 8)))
+    say("decode drift per layer: " + " ".join(f"{l}:{d:.1e}" for l, d in per_layer.items()))
+    # level, not growing: the last 64 steps drift no more than twice the first 64
+    assert per_step[-64:].max() <= 2 * per_step[:64].max(), (per_step[:64].max(), per_step[-64:].max())
+    assert dec.pre_flip_drift() <= DECODE_DRIFT_CAP, dec.pre_flip_drift()
+    assert drift <= DECODE_CARRIED_CAP, drift
     # the logits of a step read the residual after the last layer (layer 24's input)
     touched = {p - N_PROMPT for f in dec.flips() for p in reach(hp.n_layers, f)}
     clean = [s for s in range(N_DECODE) if s not in touched]
