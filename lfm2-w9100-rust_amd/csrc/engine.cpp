@@ -110,7 +110,7 @@ struct Kernels {
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
         tile_pack, gemm_q6_n64;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
-        dequant, copy, matvec_route, gateup_f;
+        dequant, copy, matvec_route, gateup_f, conv_mixer, conv_mixer_r;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
 };
@@ -211,7 +211,8 @@ static int get_kernels(Kernels **out)
                {&k->head.f16, "k_head16"},        {&k->argmax, "k_argmax"},
                {&k->argmax_final, "k_argmax_final"}, {&k->advance, "k_advance"},
                {&k->dequant, "k_q6_dequant"},    {&k->copy, "k_copy"},
-               {&k->matvec_route, "k_q6_matvec_route"}, {&k->gateup_f, "k_gateup8f"}};
+               {&k->matvec_route, "k_q6_matvec_route"}, {&k->gateup_f, "k_gateup8f"},
+               {&k->conv_mixer, "k_conv_mixer"},  {&k->conv_mixer_r, "k_conv_mixer_r"}};
     for (auto &f : fns) {
         e = hipModuleGetFunction(f.f, k->mod, f.name);
         if (e != hipSuccess) {
@@ -875,6 +876,13 @@ struct lfm_engine {
     } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
+    // conv mixers of the captured step in one launch each (k_conv_mixer*): the
+    // gated output's tagged entries, and whether the grid fits co-resident
+    unsigned long long *flow = nullptr;
+    bool fused_mixer = false;
+    // set while capture() enqueues a step: only captured steps end with the
+    // kernel that advances DevState::gen, which the fused kernels' tags need
+    bool capturing = false;
     hipGraphExec_t g_layers = nullptr, g_decode = nullptr;
     hipEvent_t win_ev[2] = {nullptr, nullptr}; // lfm_decode_run's replay window
     uint64_t nodes_layers = 0, nodes_decode = 0;
@@ -1142,6 +1150,36 @@ static int launch_gateup_fused(lfm_engine *e, const GateUpArgs &g)
     return launch_t(e->K->gateup_f, dim3((items + 15) / 16), 512, 0, e->stream, g);
 }
 
+// The conv mixer of a captured step in one launch (k_conv_mixer, or
+// k_conv_mixer_r with the fused router's partial sums): dim / 8 workgroups of
+// 8 waves, one channel and one output row per wave.
+static int launch_conv_mixer(lfm_engine *e, uint32_t l, const ConvInprojArgs &in, const MatvecArgs &m)
+{
+    ConvMixerArgs a;
+    memset(&a, 0, sizeof(a));
+    a.in = in;
+    a.out.m = m;
+    a.flow = e->flow;
+    a.phase = l;
+    const bool route = fused_router(e, l);
+    if (route) {
+        if (m.w.rows != ROUTE_WIDTH || m.w.nb > 8 || m.mode != 1)
+            return fail(LFM_EINTERNAL, "fused router: unexpected output projection shape");
+        a.out.rwt = (const float *)tensor(e, "blk.%u.ffn_gate_inp.weight", l)->tdev;
+        if (!a.out.rwt)
+            return fail(LFM_EINTERNAL, "fused router: layer %u has no transposed router weights", l);
+        a.out.rnorm = f32(e, "blk.%u.ffn_norm.weight", l);
+        a.out.rpart = e->rpart;
+        a.out.rss = e->rss;
+        a.out.xw = e->xw;
+    }
+    if (in.dim % 8 || m.w.rows != in.dim || m.in_dim != in.dim)
+        return fail(LFM_EINTERNAL, "conv mixer: unexpected shapes");
+    RC(launch_t(route ? e->K->conv_mixer_r : e->K->conv_mixer, dim3(in.dim / 8), 512, 0, e->stream, a));
+    e->dispatches += 1;
+    return LFM_OK;
+}
+
 static int enq_mixer(lfm_engine *e, uint32_t l, bool embed, bool fuse)
 {
     const lfm_hparams &hp = e->hp;
@@ -1168,8 +1206,10 @@ static int enq_mixer(lfm_engine *e, uint32_t l, bool embed, bool fuse)
         a.y = e->y;
         a.dim = dim;
         a.st = e->st;
-        RC(launch_mixer(e->K->conv, dim, e->stream, a));
         m.w = q6(e, "blk.%u.shortconv.out_proj.weight", l);
+        if (fuse && !embed && e->fused_mixer && e->capturing)
+            return launch_conv_mixer(e, l, a, m);
+        RC(launch_mixer(e->K->conv, dim, e->stream, a));
         RC(launch_out_proj(e, l, m, fuse));
         e->dispatches += 2;
         return LFM_OK;
@@ -1332,9 +1372,11 @@ static int capture(lfm_engine *e, bool decode, hipGraphExec_t *exec, uint64_t *n
     const uint64_t before = e->dispatches;
     hipGraph_t g = nullptr;
     HIPCHK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    e->capturing = true;
     int rc = enq_layers(e);
     if (rc == LFM_OK)
         rc = decode ? enq_head(e, 1) : enq_advance(e);
+    e->capturing = false;
     hipError_t ce = hipStreamEndCapture(e->stream, &g);
     *nodes = e->dispatches - before;
     e->dispatches = before;
@@ -1349,6 +1391,27 @@ static int capture(lfm_engine *e, bool decode, hipGraphExec_t *exec, uint64_t *n
     (void)hipGraphDestroy(g);
     if (ie != hipSuccess)
         return fail(LFM_EDEVICE, "hipGraphInstantiate: %s", hipGetErrorString(ie));
+    return LFM_OK;
+}
+
+// The fused conv mixer (LFM_FUSED_MIXER=1 at finalize; off by default: on the
+// MI355X its in-kernel handoff takes ~3.3 us after the last producer's store,
+// more than the kernel boundary it replaces, and the step is 0.75 ms against
+// 0.64 ms for the two-kernel chain).  Its workgroups wait for each other, so
+// the whole grid (dim / 8 workgroups of 512 threads) must be resident at once:
+// it is used only when the occupancy the runtime reports covers the grid.
+static int check_fused_mixer(lfm_engine *e)
+{
+    e->fused_mixer = false;
+    const char *env = getenv("LFM_FUSED_MIXER");
+    if (!env || env[0] != '1')
+        return LFM_OK;
+    int cus = 0, per_cu = 0, per_cu_r = 0;
+    HIPCHK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device));
+    HIPCHK(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, e->K->conv_mixer, 512, 0));
+    HIPCHK(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_r, e->K->conv_mixer_r, 512, 0));
+    const uint64_t grid = e->hp.dim / 8;
+    e->fused_mixer = (uint64_t)std::min(per_cu, per_cu_r) * (uint64_t)cus >= grid;
     return LFM_OK;
 }
 
@@ -1426,6 +1489,9 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     HIPCHK(hipMalloc(&e->rpart, ROUTE_EXPERTS * ROUTE_PARTS * 4));
     HIPCHK(hipMalloc(&e->rss, ROUTE_PARTS * 4));
     HIPCHK(hipMalloc(&e->xw, ROUTE_WIDTH * 4));
+    HIPCHK(hipMalloc(&e->flow, (size_t)dim * 8));
+    HIPCHK(hipMemset(e->flow, 0, (size_t)dim * 8)); // tag 0 never matches
+    RC(check_fused_mixer(e));
     HIPCHK(hipMemset(e->rpart, 0, ROUTE_EXPERTS * ROUTE_PARTS * 4));
     HIPCHK(hipMemset(e->rss, 0, ROUTE_PARTS * 4));
     HIPCHK(hipMemset(e->xw, 0, ROUTE_WIDTH * 4));
@@ -1566,7 +1632,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     for (void *p : e->qkvtdev)
         if (p)
             (void)hipFree(p);
-    void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->log_ids, e->log_w, e->log_logits, e->x, e->y, e->qkv, e->sw,
+    void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->log_ids, e->log_w, e->log_logits, e->flow, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
@@ -1960,15 +2026,21 @@ static int set_state(lfm_engine *e, uint32_t tok, uint32_t pos, uint32_t n_ids, 
     h.eos = eos;
     h.cursor = 0;
     h.n_ids = n_ids;
-    HIPCHK(hipMemcpyAsync(e->st, &h, sizeof(DevState), hipMemcpyHostToDevice, e->stream));
+    // everything but the step generation, which only the device advances
+    HIPCHK(hipMemcpyAsync(e->st, &h, offsetof(DevState, gen), hipMemcpyHostToDevice, e->stream));
     return LFM_OK;
 }
 
+// Reads the device state back after the stream's work; a fused kernel's
+// bounded handoff wait that timed out (the grid was not co-resident) fails the
+// call that ran it.
 static int read_state(lfm_engine *e, DevState *h)
 {
     HIPCHK(hipMemcpyAsync(e->host_st, e->st, sizeof(DevState), hipMemcpyDeviceToHost, e->stream));
     HIPCHK(hipStreamSynchronize(e->stream));
     *h = *e->host_st;
+    if (h->fault)
+        return fail(LFM_EDEVICE, "a fused decode kernel's handoff wait timed out (workgroups not co-resident)");
     return LFM_OK;
 }
 
@@ -2012,8 +2084,8 @@ extern "C" int lfm_forward_logits(lfm_engine *e, const uint32_t *ids, uint32_t n
     RC(run_prompt(e, ids, n, start));
     HIPCHK(hipMemcpyAsync(logits, e->logits, (size_t)e->hp.vocab * 4, hipMemcpyDeviceToHost,
                           e->stream));
-    HIPCHK(hipStreamSynchronize(e->stream));
-    return LFM_OK;
+    DevState h;
+    return read_state(e, &h);
 }
 
 extern "C" int lfm_forward_token(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start,

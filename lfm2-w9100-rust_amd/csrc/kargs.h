@@ -30,8 +30,12 @@ struct DevState {
     uint32_t n_ids;     // prompt length in ids
     uint32_t last_token;
     float last_value;
-    uint32_t pad[7];    // 64 bytes
-};
+    uint32_t fault;     // nonzero: a fused kernel's bounded handoff wait timed out
+    uint32_t pad[5];
+    uint32_t gen;       // step generation: the last kernel of every step adds 1;
+                        // the host never rewrites it (fused kernels' handoff tags)
+};                      // 64 bytes
+static_assert(sizeof(DevState) == 64, "DevState is 64 bytes");
 
 // Where a kernel's input vector comes from.
 struct XSrc {
@@ -423,4 +427,16 @@ struct EmbedRowsArgs {
     const uint32_t *ids;  // [T]
     float *x;             // [T][dim]
     uint32_t T;
+};
+
+// The short-conv mixer of one layer in one launch (k_conv_mixer, k_conv_mixer_r):
+// phase A = ConvInprojArgs with one channel per wave (its gated output handed
+// on through `flow`, in.y unused); phase B = the output projection y += W g
+// (out.m, one row per wave; out.m.src unused), with the router partial sums of
+// k_q6_matvec_route in k_conv_mixer_r.  dim / 8 workgroups of 8 waves.
+struct ConvMixerArgs {
+    ConvInprojArgs in;
+    MatvecRouteArgs out;
+    unsigned long long *flow; // [dim] tagged entries: gated output bits | tag << 32
+    uint32_t phase;           // this launch's phase id in the tags (the layer)
 };

@@ -581,6 +581,180 @@ extern "C" __global__ __launch_bounds__(1024) void k_conv_inproj16e(const ConvIn
     conv_inproj_body<16, 1, true>(a);
 }
 
+// ------------------------------------------------------------ in-kernel handoff
+// A fused kernel hands a vector from one phase to the next through tagged
+// entries: the value's bits and a tag in one 64-bit word, stored and polled
+// with agent-scope atomics, which are coherent across the XCDs' L2 caches
+// without a cache flush.  The tag names the step generation (DevState::gen,
+// advanced by the last kernel of every step) and the phase, so entries left by
+// an earlier step or another phase never match and nothing is reset between
+// graph replays; zeroed entries never match (bit 31 is always set).
+__device__ __forceinline__ uint32_t flow_tag(uint32_t gen, uint32_t phase)
+{
+    return 0x80000000u | ((gen & 0x7FFFFFu) << 8) | (phase & 0xFFu);
+}
+
+__device__ __forceinline__ void flow_put(unsigned long long *e, uint32_t i, float v, uint32_t tag)
+{
+    __hip_atomic_store(e + i, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every wait is bounded: after FLOW_SPIN_LIMIT polls (well over 0.1 s) the
+// waiter sets DevState::fault and goes on with what it read, and every later
+// wait of any workgroup sees the fault and stops waiting, so the grid always
+// drains; the host reports the fault.
+#define FLOW_SPIN_LIMIT (1u << 17)
+#ifndef FLOW_SLEEP
+#define FLOW_SLEEP 1 // s_sleep between polls (units of 64 clocks)
+#endif
+
+// Values of entries k .. k+7 once each carries `tag`.
+__device__ __forceinline__ void flow_get8(const unsigned long long *e, uint32_t k, uint32_t tag,
+                                          float (&v)[8], DevState *st)
+{
+    unsigned long long w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        w[i] = __hip_atomic_load(e + k + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t spins = 0;; ++spins) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ok = ok && (uint32_t)(w[i] >> 32) == tag;
+        if (ok)
+            break;
+        if (spins >= FLOW_SPIN_LIMIT || __hip_atomic_load(&st->fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            __hip_atomic_store(&st->fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(FLOW_SLEEP);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if ((uint32_t)(w[i] >> 32) != tag)
+                w[i] = __hip_atomic_load(e + k + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        v[i] = __uint_as_float((uint32_t)w[i]);
+}
+
+// Short-conv mixer in one launch (lfm.rs:450-533 then the output projection and
+// residual, with k_q6_matvec_route's router partial sums when ROUTE).  Wave w
+// of workgroup g owns channel ch = 8g + w in phase A and output row r = ch in
+// phase B; every value is computed as k_conv_inproj4 and k_q6_matvec_route /
+// k_q6_matvec4 compute it (same staging sums, lane products, reductions and
+// epilogues), so the results are bit-identical to the two-kernel chain.
+// Phase A stages the normed input, forms the channel's B, C, X rows, the conv
+// and the gate, and publishes the gated value as a tagged entry.  The
+// output-projection row's weights are issued with phase A's at the start, so
+// they arrive during phase A and the wait for all channels' values (phase B's
+// input) instead of after it.
+// The grid is dim / 8 workgroups, all co-resident (the host checks occupancy).
+template <bool ROUTE>
+__device__ __forceinline__ void conv_mixer_body(const ConvMixerArgs &a)
+{
+    constexpr int NW = 8;
+    const ConvInprojArgs &c = a.in;
+    const MatvecArgs &m = a.out.m;
+    DevState *st = c.st;
+    const uint32_t halted = load_halt(st);
+    const uint32_t gen = __hip_atomic_load(&st->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ __attribute__((aligned(16))) float gs[XS_MAX];
+    __shared__ float red[NW];
+    __shared__ float part[NW][ROUTE_EXPERTS + 1];
+    const uint32_t lane = threadIdx.x & 63, wave = wave_index();
+    const uint32_t b = lane >> 3, cl = lane & 7;
+    const bool active = b < c.w.nb;
+    const uint32_t dim = c.dim, ch = blockIdx.x * NW + wave, r = ch;
+    // phase A's loads, then what phase B needs that phase A does not produce
+    XRaw raw;
+    x_issue(c.src, dim, st, raw);
+    keep_issued(); // the input and its norm weight first: staging waits for them alone
+    const Lane wb = load_lane_c(c.w, ch, b, cl);
+    const Lane wc = load_lane_c(c.w, dim + ch, b, cl);
+    const Lane wx = load_lane_c(c.w, 2 * dim + ch, b, cl);
+    const ConvCh cv = conv_ch_load(c, ch);
+    keep_issued(); // phase A's loads before phase B's: phase A waits for its own alone
+    // phase B's weights: in flight through phase A and the handoff
+    const Lane wo = load_lane_c(m.w, r, b, cl);
+    const float yold = m.y[r + vzero()];
+    float rwe = 0.f, nwr = 0.f;
+    if constexpr (ROUTE) {
+        rwe = a.out.rwt[(size_t)r * ROUTE_EXPERTS + (lane & (ROUTE_EXPERTS - 1))];
+        nwr = a.out.rnorm[r + vzero()];
+    }
+    keep_issued();
+    if (halted)
+        return;
+    const uint32_t tag = flow_tag(gen, a.phase);
+    const float inv = x_stage<NW>(c.src, dim, st, raw, xs, red);
+    LaneX X;
+    lanex_lds(X, xs, b, cl, active);
+    float p[3];
+    p[0] = active ? lane_dot(wb, X) : 0.f;
+    p[1] = active ? lane_dot(wc, X) : 0.f;
+    p[2] = active ? lane_dot(wx, X) : 0.f;
+    wave_sum_n<3>(p);
+    if (lane == 0) {
+        float g;
+        conv_step(inv * p[0], inv * p[1], inv * p[2], cv, c.state + ch * 2, &g);
+        flow_put(a.flow, ch, g, tag);
+    }
+    // phase B: every channel's gated value, staged (no norm: inv = 1)
+    const uint32_t k = threadIdx.x * 8;
+    if (k < dim) {
+        float v[8];
+        flow_get8(a.flow, k, tag, v, st);
+        *reinterpret_cast<float4 *>(gs + k) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(gs + k + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+    LaneX G;
+    lanex_lds(G, gs, b, cl, active);
+    const float q = wave_sum(active ? lane_dot(wo, G) : 0.f);
+    const float val = yold + 1.0f * q;
+    if (lane == 0)
+        m.y[r] = val;
+    if constexpr (ROUTE) {
+        if (lane == 0)
+            a.out.xw[r] = val * nwr;
+        if (lane < ROUTE_EXPERTS)
+            part[wave][lane] = rwe * (val * nwr);
+        else if (lane == ROUTE_EXPERTS)
+            part[wave][lane] = val * val;
+        __syncthreads();
+        if (wave == 0 && lane < ROUTE_QUADS) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int i = 0; i < ROUTE_ROWS; ++i) {
+                acc.x += part[i][4 * lane + 0];
+                acc.y += part[i][4 * lane + 1];
+                acc.z += part[i][4 * lane + 2];
+                acc.w += part[i][4 * lane + 3];
+            }
+            reinterpret_cast<float4 *>(a.out.rpart)[lane * ROUTE_PARTS + blockIdx.x] = acc;
+        } else if (wave == 0 && lane == ROUTE_QUADS) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ROUTE_ROWS; ++i)
+                acc += part[i][ROUTE_EXPERTS];
+            a.out.rss[blockIdx.x] = acc;
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(512) void k_conv_mixer(const ConvMixerArgs a)
+{
+    conv_mixer_body<false>(a);
+}
+extern "C" __global__ __launch_bounds__(512) void k_conv_mixer_r(const ConvMixerArgs a)
+{
+    static_assert(ROUTE_ROWS == 8, "the fused router's partial sums cover one workgroup's 8 rows");
+    conv_mixer_body<true>(a);
+}
+
 // Attention projections: rows of q (dim), k and v (hdkv each) of the normed
 // input, written to qkv[0 .. dim + 2*hdkv).
 __device__ __forceinline__ Lane qkv_lane(const QkvArgs &a, uint32_t r, uint32_t b, uint32_t c)
@@ -1305,6 +1479,7 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax_final(const Fi
         DevState *st = a.st;
         st->last_token = bi;
         st->last_value = bv;
+        st->gen = st->gen + 1;
         if (a.advance) {
             if (bi == st->eos) {
                 st->halt = 1;
@@ -1324,6 +1499,7 @@ extern "C" __global__ void k_advance(const AdvanceArgs a)
     if (threadIdx.x != 0 || a.st->halt)
         return;
     DevState *st = a.st;
+    st->gen = st->gen + 1;
     const uint32_t cur = st->cursor + 1;
     st->cursor = cur;
     st->pos = st->pos + 1;
