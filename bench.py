@@ -7,11 +7,13 @@ Workload: 24 layers (18 gated short-conv, 6 GQA at layers 2,6,10,14,18,21),
 dense SwiGLU ff 7168 in layers 0-1, MoE 32 experts top-4 ff 1792 in layers
 2-23, vocab 65536 tied Q6_K head; seeded random weights; a 3840-token prompt
 of uniform ids prefilled in one call, then greedy decode at positions
-3840..4095 (ctx 4096).  One step = one decode token.  The K timed steps run
-from position 3840 in segments of at most 256 tokens; before each segment the
-resident state is restored (untimed) to the end of the prompt, so every timed
-token is a token of the 3840 + 256 workload whatever K is.  When K < 256 the
-whole 256-token decode is timed once more and reported as `decode_256`.
+3840..4095 (ctx 4096).  One step = one decode token.  The K timed steps run in
+segments: each restores the resident state (untimed) to the end of the prompt,
+takes the W warmup steps from there (untimed, positions 3840..3840+W-1) and
+times the next at most 256 - W steps, so every timed token is a token of the
+3840 + 256 workload whatever K is, and the timed steps follow warm ones.  The
+whole 256-token decode from 3840 is also timed once, right after a restore
+(cold), and reported as `decode_256`.
 
 Prints one JSON line: metric, value (tok/s), ms_per_step, roofline of the
 dominant kernel, the CPU baseline and prefill figures.
@@ -34,8 +36,10 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
 # HBM bytes per k_gateup8f launch from two rocprofv3 PMC passes over this bench
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the scales are what the two
-# counters read for a plain 512 MiB copy): 1.018 x the algorithmic 24 155 264 bytes.
-GATEUP_TRAFFIC_BYTES = 24588390
+# counters read for a plain 512 MiB copy), and the SHA-256 of the decode code object
+# those passes ran: the figure is reported only for that same code object.
+GATEUP_TRAFFIC_BYTES = 24579566
+GATEUP_TRAFFIC_CODE_OBJECT = "8811cb1f1cca27291a5f24a1697419fe636acd2f16ea651118f6e10bf9b570ce"
 SEED = 0x9E3779B97F4A7C15
 CTX = 4096          # context of the workload (positions 0..4095)
 N_PROMPT = 3840     # prompt tokens prefilled before decode
@@ -110,6 +114,13 @@ def prefill_flops(hp, n):
             macs += n * (hp.n_expert * dim + hp.n_used * 3 * hp.expert_ff * dim)
     macs += hp.vocab * dim
     return 2 * macs
+
+
+def code_object_sha256():
+    import hashlib
+    path = os.path.join(REPO, "lfm2-w9100-rust_amd", "lfm_kernels.hsaco")
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
 
 
 def matvec_roofline(iters=200):
@@ -288,9 +299,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-decode-256", action="store_true",
-                    help="when --steps < 256, skip the extra untimed-for-value full 256-token "
-                         "decode pass (rocprofv3 kernel tracing faults on a host-side buffer over "
-                         "one 256-replay decode call; traced runs use --steps 64 and this flag)")
+                    help="skip the extra full 256-token decode pass reported as decode_256 (not part "
+                         "of value; traced runs use it: a rocprofv3 kernel trace once faulted on a "
+                         "host-side buffer inside one 256-replay decode call)")
     ap.add_argument("--synthetic-state", action="store_true",
                     help="skip the prefill: restore a seeded binary16 KV / conv state for the "
                          "prompt positions instead (isolates decode kernels for profiling)")
@@ -330,28 +341,34 @@ def main():
         f"{prefill_s * 1e3:.1f} ms")
     snap = eng.snapshot_resident_cache(n_prompt)
 
-    if args.warmup > 0:
-        eng.decode_run(first, n_prompt, min(args.warmup, CTX - n_prompt), eos=1 << 31)
-    # timed: K steps from position 3840, restoring the prompt state before each run
+    if args.warmup >= CTX - n_prompt:
+        sys.exit(f"--warmup must leave decode positions: at most {CTX - n_prompt - 1}")
+    # timed: K steps in runs that each restore the prompt state, take the W warmup
+    # steps from it (untimed) and time the steps that follow
     toks, dt, fdt = [], 0.0, None
-    for seg in decode_segments(args.steps):
+    t_start = n_prompt + args.warmup  # first timed position
+    for seg in decode_segments(args.steps, start=t_start):
         eng.restore_session(n_prompt, snap)
+        warm, feed = [], first
+        if args.warmup:
+            warm = eng.decode_run(first, n_prompt, args.warmup, eos=1 << 31)
+            feed = warm[-1]
         lfm_hip.lib().lfm_dev_synchronize()
         t0 = time.perf_counter()
-        out = eng.decode_run(first, n_prompt, seg, eos=1 << 31)
+        out = eng.decode_run(feed, t_start, seg, eos=1 << 31)
         lfm_hip.lib().lfm_dev_synchronize()
         sdt = time.perf_counter() - t0
         dt += sdt
-        assert len(out) == seg
+        assert len(warm) == args.warmup and len(out) == seg
         if not toks:
-            toks = out
-            if seg == DECODE_TOKENS:
+            toks = warm + out  # the tokens of positions 3840 ..
+            if args.warmup == 0 and seg == DECODE_TOKENS:
                 fdt = sdt
-        elif out != toks[:seg]:
+        elif warm + out != toks[:args.warmup + seg]:
             raise RuntimeError("decode from the same state gave different tokens")
     ms_per_step = dt * 1e3 / args.steps
     tok_s = args.steps / dt
-    timed_pos = range(n_prompt, n_prompt + min(args.steps, CTX - n_prompt))
+    timed_pos = range(t_start, t_start + min(args.steps, CTX - t_start))
     wbytes, kvbytes = decode_bytes_per_token(hp, timed_pos)
     decode_gbs = (wbytes + kvbytes) * tok_s / 1e9
     log(f"[bench] decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tok_s:.1f} tok/s, "
@@ -398,8 +415,14 @@ def main():
         # MoE layers' experts
         us, nbytes = eng.time_moe_gateup(reps=10)
         gbs = nbytes / (us * 1e-6) / 1e9
+        same_build = code_object_sha256() == GATEUP_TRAFFIC_CODE_OBJECT
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": GATEUP_TRAFFIC_BYTES if same_build else None,
+                "traffic_source": "profiles/k_gateup_traffic.md, FETCH_SIZE / WRITE_SIZE passes over this "
+                                  "code object (sha256 " + GATEUP_TRAFFIC_CODE_OBJECT[:12] + ")"
+                                  if same_build else "null: the code object differs from the one the "
+                                  "PMC passes measured",
                 "kernel": "k_gateup8f (MoE router total + top-4 + routed gate+up+SwiGLU, "
                           "4 experts x 2 x 1792x2048 Q6_K)",
                 "algorithmic_bytes": nbytes, "us_per_launch": round(us, 3),
@@ -449,8 +472,9 @@ def main():
         "data": "synthetic (seeded random-init Q6_K weights and prompt ids)",
         "config": {"workload": f"prefill {n_prompt} + {DECODE_TOKENS} greedy decode steps at "
                                f"ctx {CTX} (LFM2.5-8B-A1B-shaped Q6_K token loop, bs=1)",
-                   "timed_steps": f"{args.steps} decode tokens from position {n_prompt}, in runs "
-                                  f"of at most {CTX - n_prompt} from the restored prompt state",
+                   "timed_steps": f"{args.steps} decode tokens from position {t_start}, in runs of at "
+                                  f"most {CTX - t_start}, each after restoring the prompt state and "
+                                  f"{args.warmup} untimed steps from it",
                    "layers": 24, "conv_layers": 18, "attention_layers": 6, "vocab": hp.vocab,
                    "experts": "32 top-4", "ctx": CTX, "parallelism": "single GPU"},
         "roofline": roof, "cpu_baseline": cpu,

@@ -2336,8 +2336,9 @@ extern "C" int lfm_engine_time_moe_gateup(lfm_engine *e, uint32_t reps, float *u
     // router inputs (partial sums, or logits) and bias + output
     const uint64_t wbytes = 2ull * hp.n_used * hp.expert_ff * (hp.dim / 256) * 210;
     const uint64_t rbytes = fused ? (uint64_t)(ROUTE_EXPERTS + 1) * ROUTE_PARTS * 4 : hp.n_expert * 4ull;
+    // ... and the layer's routing record (ids and weights, logits and scores)
     *bytes_per_launch = wbytes + (fused ? 1ull : 2ull) * hp.dim * 4 + rbytes + hp.n_expert * 4ull +
-                        (uint64_t)hp.n_used * hp.expert_ff * 4;
+                        (uint64_t)hp.n_used * hp.expert_ff * 4 + (16ull + 2ull * hp.n_expert) * 4;
     return LFM_OK;
 }
 

@@ -18,6 +18,15 @@ def test_decode_segments_stay_below_ctx(steps, want):
     assert all(bench.N_PROMPT + s <= bench.CTX for s in segs)
 
 
+@pytest.mark.parametrize("steps,warmup,want", [(20, 5, [20]), (256, 8, [248, 8]), (251, 5, [251])])
+def test_decode_segments_after_warmup(steps, warmup, want):
+    """Each timed run follows W untimed steps from the restored prompt state, so
+    it starts at 3840 + W and still stays below ctx."""
+    segs = bench.decode_segments(steps, start=bench.N_PROMPT + warmup)
+    assert segs == want and sum(segs) == steps
+    assert all(bench.N_PROMPT + warmup + s <= bench.CTX for s in segs)
+
+
 def test_decode_segments_small_ctx():
     assert bench.decode_segments(10, start=60, ctx=64) == [4, 4, 2]
     with pytest.raises(ValueError):
