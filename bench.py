@@ -142,6 +142,38 @@ def matvec_roofline(iters=200):
     return algo, ms_hbm, ms_mall
 
 
+def full_scale_prefill(hp, prompt):
+    """The same prompt through a model whose Q6_K sub-block scales span the whole
+    int8 range with one -128 per super-block, as model files have them: its GEMMs
+    run the split-scale kernels (exact binary16 weights for every scale)."""
+    e = lfm_hip.GpuEngine.load_synthetic(hp, lfm_hip.synth_opts(SEED, full_scales=1), ctx=CTX,
+                                         threads=16)
+    e.forward(prompt[:256], 0)  # untimed: first launches
+    e.reset_session()
+    lfm_hip.lib().lfm_dev_synchronize()
+    t = time.perf_counter()
+    logits = e.forward(prompt, 0)
+    lfm_hip.lib().lfm_dev_synchronize()
+    whole = time.perf_counter() - t
+    e.reset_session()
+    lfm_hip.lib().lfm_dev_synchronize()
+    t = time.perf_counter()
+    for s0 in range(0, len(prompt), 64):
+        nxt = e.forward_token(prompt[s0:s0 + 64], s0)
+    lfm_hip.lib().lfm_dev_synchronize()
+    chunked = time.perf_counter() - t
+    e.close()
+    flops = prefill_flops(hp, len(prompt))
+    return {"tokens": len(prompt), "ms": round(whole * 1e3, 1), "tok_s": round(len(prompt) / whole, 1),
+            "algorithmic_tflops": round(flops / whole / 1e12, 1),
+            "mfma_frac": round(flops / whole / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "chunked_ms": round(chunked * 1e3, 1),
+            "next_token_equals_whole_prompt": nxt == int(np.argmax(logits)),
+            "note": "synthetic weights with int8 sub-block scales over the whole range (one -128 per "
+                    "super-block): the GEMMs run the split-scale kernels, four matrix-core passes "
+                    "per product"}
+
+
 # ---------------------------------------------------------------- CPU baseline
 def _timed(fn, min_s, max_reps):
     """Mean seconds per call of fn() over at least one call, repeated until
@@ -302,6 +334,8 @@ def main():
                     help="skip the extra full 256-token decode pass reported as decode_256 (not part "
                          "of value; traced runs use it: a rocprofv3 kernel trace once faulted on a "
                          "host-side buffer inside one 256-replay decode call)")
+    ap.add_argument("--no-full-scale", action="store_true",
+                    help="skip the second prefill figure (the model with full-range int8 scales)")
     ap.add_argument("--synthetic-state", action="store_true",
                     help="skip the prefill: restore a seeded binary16 KV / conv state for the "
                          "prompt positions instead (isolates decode kernels for profiling)")
@@ -458,6 +492,11 @@ def main():
     # the engine is released here, while the runtime (and a tracer attached to
     # it) is up, not by its finalizer at interpreter exit
     eng.close()
+    full_scale = None
+    if not args.synthetic_state and not args.no_full_scale:
+        full_scale = full_scale_prefill(hp, prompt)
+        log(f"[bench] full-range scales: prefill {n_prompt} tokens {full_scale['ms']} ms, in 64-token "
+            f"chunks {full_scale['chunked_ms']} ms")
     cpu = None
     if not args.no_cpu_baseline:
         log(f"[bench] cpu baseline (oracle) on {cores} threads ...")
@@ -490,6 +529,7 @@ def main():
             "note": "algorithmic FLOPs (projections, router, causal attention, last-token head); "
                     "each GEMM product runs as two binary16 matrix-core passes (hi, lo)"},
         "prefill_chunked": chunked,
+        "prefill_full_int8_scales": full_scale,
         **extra,
     }
     print(json.dumps(line), flush=True)

@@ -274,6 +274,10 @@ typedef struct lfm_synth_opts {
     float router_sigma; /* ffn_gate_inp ~ N(0, router_sigma)                      */
     float bias_sigma;   /* exp_probs_b ~ N(0, bias_sigma); 0 => zeros            */
     float conv_sigma;   /* shortconv.conv ~ N(0, conv_sigma)                      */
+    uint32_t full_scales; /* 0: Q6_K sub-block scales uniform in [-32, 31]; 1: over the
+                           * whole int8 range, one per super-block at -128 (the form
+                           * real model files have: ggml's quantizer maps each block's
+                           * largest-magnitude scale to -128)                      */
 } lfm_synth_opts;
 void lfm_synth_default_opts(lfm_synth_opts *o);
 int lfm_model_tensor_count(const lfm_hparams *hp);
@@ -286,6 +290,9 @@ int lfm_synth_tensor(const lfm_synth_opts *o, const lfm_tensor_desc *d, void *ou
 /* Uniform random Q6_K blocks / normal f32 values (seeded streams). */
 int lfm_synth_q6k_blocks(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
                          uint8_t *out, int threads);
+/* The same with the full_scales choice of lfm_synth_opts. */
+int lfm_synth_q6k_blocks_ex(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
+                            int full_scales, uint8_t *out, int threads);
 int lfm_synth_normal_f32(uint64_t seed, const char *stream, uint64_t n, float mean,
                          float sigma, float *out, int threads);
 /* Generate every tensor of the model and upload it (convenience for benches). */

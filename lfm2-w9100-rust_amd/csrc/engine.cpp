@@ -108,11 +108,12 @@ struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, split_rows_ext, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
-        tile_pack, gemm_q6_n64;
+        tile_pack, gemm_q6_n64, gemm_q6_x, gemm_swiglu_x, gemm_q6_t32x, gemm_swiglu_t32x;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f, conv_mixer, conv_mixer_r;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
+    uint32_t *wide = nullptr;    // k_q6_tile_pack's flag: a scale outside [-64, 64] was seen
 };
 
 // Shapes measured best on MI355X for the LFM2-8B widths; LFM_DECODE_SHAPES
@@ -242,7 +243,9 @@ static int get_kernels(Kernels **out)
                 {&k->gemm_q6_t32n1, "k_gemm_q6_t32n1"},
                 {&k->attn_merge_split, "k_attn_merge_split"}, {&k->reduce_combine, "k_reduce_combine"}, {&k->router_small, "k_router_prefill_small"},
                 {&k->embed_rows, "k_embed_rows"}, {&k->tile_pack, "k_q6_tile_pack"},
-                {&k->gemm_q6_n64, "k_gemm_q6_n64"}};
+                {&k->gemm_q6_n64, "k_gemm_q6_n64"}, {&k->gemm_q6_x, "k_gemm_q6_x"},
+                {&k->gemm_swiglu_x, "k_gemm_q6_swiglu_x"}, {&k->gemm_q6_t32x, "k_gemm_q6_t32x"},
+                {&k->gemm_swiglu_t32x, "k_gemm_q6_swiglu_t32x"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
         if (e != hipSuccess) {
@@ -254,7 +257,11 @@ static int get_kernels(Kernels **out)
     }
     set_shapes(k);
     if (hipMalloc(&k->idle_st, sizeof(DevState)) != hipSuccess ||
-        hipMemset(k->idle_st, 0, sizeof(DevState)) != hipSuccess) {
+        hipMemset(k->idle_st, 0, sizeof(DevState)) != hipSuccess || hipMalloc(&k->wide, 4) != hipSuccess) {
+        if (k->idle_st)
+            (void)hipFree(k->idle_st);
+        if (k->wide)
+            (void)hipFree(k->wide);
         (void)hipModuleUnload(k->mod);
         (void)hipModuleUnload(k->pmod);
         delete k;
@@ -263,6 +270,7 @@ static int get_kernels(Kernels **out)
     const int src = lfm_noalloc_setup(dev);
     if (src != LFM_OK) {
         (void)hipFree(k->idle_st);
+        (void)hipFree(k->wide);
         (void)hipModuleUnload(k->mod);
         (void)hipModuleUnload(k->pmod);
         delete k;
@@ -441,14 +449,20 @@ static int make_tiles(Kernels *K, hipStream_t s, const Q6T &src, uint32_t group_
         return fail(LFM_EDEVICE, "tile copy: device allocation of %llu bytes failed",
                     (unsigned long long)(ntb * TILE_BYTES));
     }
-    TilePackArgs a{src, (uint8_t *)*dev, group_rows, gtiles, (uint32_t)tiles};
-    const int rc = launch_t(K->tile_pack, dim3((uint32_t)ntb), 64, 0, s, a);
+    TilePackArgs a{src, (uint8_t *)*dev, group_rows, gtiles, (uint32_t)tiles, K->wide};
+    uint32_t wide = 0;
+    int rc = hipMemsetAsync(K->wide, 0, 4, s) == hipSuccess ? LFM_OK : fail(LFM_EDEVICE, "tile copy: flag reset");
+    if (rc == LFM_OK)
+        rc = launch_t(K->tile_pack, dim3((uint32_t)ntb), 64, 0, s, a);
+    if (rc == LFM_OK && (hipMemcpyAsync(&wide, K->wide, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                         hipStreamSynchronize(s) != hipSuccess))
+        rc = fail(LFM_EDEVICE, "tile copy: flag read");
     if (rc != LFM_OK) {
         (void)hipFree(*dev);
         *dev = nullptr;
         return rc;
     }
-    *out = Q6Tiles{(const uint8_t *)*dev, (uint32_t)tiles, src.nb, gtiles, group_rows};
+    *out = Q6Tiles{(const uint8_t *)*dev, (uint32_t)tiles, src.nb, gtiles, group_rows, wide ? 1u : 0u};
     return LFM_OK;
 }
 
@@ -627,16 +641,20 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     if (combined)
         *combined = false;
     const bool small = T <= GEMM_TOKENS;
+    // weights with scales outside [-64, 64] take the split-scale kernels (one 32-row
+    // tile per wave for small single-weight calls, 64 tokens per large workgroup)
+    const bool exact = g.w.wide || (pair && g.w2.wide);
     // small ungrouped projections of up to 3072 rows (q/k/v, the out projections):
     // one 32-row tile per wave
-    const bool one_tile = small && !pair && nz == 1 && g.zrows <= 3072;
+    const bool one_tile = small && !pair && (exact || (nz == 1 && g.zrows <= 3072));
     // large single-weight calls whose 128-token grid would not give each CU two
     // workgroups (few row tiles: the 2048- and 3072-row projections) take 64 tokens
     // per workgroup
     const dim3 g128 = gemm_grid(g.zrows, T, nz, GEMM_ROWS, GEMM_TOKENS);
-    const bool n64 = !small && !pair && (uint64_t)g128.x * g128.y * g128.z < GEMM_N64_BELOW;
+    const bool n64 = !small && !pair && (exact || (uint64_t)g128.x * g128.y * g128.z < GEMM_N64_BELOW);
+    const bool t64 = n64 || (!small && pair && exact);
     dim3 grid = gemm_grid(g.zrows, T, nz, pair || one_tile ? GEMM_ROWS / 2 : GEMM_ROWS,
-                          small ? 32 : n64 ? GEMM_TOKENS / 2 : GEMM_TOKENS);
+                          small ? 32 : t64 ? GEMM_TOKENS / 2 : GEMM_TOKENS);
     uint32_t S = 1;
     if (part && small) {
         const uint32_t wgs = grid.x * grid.y * grid.z;
@@ -647,8 +665,10 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         // four slices, the dense gate/up pair unsplit, the dense down at twelve)
         S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, std::min<size_t>(part_cap, GEMM_PART_SOFT) / per));
     }
-    hipFunction_t f = small ? (pair ? K->gemm_swiglu_t32 : one_tile ? K->gemm_q6_t32n1 : K->gemm_q6_t32)
-                            : (pair ? K->gemm_swiglu : n64 ? K->gemm_q6_n64 : K->gemm_q6);
+    hipFunction_t f = small ? (pair ? (exact ? K->gemm_swiglu_t32x : K->gemm_swiglu_t32)
+                                    : one_tile ? (exact ? K->gemm_q6_t32x : K->gemm_q6_t32n1) : K->gemm_q6_t32)
+                            : (pair ? (exact ? K->gemm_swiglu_x : K->gemm_swiglu)
+                                    : n64 ? (exact ? K->gemm_q6_x : K->gemm_q6_n64) : K->gemm_q6);
     if (deferred)
         *deferred = S;
     if (S == 1) {

@@ -300,12 +300,16 @@ struct Q6Tiles {
     uint32_t nb;     // Q6_K blocks per row
     uint32_t gtiles; // tiles per slice
     uint32_t rows;   // rows per slice (R)
+    uint32_t wide;   // some sub-block scale (of a block with d != 0) lies outside
+                     // [-64, 64]: its weights sc (q - 32) can exceed 2048 in
+                     // magnitude and need the GEMMs' split-scale (_x) kernels
 };
 
 struct TilePackArgs {   // row-major planes -> Q6Tiles
     Q6T src;            // groups * group_rows rows
     uint8_t *dst;
     uint32_t group_rows, gtiles, tiles;
+    uint32_t *wide;     // set to 1 when a scale outside [-64, 64] is seen (d != 0)
 };
 
 // C[slot(n)][col0 + r] (+)= scale[tok(n)] * sum_k W[z*zrows + r][k] * X[tok(n)][k]

@@ -596,6 +596,15 @@ extern "C" __global__ __launch_bounds__(64) void k_q6_tile_pack(const TilePackAr
     const bool dz = (vd & 0x7FFFu) == 0;
     const uint2 vb = dz ? make_uint2(0x80808080u, 0x80808080u) : make_uint2(vs.x ^ 0x80808080u, vs.y ^ 0x80808080u);
     *reinterpret_cast<uint2 *>(d + ntb * (TILE_QL + TILE_QH) + tb * TILE_SC + p * 256 + r * 8) = vb;
+    // a stored byte b = sc + 128 outside [64, 192] is a scale outside [-64, 64]
+    bool wide = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t byte = ((i < 4 ? vb.x : vb.y) >> (8 * (i & 3))) & 0xFFu;
+        wide = wide || byte < 64u || byte > 192u;
+    }
+    if (__ballot(wide) != 0 && l == 0)
+        __hip_atomic_store(a.wide, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (p == 0)
         reinterpret_cast<uint16_t *>(d + ntb * (TILE_QL + TILE_QH + TILE_SC) + tb * TILE_D)[r] = vd;
 }
@@ -612,6 +621,25 @@ __device__ __forceinline__ StageScales stage_scales(uint32_t sc, int q)
     const uint32_t v = __builtin_amdgcn_perm(sc, 0x64646464u, q ? 0x01070006u : 0x01050004u);
     const half2v s = __builtin_bit_cast(half2v, v) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f};
     return {s, s * (half2v){(_Float16)-288.0f, (_Float16)-288.0f}};
+}
+
+// The split form of the stage's scales, for weights whose products sc (q6 - 32)
+// can exceed 2048 in magnitude (a binary16 holds every integer up to 2048 only):
+// sc = sh + sl with sh = sc & ~15 (a multiple of 16) and sl = sc & 15, formed from
+// the stored byte b = sc + 128 as (b & 0xF0) - 128 and b & 15.  Both partial
+// weights are exact binary16 values for every int8 scale: sh (q6 - 32) is 16
+// times an integer of magnitude <= 256, and |sl (q6 - 32)| <= 480; so are the
+// biases -288 sh (= -9 (sh / 16) 512) and -288 sl.
+struct SplitScales {
+    half2v sh, sl;
+};
+__device__ __forceinline__ SplitScales stage_scales_split(uint32_t sc, int q)
+{
+    const uint32_t sel = q ? 0x01070006u : 0x01050004u;
+    const uint32_t vh = __builtin_amdgcn_perm(sc & 0xF0F0F0F0u, 0x64646464u, sel);
+    const uint32_t vl = __builtin_amdgcn_perm(sc & 0x0F0F0F0Fu, 0x64646464u, sel);
+    return {__builtin_bit_cast(half2v, vh) - (half2v){(_Float16)1152.0f, (_Float16)1152.0f},
+            __builtin_bit_cast(half2v, vl) - (half2v){(_Float16)1024.0f, (_Float16)1024.0f}};
 }
 
 // The 8 binary16 weights sc * (q6 - 32) of sub-block s (0..3) of a chunk, in MFMA
@@ -703,7 +731,11 @@ __device__ __forceinline__ void store_rows16(float *out, uint32_t rb, uint32_t z
     }
 }
 
-template <bool PAIR, int NJ>
+// EXACT: the weights are formed with the split scales (stage_scales_split), two
+// A fragments per chunk and sub-block, each multiplied by the hi and lo
+// activation halves: four matrix-core products per k-step instead of two, and
+// exact binary16 weights whatever the scales (the _x kernels).
+template <bool PAIR, int NJ, bool EXACT = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs &a)
 {
     constexpr uint32_t TNW = 32 * NJ; // token columns per workgroup (128, or 32 for small calls)
@@ -842,6 +874,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
             if ((hb & 1) == 0 && hb + 2 < nhb)
                 dnext = loadD((hb >> 1) + 1);
         }
+        if constexpr (!EXACT) {
         // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
         half2v ss[2][2];
 #pragma unroll
@@ -883,6 +916,59 @@ __device__ __forceinline__ void gemm_body(const GemmArgs &a)
                 for (int i = 0; i < 2; ++i)
                     afc[i] = afn[i];
             }
+        }
+        } else {
+        SplitScales sp[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch)
+                sp[i][ch] = stage_scales_split(A[i][ch].sc, q);
+        half8 afh[2], afl[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            afh[i] = decode_frag(A[i][0], 2 * q, sp[i][0].sh);
+            afl[i] = decode_frag(A[i][0], 2 * q, sp[i][0].sl);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t kp = ks * 2 + p;
+            half8 anh[2], anl[2], bfh[2], bfl[2];
+            bfh[0] = lds_frag(bh, swz(lr, kp));
+            bfl[0] = lds_frag(bl, swz(lr, kp));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if (j + 1 < NJ) {
+                    bfh[(j + 1) & 1] = lds_frag(bh, swz((j + 1) * 32 + lr, kp));
+                    bfl[(j + 1) & 1] = lds_frag(bl, swz((j + 1) * 32 + lr, kp));
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afh[i], bfh[j & 1], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bfh[j & 1], acc[i][j], 0, 0, 0);
+                }
+                if (j == 1 && ks < 3) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const SplitScales &n = sp[i][(ks + 1) & 1];
+                        anh[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), n.sh);
+                        anl[i] = decode_frag(A[i][(ks + 1) & 1], 2 * q + ((ks + 1) >> 1), n.sl);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afh[i], bfl[j & 1], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bfl[j & 1], acc[i][j], 0, 0, 0);
+                }
+            }
+            if (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    afh[i] = anh[i];
+                    afl[i] = anl[i];
+                }
+            }
+        }
         }
         if (q == 0 && (hb & 1) && hb + 1 < nhb) // stage 4kb + 2: publish block kb + 1's scale
             set_d(((hb >> 1) + 1) & 1, dnextf);
@@ -987,6 +1073,20 @@ k_gemm_q6_swiglu(const GemmArgs a)
     gemm_body<true, 4>(a);
 }
 
+// Split-scale forms (weights with some |sc| > 64): 64 token columns per workgroup,
+// so that the second set of weight fragments fits the registers.
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6_x(const GemmArgs a)
+{
+    gemm_body<false, 2, true>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_q6_swiglu_x(const GemmArgs a)
+{
+    gemm_body<true, 2, true>(a);
+}
+
 // The same products for calls of up to 128 tokens (chunked prefill: about 8
 // tokens per expert at 64 tokens), 32 tokens per workgroup: a quarter of the
 // padded matrix-core work, and every wave runs on its own.  A lane loads its
@@ -996,7 +1096,8 @@ k_gemm_q6_swiglu(const GemmArgs a)
 // so there is no LDS tile and no barrier, and each wave waits only for the
 // loads its next instructions use.  Same arithmetic per (row, token) as
 // gemm_body.  NI: 32-row tiles per wave (the pair form: its gate and up tile).
-template <bool PAIR, int NI, int G>
+// EXACT: split-scale weights as in gemm_body (the _x kernels).
+template <bool PAIR, int NI, int G, bool EXACT = false>
 __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 {
     static_assert(!PAIR || NI == 2, "the pair form holds a gate and an up tile per wave");
@@ -1148,9 +1249,11 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         issue_fence();
         const int q = j & 1;
         AChunk (&A)[NI][2] = W[j >> 1];
-        half8 afc[NI], bch[4], bcl[4];
+        half8 bch[4], bcl[4];
         // k-step kq reads k-piece 2 kq + p of row lr
         lds_frags_issue(lds_addr(Bs[st % NBUF]) + (p * 256 + lr * 8) * 2, bch, bcl);
+        if constexpr (!EXACT) {
+        half8 afc[NI];
         // the stage's scales: sub-blocks 2q, 2q + 1 of each chunk
         StageScales ss[NI][2];
 #pragma unroll
@@ -1181,6 +1284,50 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                 for (int i = 0; i < NI; ++i)
                     afc[i] = afn[i];
             }
+        }
+        } else {
+        half8 afh[NI], afl[NI];
+        SplitScales sp[NI][2];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch)
+                sp[i][ch] = stage_scales_split(A[i][ch].sc, q);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            afh[i] = decode_frag(A[i][0], 2 * q, sp[i][0].sh);
+            afl[i] = decode_frag(A[i][0], 2 * q, sp[i][0].sl);
+        }
+        lds_frags_wait(bch, bcl);
+#pragma unroll
+        for (int kq = 0; kq < 4; ++kq) {
+            half8 anh[NI], anl[NI];
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afh[i], bch[kq], acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bch[kq], acc[i], 0, 0, 0);
+            }
+            if (kq < 3) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    const SplitScales &n = sp[i][(kq + 1) & 1];
+                    anh[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), n.sh);
+                    anl[i] = decode_frag(A[i][(kq + 1) & 1], 2 * q + ((kq + 1) >> 1), n.sl);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afh[i], bcl[kq], acc[i], 0, 0, 0);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bcl[kq], acc[i], 0, 0, 0);
+            }
+            if (kq < 3) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    afh[i] = anh[i];
+                    afl[i] = anl[i];
+                }
+            }
+        }
         }
         if (G == 2 && (j & 1) && st + 1 < nst) {
             // Stages st + 1 and st + 2 have their tiles and weights, and every wave is
@@ -1321,6 +1468,18 @@ extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32(cons
 extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32n1(const GemmArgs a)
 {
     gemm_small_body<false, 1, 2>(a); // three workgroups per CU: 6 tile buffers fit their LDS
+}
+
+// Split-scale forms (weights with some |sc| > 64): one 32-row tile per wave for
+// single weights, the gate and up tiles for the pair.
+extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_t32x(const GemmArgs a)
+{
+    gemm_small_body<false, 1, 2, true>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) void k_gemm_q6_swiglu_t32x(const GemmArgs a)
+{
+    gemm_small_body<true, 2, 4, true>(a);
 }
 
 // Sums the K slices of a split GEMM in slice order and applies its epilogue:

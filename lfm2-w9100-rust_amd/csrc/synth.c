@@ -7,7 +7,10 @@
  *
  * Tensor names/shapes follow the reference's model (engine/src/lfm.rs:330-669,
  * resident_graph.rs:237-503).  Distributions:
- *   Q6_K weights : ql/qh uniform bytes, int8 scales uniform in [-32, 31],
+ *   Q6_K weights : ql/qh uniform bytes, int8 scales uniform in [-32, 31]
+ *                  (full_scales: uniform in [-127, 127] with one sub-block of
+ *                  each super-block at -128, the form ggml's Q6_K quantizer
+ *                  writes: the largest-magnitude scale maps to -128),
  *                  d = binary16(N(0, d_sigma))
  *   norms        : 1 + N(0, norm_sigma)           router: N(0, router_sigma)
  *   expert bias  : N(0, bias_sigma) (zeros if 0)  conv  : N(0, conv_sigma)
@@ -102,7 +105,7 @@ static void normal_pair(uint64_t *s, double *z0, double *z1)
     *z1 = r * sin(t);
 }
 
-static void q6k_block(uint64_t tseed, uint64_t b, float d_sigma, uint8_t *out)
+static void q6k_block(uint64_t tseed, uint64_t b, float d_sigma, int full, uint8_t *out)
 {
     uint64_t s = tseed + (b + 1) * 0xD1B54A32D192ED03ull;
     for (int i = 0; i < 24; ++i) {
@@ -112,9 +115,13 @@ static void q6k_block(uint64_t tseed, uint64_t b, float d_sigma, uint8_t *out)
     }
     for (int i = 0; i < 2; ++i) {
         const uint64_t v = sm_next(&s);
-        for (int k = 0; k < 8; ++k)
-            out[192 + i * 8 + k] = (uint8_t)(int8_t)((int)((v >> (8 * k)) & 63u) - 32);
+        for (int k = 0; k < 8; ++k) {
+            const int byte = (int)((v >> (8 * k)) & 255u);
+            out[192 + i * 8 + k] = (uint8_t)(int8_t)(full ? byte % 255 - 127 : (byte & 63) - 32);
+        }
     }
+    if (full)
+        out[192 + (sm_next(&s) & 15u)] = (uint8_t)(int8_t)-128;
     double z0, z1;
     normal_pair(&s, &z0, &z1);
     const uint16_t d = lfm_f32_to_f16((float)(d_sigma * z0));
@@ -123,7 +130,7 @@ static void q6k_block(uint64_t tseed, uint64_t b, float d_sigma, uint8_t *out)
 }
 
 typedef struct job {
-    int kind; /* 0 q6k, 1 normal */
+    int kind; /* 0 q6k, 1 normal, 2 q6k with full-range scales */
     uint64_t tseed, begin, end;
     float a, b; /* q6k: d_sigma; normal: mean, sigma */
     void *out;
@@ -131,9 +138,9 @@ typedef struct job {
 
 static void run_job(job *j)
 {
-    if (j->kind == 0) {
+    if (j->kind == 0 || j->kind == 2) {
         for (uint64_t b = j->begin; b < j->end; ++b)
-            q6k_block(j->tseed, b, j->a, (uint8_t *)j->out + b * 210);
+            q6k_block(j->tseed, b, j->a, j->kind == 2, (uint8_t *)j->out + b * 210);
     } else {
         float *o = (float *)j->out;
         for (uint64_t k = j->begin; k < j->end; ++k) { /* k = pair index */
@@ -178,14 +185,20 @@ static void run_parallel(job proto, uint64_t n, int threads)
         pthread_join(tid[t], NULL);
 }
 
-int lfm_synth_q6k_blocks(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
-                         uint8_t *out, int threads)
+int lfm_synth_q6k_blocks_ex(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
+                            int full_scales, uint8_t *out, int threads)
 {
     if (!stream || !out)
         return LFM_EINVAL;
-    job j = {0, stream_seed(seed, stream), 0, 0, d_sigma, 0.f, out};
+    job j = {full_scales ? 2 : 0, stream_seed(seed, stream), 0, 0, d_sigma, 0.f, out};
     run_parallel(j, nblocks, threads);
     return LFM_OK;
+}
+
+int lfm_synth_q6k_blocks(uint64_t seed, const char *stream, uint64_t nblocks, float d_sigma,
+                         uint8_t *out, int threads)
+{
+    return lfm_synth_q6k_blocks_ex(seed, stream, nblocks, d_sigma, 0, out, threads);
 }
 
 int lfm_synth_normal_f32(uint64_t seed, const char *stream, uint64_t n, float mean, float sigma,
@@ -214,6 +227,7 @@ void lfm_synth_default_opts(lfm_synth_opts *o)
     o->router_sigma = 0.02f;
     o->bias_sigma = 0.0f;
     o->conv_sigma = 0.1f;
+    o->full_scales = 0;
 }
 
 static int layer_tensor_count(const lfm_hparams *hp, uint32_t l)
@@ -378,7 +392,8 @@ int lfm_synth_tensor(const lfm_synth_opts *o, const lfm_tensor_desc *d, void *ou
     if (d->ggml_type == LFM_GGML_TYPE_Q6_K) {
         if (d->ne[0] % 256)
             return LFM_EINVAL;
-        return lfm_synth_q6k_blocks(o->seed, d->name, nbytes / 210, o->d_sigma, (uint8_t *)out, threads);
+        return lfm_synth_q6k_blocks_ex(o->seed, d->name, nbytes / 210, o->d_sigma, (int)o->full_scales,
+                                       (uint8_t *)out, threads);
     }
     const uint64_t n = nbytes / 4;
     switch (d->kind) {

@@ -70,6 +70,7 @@ class SynthOpts(C.Structure):
     _fields_ = [
         ("seed", C.c_uint64), ("d_sigma", C.c_float), ("norm_sigma", C.c_float),
         ("router_sigma", C.c_float), ("bias_sigma", C.c_float), ("conv_sigma", C.c_float),
+        ("full_scales", C.c_uint32),
     ]
 
 
@@ -178,6 +179,7 @@ def lib():
         "lfm_tensor_nbytes": (sz, [C.POINTER(TensorDesc)]),
         "lfm_synth_tensor": (i32, [C.POINTER(SynthOpts), C.POINTER(TensorDesc), P, sz, i32]),
         "lfm_synth_q6k_blocks": (i32, [u64, C.c_char_p, u64, f32, P, i32]),
+        "lfm_synth_q6k_blocks_ex": (i32, [u64, C.c_char_p, u64, f32, i32, P, i32]),
         "lfm_synth_normal_f32": (i32, [u64, C.c_char_p, u64, f32, f32, P, i32]),
         "lfm_engine_load_synthetic": (i32, [P, C.POINTER(SynthOpts), i32]),
         "lfm_f32_to_f16": (C.c_uint16, [f32]), "lfm_f16_to_f32": (f32, [C.c_uint16]),
@@ -275,10 +277,10 @@ def synth_tensor(desc: TensorDesc, opts: Optional[SynthOpts] = None, threads: in
 
 
 def synth_q6k_blocks(seed: int, stream: str, nblocks: int, d_sigma: float = 1e-3,
-                     threads: int = 8) -> np.ndarray:
+                     threads: int = 8, full_scales: bool = False) -> np.ndarray:
     out = np.empty(nblocks * Q6_K_BYTES, dtype=np.uint8)
-    _check(lib().lfm_synth_q6k_blocks(seed, stream.encode(), nblocks, d_sigma, out.ctypes.data,
-                                      threads))
+    _check(lib().lfm_synth_q6k_blocks_ex(seed, stream.encode(), nblocks, d_sigma, int(full_scales),
+                                         out.ctypes.data, threads))
     return out
 
 

@@ -80,3 +80,16 @@ def test_model_tensor_table(lfm):
     q6 = sum(lfm.lib().lfm_tensor_nbytes(d) for d in descs if d.ggml_type == 14)
     # 6.84 GB model; decode streams every Q6 weight except the unused experts
     assert 6.8e9 < total < 6.9e9 and q6 > 0.99 * total
+
+
+def test_full_scale_blocks(lfm):
+    """The full-scale synthetic blocks: scales in [-127, 127] plus exactly one -128
+    per super-block (ggml's quantizer maps a block's largest-magnitude scale to
+    -128), the other bytes as in the default stream's layout."""
+    raw = lfm.synth_q6k_blocks(7, "full.test", 4096, full_scales=True).reshape(-1, 210)
+    sc = raw[:, 192:208].view(np.int8).astype(int)
+    assert (sc == -128).sum(axis=1).tolist() == [1] * 4096
+    assert sc.max() <= 127 and (np.abs(sc) > 64).mean() > 0.4
+    default = lfm.synth_q6k_blocks(7, "full.test", 4096).reshape(-1, 210)
+    assert np.array_equal(default[:, :192], raw[:, :192])  # same code bytes
+    assert np.abs(default[:, 192:208].view(np.int8).astype(int)).max() <= 32

@@ -184,3 +184,48 @@ def test_prefill_mixed_chunk_sizes(gpu, oracle, real_width):
     w = gpu_engine(hp, tensors, ctx=512)
     lw = w.forward(prompt, 0)
     assert rel_l2(lg, lw) <= 1e-3
+
+
+def test_prefill_full_int8_scales_model(gpu, oracle):
+    """A real-width model whose Q6_K weights use the whole int8 scale range, as
+    model files do (synthetic full_scales: one sub-block per super-block at -128).
+    Its GEMMs take the split-scale kernels, so the whole-prompt call (large-call
+    kernels, 300 tokens) and the same prompt in 64-token calls (small-call
+    kernels) stay as close to the decode graph's stepwise forward (weights formed
+    in fp32) as the synthetic model's prefill does, and match the oracle."""
+    hp = gpu.make_hparams(dim=2048, heads=32, n_layers=4, attention_layers=(1, 3), kv=8,
+                          vocab=4096, eos=1 << 30, n_expert=32, n_used=4, expert_ff=1792,
+                          n_ff=7168, dense_lead=1)
+    tensors = model_tensors(hp, gpu.synth_opts(0x5EED, full_scales=1))
+    raw = next(d for nm, _, _, d in tensors if nm == "blk.1.ffn_gate_exps.weight")
+    sc = raw.reshape(-1, 210)[:, 192:208].view(np.int8)
+    assert sc.min() == -128 and np.abs(sc.astype(int)).max() == 128
+    n = 300
+    prompt = [int(t) for t in np.random.default_rng(31).integers(0, hp.vocab, n)]
+    g = gpu_engine(hp, tensors, ctx=512)
+    lw = g.forward(prompt, 0)
+    sw = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    g.reset_session()
+    for s in range(0, n, 64):
+        g.forward_token(prompt[s:s + 64], s)
+    lc = g.snapshot_resident_logits()
+    sc_ = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    g.reset_session()
+    g.set_prefill_mode(True)
+    ls = g.forward(prompt, 0)
+    ss = np.frombuffer(g.snapshot_resident_cache(n), np.float32)
+    g.close()
+    o = oracle_engine(oracle, hp, tensors, ctx=512)
+    lo = o.forward(prompt, 0)
+    so = np.frombuffer(o.snapshot(n), np.float32)
+    o.close()
+    e = {"whole vs stepwise": (rel_l2(lw, ls), rel_l2(sw, ss)),
+         "chunked vs stepwise": (rel_l2(lc, ls), rel_l2(sc_, ss)),
+         "whole vs oracle": (rel_l2(lw, lo), rel_l2(sw, so)),
+         "stepwise vs oracle": (rel_l2(ls, lo), rel_l2(ss, so))}
+    print("full-scale model, logits / state rel-L2: "
+          + "; ".join(f"{k} {a:.2e} / {b:.2e}" for k, (a, b) in e.items()))
+    for k in ("whole vs stepwise", "chunked vs stepwise"):  # measured <= 3e-6
+        assert e[k][0] <= 2e-5 and e[k][1] <= 2e-5, (k, e[k])
+    for k in ("whole vs oracle", "stepwise vs oracle"):
+        assert e[k][0] <= 1e-3 and e[k][1] <= 1e-3, (k, e[k])
