@@ -142,17 +142,21 @@ def test_prefill_chunks_repeat_bit_exact(gpu, real_width):
     """Small calls take each token's slot in its experts' lists with an atomic add,
     so a token's row may sit elsewhere in its expert's tile from one run to the
     next; what is computed for it must not change: two engines prefilling the
-    same 192 tokens in 64-token calls give bit-identical logits and state."""
+    same 192 tokens in 64-token calls, then 300 more in one large call, give
+    bit-identical logits and state."""
     hp, tensors = real_width
-    prompt = [int(t) for t in np.random.default_rng(17).integers(0, hp.vocab, 192)]
+    prompt = [int(t) for t in np.random.default_rng(17).integers(0, hp.vocab, 492)]
     outs = []
     for _ in range(2):
         g = gpu_engine(hp, tensors, ctx=512)
         for s in range(0, 192, 64):
             lg = g.forward(prompt[s:s + 64], s)
-        outs.append((lg.view(np.uint32).copy(), np.frombuffer(g.snapshot_resident_cache(192), np.uint32).copy()))
-    assert np.array_equal(outs[0][0], outs[1][0])
-    assert np.array_equal(outs[0][1], outs[1][1])
+        lw = g.forward(prompt[192:], 192)
+        outs.append((lg.view(np.uint32).copy(), np.frombuffer(g.snapshot_resident_cache(192), np.uint32).copy(),
+                     lw.view(np.uint32).copy(), np.frombuffer(g.snapshot_resident_cache(492), np.uint32).copy()))
+        g.close()
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
 
 
 def test_prefill_mixed_chunk_sizes(gpu, oracle, real_width):
