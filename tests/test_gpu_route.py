@@ -94,3 +94,76 @@ def test_fused_and_unfused_routers_agree(gpu, oracle):
         if srt[3] - srt[4] > ROUTE_MARGIN:
             assert fused[0] == plain[0], (i, fused, plain)
             assert np.allclose(fused[1], plain[1], rtol=0, atol=1e-6)
+
+
+def tied_router(tensors, hp, layer, rows):
+    """The tensors with layer `layer`'s router rows replaced by `rows` ([n_expert][dim])."""
+    name = f"blk.{layer}.ffn_gate_inp.weight"
+    out = []
+    for nm, t, shape, data in tensors:
+        if nm == name:
+            data = np.ascontiguousarray(rows, dtype=np.float32).reshape(-1)
+        out.append((nm, t, shape, data))
+    return out
+
+
+@pytest.mark.parametrize("n_expert", [4, 32, 64])
+def test_route_exact_ties(gpu, oracle, n_expert):
+    """The tie rule at exact ties, with 4, 32 and 64 experts, as the reference's
+    hardware check asks (resident_check.rs:35-84: stable ties, weights within 1e-6).
+    With every router row zero all scores are equal: ranks 0..3 are experts 0..3
+    and every weight is 1/4.  With row 2g + 1 a copy of row 2g the two scores are
+    bit-identical: expert 2g + 1 is never chosen without 2g and never ranks before
+    it, the two weights are equal, and the ids equal the oracle's (stable sort)
+    wherever the best excluded score of another pair is more than ROUTE_MARGIN
+    below the 4th.  32 experts at dim 2048 run the step's fused router
+    (lfm_engine_run_layer) and the separate one (lfm_engine_run_ffn); the other
+    counts run the separate one."""
+    dim = 2048 if n_expert == 32 else 256
+    hp = gpu.make_hparams(dim=dim, heads=dim // 64, n_layers=1, attention_layers=(), kv=8, vocab=256,
+                          eos=1 << 30, n_expert=n_expert, n_used=4,
+                          expert_ff=1792 if n_expert == 32 else 256, n_ff=256, dense_lead=0)
+    base = model_tensors(hp, gpu.synth_opts(SEED))
+    rng = np.random.default_rng(n_expert)
+    pairs = rng.normal(0.0, 0.1, (n_expert // 2, dim)).astype(np.float32)
+    cases = {"zero": np.zeros((n_expert, dim), np.float32), "pairs": np.repeat(pairs, 2, axis=0)}
+    for case, rows in cases.items():
+        tensors = tied_router(base, hp, 0, rows)
+        g = gpu_engine(hp, tensors, ctx=16)
+        o = oracle_engine(oracle, hp, tensors, ctx=16)
+        fused = g.fused_router(0)
+        assert fused == (n_expert == 32)
+        checked = 0
+        for i in range(60):
+            x = gpu.synth_normal(SEED + 3 * i, "route.ties", dim) * np.float32(10.0 ** ((i % 3) - 1))
+            routes = []
+            if fused:
+                _, x_mid = g.run_layer(0, x, 0)
+                routes.append(g.last_route())
+            else:
+                x_mid = x
+            g.run_ffn(0, x_mid)
+            routes.append(g.last_route())
+            ids_o, w_o, scores, _ = o.route_layer(0, x_mid)
+            for ids, w in routes:
+                if case == "zero":
+                    assert ids == [0, 1, 2, 3], (n_expert, i, ids)
+                    assert np.array_equal(w, np.full(4, 0.25, np.float32)), (n_expert, i, w)
+                    continue
+                for r, e in enumerate(ids):
+                    if e % 2:  # the odd expert of a pair only after its even twin
+                        assert e - 1 in ids[:r], (n_expert, i, ids)
+                        assert w[r] == w[ids.index(e - 1)], (n_expert, i, ids, w)
+                # the 4th pick against the best excluded expert of another pair
+                srt = sorted(range(n_expert), key=lambda e: (-float(scores[e]), e))
+                fourth = srt[3]
+                rest = [e for e in srt[4:] if e // 2 != fourth // 2]
+                if not rest or scores[fourth] - scores[rest[0]] > ROUTE_MARGIN:
+                    assert ids == ids_o, (n_expert, i, ids, ids_o)
+                    assert np.allclose(w, w_o, rtol=0, atol=1e-6), (n_expert, i, w, w_o)
+                    checked += 1
+        g.close()
+        o.close()
+        print(f"{n_expert} experts, {case} rows: {checked} routings compared with the oracle")
+        if case == "pairs":
+            assert checked >= 40
