@@ -113,7 +113,6 @@ struct Kernels {
         dequant, copy, matvec_route, gateup_f, conv_mixer, conv_mixer_r;
     Shape matvec, conv, qkv, gateup, head;
     DevState *idle_st = nullptr; // zeroed state for op-level matvecs (never halted)
-    uint32_t *wide = nullptr;    // k_q6_tile_pack's flag: a scale outside [-64, 64] was seen
 };
 
 // Shapes measured best on MI355X for the LFM2-8B widths; LFM_DECODE_SHAPES
@@ -257,11 +256,9 @@ static int get_kernels(Kernels **out)
     }
     set_shapes(k);
     if (hipMalloc(&k->idle_st, sizeof(DevState)) != hipSuccess ||
-        hipMemset(k->idle_st, 0, sizeof(DevState)) != hipSuccess || hipMalloc(&k->wide, 4) != hipSuccess) {
+        hipMemset(k->idle_st, 0, sizeof(DevState)) != hipSuccess) {
         if (k->idle_st)
             (void)hipFree(k->idle_st);
-        if (k->wide)
-            (void)hipFree(k->wide);
         (void)hipModuleUnload(k->mod);
         (void)hipModuleUnload(k->pmod);
         delete k;
@@ -270,7 +267,6 @@ static int get_kernels(Kernels **out)
     const int src = lfm_noalloc_setup(dev);
     if (src != LFM_OK) {
         (void)hipFree(k->idle_st);
-        (void)hipFree(k->wide);
         (void)hipModuleUnload(k->mod);
         (void)hipModuleUnload(k->pmod);
         delete k;
@@ -434,7 +430,9 @@ static Q6T q6view(const void *dev, uint64_t rows, uint64_t in_dim)
 }
 
 // The prefill GEMMs' copy of a row-major Q6_K matrix of src.rows / group_rows
-// slices in 32-row tiles (layout at Q6Tiles), written by k_q6_tile_pack on s.
+// slices in 32-row tiles (layout at Q6Tiles), written by k_q6_tile_pack on s.  The
+// kernel's wide-scale flag sits in the same allocation, past the tiles, so that
+// packs on other streams or threads (other engines, lfm_q6k_gemm) never share it.
 static int make_tiles(Kernels *K, hipStream_t s, const Q6T &src, uint32_t group_rows, void **dev, Q6Tiles *out)
 {
     *dev = nullptr;
@@ -444,17 +442,19 @@ static int make_tiles(Kernels *K, hipStream_t s, const Q6T &src, uint32_t group_
     const uint64_t tiles = (uint64_t)(src.rows / group_rows) * gtiles, ntb = tiles * src.nb;
     if (ntb > 0x7FFFFFFFull)
         return fail(LFM_EINVAL, "tile copy: %llu tile-blocks exceed the grid", (unsigned long long)ntb);
-    if (hipMalloc(dev, ntb * TILE_BYTES) != hipSuccess) {
+    const uint64_t bytes = ntb * TILE_BYTES, flag_at = (bytes + 255) / 256 * 256;
+    if (hipMalloc(dev, flag_at + 256) != hipSuccess) {
         *dev = nullptr;
         return fail(LFM_EDEVICE, "tile copy: device allocation of %llu bytes failed",
-                    (unsigned long long)(ntb * TILE_BYTES));
+                    (unsigned long long)(flag_at + 256));
     }
-    TilePackArgs a{src, (uint8_t *)*dev, group_rows, gtiles, (uint32_t)tiles, K->wide};
+    uint32_t *flag = reinterpret_cast<uint32_t *>((uint8_t *)*dev + flag_at);
+    TilePackArgs a{src, (uint8_t *)*dev, group_rows, gtiles, (uint32_t)tiles, flag};
     uint32_t wide = 0;
-    int rc = hipMemsetAsync(K->wide, 0, 4, s) == hipSuccess ? LFM_OK : fail(LFM_EDEVICE, "tile copy: flag reset");
+    int rc = hipMemsetAsync(flag, 0, 4, s) == hipSuccess ? LFM_OK : fail(LFM_EDEVICE, "tile copy: flag reset");
     if (rc == LFM_OK)
         rc = launch_t(K->tile_pack, dim3((uint32_t)ntb), 64, 0, s, a);
-    if (rc == LFM_OK && (hipMemcpyAsync(&wide, K->wide, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+    if (rc == LFM_OK && (hipMemcpyAsync(&wide, flag, 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
                          hipStreamSynchronize(s) != hipSuccess))
         rc = fail(LFM_EDEVICE, "tile copy: flag read");
     if (rc != LFM_OK) {
@@ -854,9 +854,8 @@ struct lfm_engine {
     uint32_t *sel = nullptr;        // routing records, ROUTE_REC_WORDS per layer
     uint32_t last_route_layer = 0;  // the MoE layer whose record was enqueued last
     // prefill routing log (lfm_engine_set_route_log): per layer and prompt
-    // position of the last multi-token call, ids[4] and weights[4], plus the
-    // router logits [n_expert] where the call computed them (calls over
-    // GEMM_TOKENS tokens); log_first[l] / log_n[l] give the token rows logged
+    // position of the last multi-token call, ids[4], weights[4] and the router
+    // logits [n_expert]; log_first[l] / log_n[l] give the token rows logged
     bool route_log = false;
     uint32_t *log_ids = nullptr;
     float *log_w = nullptr, *log_logits = nullptr;
@@ -2536,11 +2535,21 @@ extern "C" int lfm_engine_route_records(lfm_engine *e, uint32_t *words, size_t c
 extern "C" int lfm_engine_set_route_log(lfm_engine *e, int on)
 {
     RC(need_final(e));
-    if (on && !e->log_ids) {
+    if (on && !e->log_ids) { // all three buffers or none
         const size_t rows = (size_t)e->hp.n_layers * e->ctx;
-        HIPCHK(hipMalloc(&e->log_ids, rows * 16));
-        HIPCHK(hipMalloc(&e->log_w, rows * 16));
-        HIPCHK(hipMalloc(&e->log_logits, rows * e->hp.n_expert * 4));
+        uint32_t *ids = nullptr;
+        float *w = nullptr, *lg = nullptr;
+        if (hipMalloc(&ids, rows * 16) != hipSuccess || hipMalloc(&w, rows * 16) != hipSuccess ||
+            hipMalloc(&lg, rows * e->hp.n_expert * 4) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(ids);
+            (void)hipFree(w);
+            (void)hipFree(lg);
+            return fail(LFM_EDEVICE, "routing log: device allocation failed");
+        }
+        e->log_ids = ids;
+        e->log_w = w;
+        e->log_logits = lg;
         e->log_first.assign(e->hp.n_layers, 0u);
         e->log_n.assign(e->hp.n_layers, 0u);
         e->log_has_logits.assign(e->hp.n_layers, 0);
