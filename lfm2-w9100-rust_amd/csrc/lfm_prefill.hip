@@ -1677,8 +1677,13 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_rope_kv_prefill(const
 // v_mfma_f32_32x32x16_f16 on q split into binary16 hi + lo (K is binary16 in the
 // cache), so each lane holds one query's 16 scores: the online softmax (running
 // max m, sum l, fp32) needs only in-lane work and one swap across lane halves.
-// The lane's probabilities, split hi + lo, are exactly the B operand of
-// v_mfma_f32_32x32x8_f16 for O^T += V^T P^T.  out = O / l.
+// The lane's probabilities, split hi + lo, feed O^T += V^T P^T on the same
+// 32x32x16 MFMA: for keys 16 G .. 16 G + 15, lane slot j of both operands is key
+// 16 G + 8 (j / 4) + 4 (lane / 32) + j % 4, i.e. the lane's score items 8 G .. 8 G
+// + 7 and two 4-key pieces of each V^T row (the 32x32x8 form, which takes as long
+// per instruction, would need twice the instructions).  Only blocks that reach past
+// the tile's first query position are masked; the rescale of O is skipped when no
+// lane's running maximum changed (a factor of exactly 1).  out = O / l.
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef float floatx16a __attribute__((ext_vector_type(16)));
 #define FA_Q 32    // queries per workgroup
@@ -1769,43 +1774,57 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], sacc, 0, 0, 0);
                 sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], sacc, 0, 0, 0);
             }
-            // lane's items: keys 8*(e/4) + 4*lh + e%4 of the block, query lq
+            // lane's items: keys 8*(e/4) + 4*lh + e%4 of the block, query lq.  A block
+            // that ends before the tile's first query position needs no mask; its
+            // scores are finite, and so is the new maximum.
+            const bool diag = (kb_lo + blk + 1) * FA_K > a.start + t0;
             float bm = -INFINITY;
+            if (diag) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t kpos = (kb_lo + blk) * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
-                if (kpos > qpos)
-                    sacc[e] = -INFINITY;
-                bm = fmaxf(bm, sacc[e]);
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t kpos = (kb_lo + blk) * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
+                    if (kpos > qpos)
+                        sacc[e] = -INFINITY;
+                }
             }
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                bm = fmaxf(bm, sacc[e]);
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
             const float mn = fmaxf(m, bm);
             const float r = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.f;
             float ps = 0.f;
-            half4v phi[4], plo[4];
+            half8 phi[2], plo[2];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float p = sacc[e] > -INFINITY ? __builtin_amdgcn_exp2f(sacc[e] - mn) : 0.f;
+                const float p = !diag || sacc[e] > -INFINITY ? __builtin_amdgcn_exp2f(sacc[e] - mn) : 0.f;
                 ps += p;
                 const _Float16 hi = (_Float16)p;
-                phi[e / 4][e % 4] = hi;
-                plo[e / 4][e % 4] = (_Float16)(p - (float)hi);
+                phi[e / 8][e % 8] = hi;
+                plo[e / 8][e % 8] = (_Float16)(p - (float)hi);
             }
             ps += __shfl_xor(ps, 32, 64);
             l = l * r + ps;
             m = mn;
+            if (__ballot(r != 1.0f) != 0) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                o0[e] *= r, o1[e] *= r;
-            // O^T[dim][query] += V^T[dim][key] P^T[key][query], keys in groups of 8
+                for (int e = 0; e < 16; ++e)
+                    o0[e] *= r, o1[e] *= r;
+            }
+            // O^T[dim][query] += V^T[dim][key] P^T[key][query], keys in groups of 16
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const half4v v0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 8 * g + 4 * lh]);
-                const half4v v1 = *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 8 * g + 4 * lh]);
-                o0 = __builtin_amdgcn_mfma_f32_32x32x8f16(v0, phi[g], o0, 0, 0, 0);
-                o0 = __builtin_amdgcn_mfma_f32_32x32x8f16(v0, plo[g], o0, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x8f16(v1, phi[g], o1, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x8f16(v1, plo[g], o1, 0, 0, 0);
+            for (int G = 0; G < 2; ++G) {
+                const half4v a0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 4 * lh]);
+                const half4v b0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 8 + 4 * lh]);
+                const half4v a1 = *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 4 * lh]);
+                const half4v b1 =
+                    *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 8 + 4 * lh]);
+                const half8 v0 = {a0[0], a0[1], a0[2], a0[3], b0[0], b0[1], b0[2], b0[3]};
+                const half8 v1 = {a1[0], a1[1], a1[2], a1[3], b1[0], b1[1], b1[2], b1[3]};
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, phi[G], o0, 0, 0, 0);
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, plo[G], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, phi[G], o1, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, plo[G], o1, 0, 0, 0);
             }
         }
         if (blk + 1 < nblk)
