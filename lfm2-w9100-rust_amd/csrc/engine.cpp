@@ -107,7 +107,7 @@ struct Shape {
 struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, split_rows_ext, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
-        gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_prefill, route_topk, route_group, combine_prefill, embed_rows,
+        gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_mfma, router_split, route_topk, route_group, combine_prefill, embed_rows,
         tile_pack, gemm_q6_n64, gemm_q6_x, gemm_swiglu_x, gemm_q6_t32x, gemm_swiglu_t32x;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f, conv_mixer, conv_mixer_r;
@@ -235,7 +235,7 @@ static int get_kernels(Kernels **out)
                 {&k->gemm_q6, "k_gemm_q6"},
                 {&k->conv_prefill, "k_conv_prefill"},
                 {&k->rope_kv_prefill, "k_rope_kv_prefill"}, {&k->attn_prefill, "k_attn_prefill"},
-                {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_prefill, "k_router_prefill"},
+                {&k->gemm_swiglu, "k_gemm_q6_swiglu"}, {&k->router_mfma, "k_router_mfma"}, {&k->router_split, "k_router_split"},
                 {&k->route_topk, "k_route_topk"},       {&k->route_group, "k_route_group"},
                 {&k->combine_prefill, "k_combine_prefill"}, {&k->gemm_reduce, "k_gemm_reduce"},
                 {&k->gemm_q6_t32, "k_gemm_q6_t32"},     {&k->gemm_swiglu_t32, "k_gemm_q6_swiglu_t32"},
@@ -832,6 +832,10 @@ struct DevTensor {
     uint64_t ne[4] = {1, 1, 1, 1};
     void *dev = nullptr;
     void *tdev = nullptr; // router weights [ROUTE_WIDTH][ROUTE_EXPERTS]: the transposed copy
+    // router weights: max |w| (at upload), and at finalize their binary16 hi / lo
+    // split of w * rscale (hi [E][dim] then lo), which the large calls' router reads
+    float amax = 0.f, rscale = 1.f;
+    void *rsplit = nullptr;
     size_t nbytes = 0;
     Q6T q6{};
     void *tiles_dev = nullptr; // prefill GEMM weights: the 32-row tile copy (at finalize)
@@ -1059,6 +1063,8 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
             (void)hipFree(old->second.tdev);
         if (old->second.tiles_dev)
             (void)hipFree(old->second.tiles_dev);
+        if (old->second.rsplit)
+            (void)hipFree(old->second.rsplit);
         e->tensors.erase(old);
     }
     // Router weights at the fused router's shape ([ROUTE_WIDTH inputs] x
@@ -1066,6 +1072,11 @@ extern "C" int lfm_engine_upload_tensor(lfm_engine *e, const char *name, uint32_
     // transposed copy [input][expert]: the output projection reads one input
     // row's 32 weights as one 128-byte line.
     const size_t nlen = strlen(name), slen = strlen("ffn_gate_inp.weight");
+    if (type == LFM_GGML_TYPE_F32 && nd == 2 && nlen >= slen && strcmp(name + nlen - slen, "ffn_gate_inp.weight") == 0) {
+        const float *src = (const float *)host;
+        for (size_t i = 0; i < n; ++i)
+            t.amax = std::max(t.amax, fabsf(src[i]));
+    }
     if (type == LFM_GGML_TYPE_F32 && nd == 2 && ne[0] == ROUTE_WIDTH && ne[1] == ROUTE_EXPERTS &&
         nlen >= slen && strcmp(name + nlen - slen, "ffn_gate_inp.weight") == 0) {
         std::vector<float> tr((size_t)ROUTE_WIDTH * ROUTE_EXPERTS);
@@ -1567,6 +1578,21 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         }
         if (gemm && t.type == LFM_GGML_TYPE_Q6_K && t.nd >= 2 && !t.tiles_dev)
             RC(make_tiles(e->K, e->stream, t.q6, (uint32_t)t.ne[1], &t.tiles_dev, &t.tiles));
+        // router rows for the large calls' matrix-core router: w * 2^s in binary16
+        // hi + lo, 2^s putting max |w| in [2^13, 2^14) so the lo halves stay normal
+        const size_t rl = strlen("ffn_gate_inp.weight");
+        if (t.type == LFM_GGML_TYPE_F32 && t.nd == 2 && !t.rsplit && n > rl &&
+            kv.first.compare(n - rl, rl, "ffn_gate_inp.weight") == 0) {
+            const uint64_t cnt = t.ne[0] * t.ne[1];
+            int ex = 0;
+            if (t.amax > 0.f && std::isfinite(t.amax))
+                frexpf(t.amax, &ex);
+            t.rscale = t.amax > 0.f && std::isfinite(t.amax) ? ldexpf(1.0f, 14 - ex) : 1.0f;
+            HIPCHK(hipMalloc(&t.rsplit, cnt * 4));
+            RouterSplitArgs ra{(const float *)t.dev, (uint16_t *)t.rsplit, (uint16_t *)t.rsplit + cnt, (uint32_t)cnt,
+                               t.rscale};
+            RC(launch_t(e->K->router_split, dim3((uint32_t)((cnt + 63) / 64)), 64, 0, e->stream, ra));
+        }
     }
     HIPCHK(hipStreamSynchronize(e->stream));
     e->kc.assign(hp.n_layers, nullptr);
@@ -1647,6 +1673,8 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
             (void)hipFree(kv.second.tdev);
         if (kv.second.tiles_dev)
             (void)hipFree(kv.second.tiles_dev);
+        if (kv.second.rsplit)
+            (void)hipFree(kv.second.rsplit);
     }
     for (void *p : e->qkvtdev)
         if (p)
@@ -1954,8 +1982,15 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
     } else if (T <= GEMM_TOKENS) { // few tokens: one workgroup per (expert, token)
         RC(launch(e->K->router_small, dim3(E, T), 0, e->stream, ra));
         e->dispatches += 1;
-    } else {
-        RC(launch(e->K->router_prefill, dim3((T + 15) / 16), 0, e->stream, ra));
+    } else { // large calls: the FFN input's split first; the router reads its hi / lo
+        RC(pf_split(e, x, norm, T, dim, T, true, 4));
+        const DevTensor *rt = tensor(e, "blk.%u.ffn_gate_inp.weight", l);
+        if (!rt || !rt->rsplit || rt->ne[0] != dim || rt->ne[1] != E)
+            return fail(LFM_EINTERNAL, "prefill router: layer %u has no split router rows", l);
+        const uint16_t *wh = (const uint16_t *)rt->rsplit;
+        RouterMfmaArgs rm{e->pf.hi, e->pf.lo, e->pf.scale, wh, wh + (size_t)E * dim, 1.0f / rt->rscale,
+                          e->pf.logits, T, dim, E};
+        RC(launch(e->K->router_mfma, dim3((T + 31) / 32), 0, e->stream, rm));
         e->dispatches += 1;
     }
     // small calls: the split forms the expert lists itself (no k_route_group), and
@@ -1973,7 +2008,8 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
         e->dispatches += 1;
     }
-    RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, small, self_route ? &rg : nullptr));
+    if (small) // (large calls split before routing)
+        RC(pf_split(e, x, norm, T, dim, T, true, 4, nullptr, nullptr, 0, true, self_route ? &rg : nullptr));
     if (e->route_log) // the call's routing is final here (ids, weights, logits)
         RC(log_routes(e, l, (uint32_t)((x - e->pf.x) / dim), T, true));
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,

@@ -403,6 +403,22 @@ struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)
     uint32_t T, dim, n_expert;
 };
 
+struct RouterSplitArgs {    // hi / lo = binary16 split of w * scale (n values)
+    const float *w;
+    uint16_t *hi, *lo;
+    uint32_t n;
+    float scale;
+};
+
+struct RouterMfmaArgs {     // logits[t][e] = xscale[t] * unscale * sum_k W'[e][k] X'[t][k]
+    const uint16_t *x_hi, *x_lo; // [T][K] binary16 split of the FFN input (row-major)
+    const float *xscale;         // [T] its row scales
+    const uint16_t *w_hi, *w_lo; // [E][K] binary16 split of the router rows times 2^s
+    float unscale;               // 2^-s
+    float *logits;               // [T][E]
+    uint32_t T, K, E;
+};
+
 struct RouteGroupArgs {   // per token top-k, then per expert the ordered (token, rank) list
     const float *logits, *bias;  // logits [T][n_expert] (read by k_route_topk)
     uint32_t *sel;        // [T][4] ids

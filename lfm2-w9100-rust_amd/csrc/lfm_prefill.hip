@@ -1906,112 +1906,72 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge_split(cons
 }
 
 // ------------------------------------------------------------------ FFN pieces
-// Router logits for T tokens (lfm.rs:599-607): a workgroup takes 16 tokens.
-// 128-wide slices of x . w and of the f32 router rows are staged in LDS (rows
-// padded by 4 floats, so the 16-byte reads below are conflict-free), the next
-// slice's loads in flight while thread (token tid / 16, experts tid % 16 + 16 j)
-// accumulates its dot products in k order, four k at a time; the RMSNorm sum of
-// squares is gathered from the same staged loads, and logits = inv * sum.  NE = 2
-// covers up to 32 experts, 4 up to 64.
-#define RT_TOK 16
-#define RT_K 128
-#define RT_PAD (RT_K + 4)
-#define RT_EMAX 64
-template <int NE>
-__device__ __forceinline__ void router_dots(const float *xr, const float *ws, uint32_t eg, float (&acc)[4])
+// Router logits of a large call on the matrix cores (lfm.rs:599-607): logits[t][e] =
+// sum_k W[e][k] xn[t][k], xn = RMSNorm(x_t) * ffn_norm, from the FFN input's split
+// (binary16 hi + lo of xn / xscale[t], row-major, written before this kernel) and the
+// router rows split once into hi + lo of W * 2^s (k_router_split; s puts max |W| in
+// [2^13, 2^14), so the lo halves stay normal).  A workgroup takes 32 tokens; wave w
+// sums the k-steps [w nks / 4, (w + 1) nks / 4) of 16 with three products per step
+// (Wh Xh, Wh Xl, Wl Xh on v_mfma_f32_32x32x16_f16; Wl Xl is below 2^-22 of a term),
+// the next step's fragments loaded during the current one's products, and wave 0
+// adds the four partial tiles in order.  32 experts per pass (two passes for up to
+// 64).  Lane l holds expert rows 8 (j / 4) + 4 (l / 32) + j % 4 of token l % 32.
+extern "C" __global__ __launch_bounds__(64) void k_router_split(const RouterSplitArgs a)
 {
-#pragma unroll 4
-    for (uint32_t kk = 0; kk < RT_K; kk += 4) {
-        const float4 x4 = *reinterpret_cast<const float4 *>(xr + kk);
-#pragma unroll
-        for (int j = 0; j < NE; ++j) {
-            const float4 w4 = *reinterpret_cast<const float4 *>(ws + (eg + 16 * j) * RT_PAD + kk);
-            acc[j] = fmaf(x4.x, w4.x, acc[j]);
-            acc[j] = fmaf(x4.y, w4.y, acc[j]);
-            acc[j] = fmaf(x4.z, w4.z, acc[j]);
-            acc[j] = fmaf(x4.w, w4.w, acc[j]);
-        }
-    }
+    const uint32_t i = blockIdx.x * 64 + threadIdx.x;
+    if (i >= a.n)
+        return;
+    _Float16 h, l;
+    split_f16(a.w[i] * a.scale, h, l);
+    a.hi[i] = __builtin_bit_cast(uint16_t, h);
+    a.lo[i] = __builtin_bit_cast(uint16_t, l);
 }
 
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_prefill(const RouterPrefillArgs a)
+extern "C" __global__ __launch_bounds__(WG_THREADS) void k_router_mfma(const RouterMfmaArgs a)
 {
-    __shared__ float inv[RT_TOK];
-    __shared__ __attribute__((aligned(16))) float xs[RT_TOK * RT_PAD];
-    __shared__ __attribute__((aligned(16))) float ws[RT_EMAX * RT_PAD];
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    const uint32_t t0 = blockIdx.x * RT_TOK;
-    const uint32_t tt = tid / 16, eg = tid % 16;
-    const bool wide = a.n_expert > 32;    // uniform
-    const uint32_t nw4 = wide ? 8 : 4;    // float4 of router rows per thread and slice
-    // staging: x piece v of thread tid is token (tid + 256v) / 32, floats
-    // ((tid + 256v) % 32) * 4 ..; router piece v is row (tid + 256v) / 32 likewise
-    float4 xr[2], nr[2], wr[8];
-    float ss[2] = {0.f, 0.f};
-    auto fetch = [&](uint32_t k0) {
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const uint32_t p = lane >> 5, lr = lane & 31, t0 = blockIdx.x * 32;
+    if (t0 >= a.T)
+        return;
+    const uint32_t t = min(t0 + lr, a.T - 1), nks = a.K / 16;
+    const uint32_t ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;
+    __shared__ floatx16 part[4][64];
+    const half8 *xh = reinterpret_cast<const half8 *>(a.x_hi) + ((size_t)t * a.K + 8 * p) / 8;
+    const half8 *xl = reinterpret_cast<const half8 *>(a.x_lo) + ((size_t)t * a.K + 8 * p) / 8;
+    for (uint32_t et = 0; et < a.E; et += 32) {
+        const uint32_t e = min(et + lr, a.E - 1);
+        const half8 *wh = reinterpret_cast<const half8 *>(a.w_hi) + ((size_t)e * a.K + 8 * p) / 8;
+        const half8 *wl = reinterpret_cast<const half8 *>(a.w_lo) + ((size_t)e * a.K + 8 * p) / 8;
+        floatx16 acc;
 #pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const uint32_t u = tid + WG_THREADS * v, t = t0 + u / 32, kk = (u % 32) * 4;
-            xr[v] = t < a.T ? *reinterpret_cast<const float4 *>(a.x + (size_t)t * a.dim + k0 + kk)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-            nr[v] = *reinterpret_cast<const float4 *>(a.norm_w + k0 + kk);
+        for (int j = 0; j < 16; ++j)
+            acc[j] = 0.f;
+        half8 bh = xh[2 * ks0], bl = xl[2 * ks0], ah = wh[2 * ks0], al = wl[2 * ks0];
+        for (uint32_t ks = ks0; ks < ks1; ++ks) {
+            const uint32_t kn = min(ks + 1, ks1 - 1); // the next step's fragments (the last re-reads its own)
+            const half8 nbh = xh[2 * kn], nbl = xl[2 * kn], nah = wh[2 * kn], nal = wl[2 * kn];
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc, 0, 0, 0);
+            bh = nbh, bl = nbl, ah = nah, al = nal;
         }
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            const uint32_t u = tid + WG_THREADS * v, e = u / 32, kk = (u % 32) * 4;
-            if (v < (int)nw4)
-                wr[v] = e < a.n_expert ? *reinterpret_cast<const float4 *>(a.w + (size_t)e * a.dim + k0 + kk)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto stage = [&]() {
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const uint32_t u = tid + WG_THREADS * v, r = u / 32, kk = (u % 32) * 4;
-            const float4 x4 = xr[v], n4 = nr[v];
-            ss[v] += x4.x * x4.x + x4.y * x4.y + x4.z * x4.z + x4.w * x4.w;
-            *reinterpret_cast<float4 *>(&xs[r * RT_PAD + kk]) =
-                make_float4(x4.x * n4.x, x4.y * n4.y, x4.z * n4.z, x4.w * n4.w);
-        }
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-            const uint32_t u = tid + WG_THREADS * v, e = u / 32, kk = (u % 32) * 4;
-            if (v < (int)nw4)
-                *reinterpret_cast<float4 *>(&ws[e * RT_PAD + kk]) = wr[v];
-        }
-    };
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    fetch(0);
-    for (uint32_t k0 = 0; k0 < a.dim; k0 += RT_K) {
-        __syncthreads(); // the previous slice's dot products are done
-        stage();
-        if (k0 + RT_K < a.dim)
-            fetch(k0 + RT_K); // in flight during this slice's dot products
+        part[wave][lane] = acc;
         __syncthreads();
-        if (wide)
-            router_dots<4>(xs + tt * RT_PAD, ws, eg, acc);
-        else
-            router_dots<2>(xs + tt * RT_PAD, ws, eg, acc);
-    }
-    // RMSNorm scale: token (tid + 256v) / 32 is shared by the 32 lanes of a wave half
+        if (wave == 0 && t0 + lr < a.T) {
+            floatx16 s = part[0][lane];
+            s += part[1][lane];
+            s += part[2][lane];
+            s += part[3][lane];
+            const float f = a.xscale[t0 + lr] * a.unscale;
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-        float q = ss[v];
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1)
-            q += __shfl_xor(q, off, 64);
-        if ((lane & 31) == 0)
-            inv[(tid + WG_THREADS * v) / 32] = 1.0f / sqrtf(q / (float)a.dim + a.eps);
-    }
-    __syncthreads();
-    const uint32_t t = t0 + tt;
-    if (t < a.T)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = eg + 16 * j;
-            if (e < a.n_expert)
-                a.logits[(size_t)t * a.n_expert + e] = inv[tt] * acc[j];
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t ee = et + 8 * (j / 4) + 4 * p + (j % 4);
+                if (ee < a.E)
+                    a.logits[(size_t)(t0 + lr) * a.E + ee] = s[j] * f;
+            }
         }
+        __syncthreads();
+    }
 }
 
 // Router logits for calls of up to 128 tokens: one workgroup per (expert, token)
