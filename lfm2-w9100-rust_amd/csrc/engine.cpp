@@ -2005,7 +2005,7 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         e->dispatches += 1;
     }
     if (!small) {
-        RC(launch(e->K->route_group, dim3(E), 0, e->stream, rg));
+        RC(launch_t(e->K->route_group, dim3(E), 1024, 0, e->stream, rg));
         e->dispatches += 1;
     }
     if (small) // (large calls split before routing)

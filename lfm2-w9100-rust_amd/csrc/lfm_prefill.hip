@@ -2035,15 +2035,19 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_topk(const Rout
 
 // Per expert (one workgroup each) the (token, rank) pairs that selected it, in
 // token order: tok[e][i] = token, slot[e][i] = token * 4 + rank; counts[e].
-extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const RouteGroupArgs a)
+// 1024 threads, so that a 3840-token call takes four passes of ballots and
+// barriers instead of fifteen.
+#define RG_THREADS 1024
+extern "C" __global__ __launch_bounds__(RG_THREADS) void k_route_group(const RouteGroupArgs a)
 {
+    constexpr uint32_t NWV = RG_THREADS / 64;
     const uint32_t e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ uint32_t wave_cnt[4];
+    __shared__ uint32_t wave_cnt[NWV];
     __shared__ uint32_t base;
     if (tid == 0)
         base = 0;
     __syncthreads();
-    for (uint32_t t0 = 0; t0 < a.T; t0 += WG_THREADS) {
+    for (uint32_t t0 = 0; t0 < a.T; t0 += RG_THREADS) {
         const uint32_t t = t0 + tid;
         uint32_t rank_of_e = 4; // 4: not selected
         if (t < a.T) {
@@ -2069,8 +2073,12 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_route_group(const Rou
                 a.pos[t * 4 + rank_of_e] = off + before;
         }
         __syncthreads();
-        if (tid == 0)
-            base += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+        if (tid == 0) {
+            uint32_t sum = base;
+            for (uint32_t w = 0; w < NWV; ++w)
+                sum += wave_cnt[w];
+            base = sum;
+        }
         __syncthreads();
     }
     if (tid == 0)
