@@ -56,13 +56,16 @@ def check_prefill(gpu, oracle, hp, tensors, n, ctx):
     return g, o, prompt, lg, lo
 
 
-def test_prefill_wide_router(gpu, oracle):
-    """48 experts top-4: the prefill router's path for more than 32 experts."""
+@pytest.mark.parametrize("n", [70, 200])
+def test_prefill_wide_router(gpu, oracle, n):
+    """48 experts top-4: the prefill routers' paths for more than 32 experts (at 70
+    tokens the small call's; at 200 the large call's matrix-core router, whose second
+    pass covers experts 32..47)."""
     hp = gpu.make_hparams(dim=256, heads=4, n_layers=2, attention_layers=(1,), kv=2, vocab=500,
                           eos=1 << 30, n_expert=48, n_used=4, expert_ff=256, n_ff=512,
                           dense_lead=1)
     tensors = model_tensors(hp, gpu.synth_opts(0x5EED, bias_sigma=0.1))
-    check_prefill(gpu, oracle, hp, tensors, 70, 128)
+    check_prefill(gpu, oracle, hp, tensors, n, 256)
 
 
 @pytest.mark.parametrize("n", [2, 24, 300])
