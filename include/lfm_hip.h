@@ -132,6 +132,14 @@ int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap);
  * (stepwise = 0); stepwise = 1 runs them as one captured decode step per token
  * instead (the reference's token-by-token equivalence, used by parity tests). */
 int lfm_engine_set_prefill_mode(lfm_engine *e, int stepwise);
+/* No counterpart in the reference (its weights stay Q6_K on the device): device
+ * bytes this engine holds in binary16 copies of its GEMM weights, which the
+ * multi-token forwards of more than 128 tokens read instead of decoding Q6_K.
+ * lfm_engine_finalize makes one per weight whose sub-block scales all lie within
+ * [-64, 64] (binary16 holds those weights exactly; 2.4 times the weight's Q6_K
+ * bytes, about 16.4 GB for LFM2.5-8B-A1B) unless the environment sets
+ * LFM_PREFILL_H16=0 or the device has no memory left for it; 0 when none. */
+int lfm_engine_h16_bytes(const lfm_engine *e, uint64_t *bytes);
 /* gpu.dispatch_count(): kernels launched by this engine so far. */
 uint64_t lfm_dispatch_count(const lfm_engine *e);
 /* device_name (gpu_lfm.rs:126-128). */

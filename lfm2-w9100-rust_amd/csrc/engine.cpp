@@ -108,7 +108,8 @@ struct Kernels {
     hipModule_t mod = nullptr, pmod = nullptr;
     hipFunction_t split_rows, split_rows_ext, gemm_q6, conv_prefill, rope_kv_prefill, attn_prefill,
         gemm_swiglu, gemm_q6_t32, gemm_q6_t32n1, gemm_swiglu_t32, gemm_reduce, reduce_combine, attn_merge_split, router_small, router_mfma, router_split, route_topk, route_group, combine_prefill, embed_rows,
-        tile_pack, gemm_q6_n64, gemm_q6_x, gemm_swiglu_x, gemm_q6_t32x, gemm_swiglu_t32x;
+        tile_pack, gemm_q6_n64, gemm_q6_x, gemm_swiglu_x, gemm_q6_t32x, gemm_swiglu_t32x, tile_h16, gemm_h16,
+        gemm_h16_n64, gemm_swiglu_h16;
     hipFunction_t matvec_long, attn, attn_merge, router, moe_down, argmax, argmax_final, advance,
         dequant, copy, matvec_route, gateup_f, conv_mixer, conv_mixer_r;
     Shape matvec, conv, qkv, gateup, head;
@@ -244,7 +245,9 @@ static int get_kernels(Kernels **out)
                 {&k->embed_rows, "k_embed_rows"}, {&k->tile_pack, "k_q6_tile_pack"},
                 {&k->gemm_q6_n64, "k_gemm_q6_n64"}, {&k->gemm_q6_x, "k_gemm_q6_x"},
                 {&k->gemm_swiglu_x, "k_gemm_q6_swiglu_x"}, {&k->gemm_q6_t32x, "k_gemm_q6_t32x"},
-                {&k->gemm_swiglu_t32x, "k_gemm_q6_swiglu_t32x"}};
+                {&k->gemm_swiglu_t32x, "k_gemm_q6_swiglu_t32x"}, {&k->tile_h16, "k_q6_tile_h16"},
+                {&k->gemm_h16, "k_gemm_h16"}, {&k->gemm_h16_n64, "k_gemm_h16_n64"},
+                {&k->gemm_swiglu_h16, "k_gemm_swiglu_h16"}};
     for (auto &f : pfns) {
         e = hipModuleGetFunction(f.f, k->pmod, f.name);
         if (e != hipSuccess) {
@@ -462,7 +465,48 @@ static int make_tiles(Kernels *K, hipStream_t s, const Q6T &src, uint32_t group_
         *dev = nullptr;
         return rc;
     }
-    *out = Q6Tiles{(const uint8_t *)*dev, (uint32_t)tiles, src.nb, gtiles, group_rows, wide ? 1u : 0u};
+    *out = Q6Tiles{(const uint8_t *)*dev, (uint32_t)tiles, src.nb, gtiles, group_rows, wide ? 1u : 0u, nullptr};
+    return LFM_OK;
+}
+
+// The binary16 fragment copy of a tile copy (kargs.h TILE_H16), which the large-call
+// GEMMs read instead of decoding Q6_K: made when every scale of the tensor lies
+// within [-64, 64] (binary16 then holds its weights exactly) unless LFM_PREFILL_H16=0.
+// 16 KB per tile-block (2.4 times the Q6_K bytes).  Without it (wide scales, the
+// variable set, or no device memory for it) t->h16 stays null and those calls
+// decode Q6_K in registers as the small calls do.
+static bool h16_wanted()
+{
+    const char *v = getenv("LFM_PREFILL_H16");
+    return !(v && strcmp(v, "0") == 0);
+}
+
+static bool ends_with(const std::string &s, const char *suffix)
+{
+    const size_t m = strlen(suffix);
+    return s.size() >= m && s.compare(s.size() - m, m, suffix) == 0;
+}
+
+static int make_h16(Kernels *K, hipStream_t s, Q6Tiles *t, void **dev)
+{
+    *dev = nullptr;
+    t->h16 = nullptr;
+    if (t->wide || !h16_wanted())
+        return LFM_OK;
+    const uint64_t ntb = (uint64_t)t->tiles * t->nb;
+    if (hipMalloc(dev, ntb * TILE_H16) != hipSuccess) {
+        (void)hipGetLastError(); // out of device memory: keep the Q6_K kernels
+        *dev = nullptr;
+        return LFM_OK;
+    }
+    TileH16Args a{*t, (uint8_t *)*dev};
+    const int rc = launch_t(K->tile_h16, dim3((uint32_t)ntb), 64, 0, s, a);
+    if (rc != LFM_OK) {
+        (void)hipFree(*dev);
+        *dev = nullptr;
+        return rc;
+    }
+    t->h16 = (const uint8_t *)*dev;
     return LFM_OK;
 }
 
@@ -653,6 +697,8 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     const dim3 g128 = gemm_grid(g.zrows, T, nz, GEMM_ROWS, GEMM_TOKENS);
     const bool n64 = !small && !pair && (exact || (uint64_t)g128.x * g128.y * g128.z < GEMM_N64_BELOW);
     const bool t64 = n64 || (!small && pair && exact);
+    // large calls over weights with a binary16 fragment copy read it (no decode)
+    const bool h16 = !small && !exact && g.w.h16 && (!pair || g.w2.h16);
     dim3 grid = gemm_grid(g.zrows, T, nz, pair || one_tile ? GEMM_ROWS / 2 : GEMM_ROWS,
                           small ? 32 : t64 ? GEMM_TOKENS / 2 : GEMM_TOKENS);
     uint32_t S = 1;
@@ -667,6 +713,7 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
     }
     hipFunction_t f = small ? (pair ? (exact ? K->gemm_swiglu_t32x : K->gemm_swiglu_t32)
                                     : one_tile ? (exact ? K->gemm_q6_t32x : K->gemm_q6_t32n1) : K->gemm_q6_t32)
+                    : h16 ? (pair ? K->gemm_swiglu_h16 : n64 ? K->gemm_h16_n64 : K->gemm_h16)
                             : (pair ? (exact ? K->gemm_swiglu_x : K->gemm_swiglu)
                                     : n64 ? (exact ? K->gemm_q6_x : K->gemm_q6_n64) : K->gemm_q6);
     if (deferred)
@@ -749,9 +796,11 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     int rc = launch(K->split_rows, dim3(T), 0, s, sa);
     GemmArgs ga;
     memset(&ga, 0, sizeof(ga));
-    void *tiles = nullptr;
+    void *tiles = nullptr, *h16 = nullptr;
     if (rc == LFM_OK)
         rc = make_tiles(K, s, q6view(packed, rows, in_dim), (uint32_t)rows, &tiles, &ga.w);
+    if (rc == LFM_OK && T > GEMM_TOKENS)
+        rc = make_h16(K, s, &ga.w, &h16);
     ga.x_hi = hi;
     ga.x_lo = lo;
     ga.xscale = scale;
@@ -778,6 +827,8 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
         (void)hipFree(part);
     if (tiles)
         (void)hipFree(tiles);
+    if (h16)
+        (void)hipFree(h16);
     return rc;
 }
 
@@ -839,6 +890,7 @@ struct DevTensor {
     size_t nbytes = 0;
     Q6T q6{};
     void *tiles_dev = nullptr; // prefill GEMM weights: the 32-row tile copy (at finalize)
+    void *h16_dev = nullptr;   // and its binary16 fragment copy (tiles.h16; nullable)
     Q6Tiles tiles{};
 };
 
@@ -876,7 +928,7 @@ struct lfm_engine {
     std::vector<Q6T> qkvw;
     std::vector<void *> qkvdev;
     std::vector<Q6Tiles> qkvt; // tile copies of qkvw (prefill)
-    std::vector<void *> qkvtdev;
+    std::vector<void *> qkvtdev, qkvh16dev;
     std::vector<float *> conv;
     uint32_t head_grid = 1, nchunk = 1;
     float *rope = nullptr; // [ctx][32] (cos, sin)
@@ -1559,10 +1611,13 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     // ordered with the engine's non-blocking stream: finish them first.
     HIPCHK(hipDeviceSynchronize());
     e->qkvtdev.assign(hp.n_layers, nullptr);
+    e->qkvh16dev.assign(hp.n_layers, nullptr);
     e->qkvt.assign(hp.n_layers, Q6Tiles{});
     for (uint32_t l = 0; l < hp.n_layers; ++l)
-        if (hp.kv_heads[l])
+        if (hp.kv_heads[l]) {
             RC(make_tiles(e->K, e->stream, e->qkvw[l], e->qkvw[l].rows, &e->qkvtdev[l], &e->qkvt[l]));
+            RC(make_h16(e->K, e->stream, &e->qkvt[l], &e->qkvh16dev[l]));
+        }
     static const char *const gemm_weights[] = {"shortconv.in_proj.weight", "shortconv.out_proj.weight",
                                                "attn_output.weight",       "ffn_gate.weight",
                                                "ffn_up.weight",            "ffn_down.weight",
@@ -1576,8 +1631,16 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
             const size_t m = strlen(suf);
             gemm = gemm || (n > m && kv.first.compare(n - m, m, suf) == 0 && kv.first[n - m - 1] == '.');
         }
-        if (gemm && t.type == LFM_GGML_TYPE_Q6_K && t.nd >= 2 && !t.tiles_dev)
+        if (gemm && t.type == LFM_GGML_TYPE_Q6_K && t.nd >= 2 && !t.tiles_dev) {
             RC(make_tiles(e->K, e->stream, t.q6, (uint32_t)t.ne[1], &t.tiles_dev, &t.tiles));
+            // not for the experts' gate / up pair: its binary16 copy (2.4 times 193 MB
+            // per layer) streams from HBM at every large call, where the Q6_K bytes
+            // and their decode in registers measured faster (the other weights are
+            // read by several token tiles through the caches)
+            const bool pair_exps = ends_with(kv.first, "ffn_gate_exps.weight") || ends_with(kv.first, "ffn_up_exps.weight");
+            if (!pair_exps)
+                RC(make_h16(e->K, e->stream, &t.tiles, &t.h16_dev));
+        }
         // router rows for the large calls' matrix-core router: w * 2^s in binary16
         // hi + lo, 2^s putting max |w| in [2^13, 2^14) so the lo halves stay normal
         const size_t rl = strlen("ffn_gate_inp.weight");
@@ -1673,10 +1736,15 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
             (void)hipFree(kv.second.tdev);
         if (kv.second.tiles_dev)
             (void)hipFree(kv.second.tiles_dev);
+        if (kv.second.h16_dev)
+            (void)hipFree(kv.second.h16_dev);
         if (kv.second.rsplit)
             (void)hipFree(kv.second.rsplit);
     }
     for (void *p : e->qkvtdev)
+        if (p)
+            (void)hipFree(p);
+    for (void *p : e->qkvh16dev)
         if (p)
             (void)hipFree(p);
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->log_ids, e->log_w, e->log_logits, e->flow, e->x, e->y, e->qkv, e->sw,
@@ -2307,6 +2375,21 @@ extern "C" int lfm_snapshot_logits(lfm_engine *e, float *out, size_t cap)
 }
 
 extern "C" uint64_t lfm_dispatch_count(const lfm_engine *e) { return e ? e->dispatches : 0; }
+
+extern "C" int lfm_engine_h16_bytes(const lfm_engine *e, uint64_t *bytes)
+{
+    if (!e || !bytes)
+        return fail(LFM_EINVAL, "lfm_engine_h16_bytes: null argument");
+    uint64_t n = 0;
+    for (const auto &kv : e->tensors)
+        if (kv.second.h16_dev)
+            n += (uint64_t)kv.second.tiles.tiles * kv.second.tiles.nb * TILE_H16;
+    for (size_t l = 0; l < e->qkvh16dev.size(); ++l)
+        if (e->qkvh16dev[l])
+            n += (uint64_t)e->qkvt[l].tiles * e->qkvt[l].nb * TILE_H16;
+    *bytes = n;
+    return LFM_OK;
+}
 
 extern "C" int lfm_engine_set_prefill_mode(lfm_engine *e, int stepwise)
 {

@@ -303,13 +303,28 @@ struct Q6Tiles {
     uint32_t wide;   // some sub-block scale (of a block with d != 0) lies outside
                      // [-64, 64]: its weights sc (q - 32) can exceed 2048 in
                      // magnitude and need the GEMMs' split-scale (_x) kernels
+    const uint8_t *h16; // nullable: the binary16 fragment copy below (not wide only)
 };
+
+// The binary16 fragment copy of a Q6Tiles (the large-call GEMMs' A operands,
+// decoded once): tile-block tb holds the 32 rows x 256 k integer weights
+// sc (q - 32) of its rows' block, exact in binary16 for scales within [-64, 64],
+// as 16 k-steps of 16 k: k-step j of the block is 1 KB at byte 1024 j, lane
+// l = 32 p + r of a wave at 16 l holding row r's weights k = 16 j + 8 p .. + 7,
+// i.e. the A fragment of v_mfma_f32_32x32x16_f16 for that k-step.  The block
+// scale d stays in the Q6Tiles d plane.
+#define TILE_H16 16384u
 
 struct TilePackArgs {   // row-major planes -> Q6Tiles
     Q6T src;            // groups * group_rows rows
     uint8_t *dst;
     uint32_t group_rows, gtiles, tiles;
     uint32_t *wide;     // set to 1 when a scale outside [-64, 64] is seen (d != 0)
+};
+
+struct TileH16Args {    // Q6Tiles -> its binary16 fragment copy
+    Q6Tiles src;
+    uint8_t *dst;       // src.tiles * src.nb * TILE_H16 bytes
 };
 
 // C[slot(n)][col0 + r] (+)= scale[tok(n)] * sum_k W[z*zrows + r][k] * X[tok(n)][k]

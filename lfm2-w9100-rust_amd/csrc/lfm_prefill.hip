@@ -679,6 +679,31 @@ __device__ __forceinline__ half8 decode_frag(const AChunk &c, uint32_t s, half2v
     return decode_frag(c, s, sc[s & 1], sc[s & 1] * (_Float16)-288.0f);
 }
 
+// Q6Tiles -> binary16 fragment copy (kargs.h TILE_H16): workgroup tb (one wave)
+// decodes tile-block tb exactly as the GEMMs decode it in registers (same chunk
+// loads, same scales, same fused multiply-add per fragment), so the copy holds the
+// A fragments those kernels would form, k-step by k-step.
+extern "C" __global__ __launch_bounds__(64) void k_q6_tile_h16(const TileH16Args a)
+{
+    const size_t tb = blockIdx.x, ntb = (size_t)a.src.tiles * a.src.nb;
+    const uint32_t lane = threadIdx.x;
+    uint8_t *out = a.dst + tb * TILE_H16 + lane * 16;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+        AChunk A[2];
+        load_tile_chunks(a.src.base, ntb, tb, h, lane, A);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const half2v s0 = stage_scales(A[0].sc, q).sc, s1 = stage_scales(A[1].sc, q).sc;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) { // k-step ks of stage 2h + q: chunk ks % 2, sub-block 2q + ks / 2
+                const half8 f = decode_frag(A[ks & 1], 2 * q + (ks >> 1), (ks & 1) ? s1 : s0);
+                *reinterpret_cast<half8 *>(out + ((2 * h + q) * 4 + ks) * 1024) = f;
+            }
+        }
+    }
+}
+
 // C[n][row] (+)= sum_k W[row][k] * X[n][k] for weight rows [0, zrows) of group
 // z and token columns n < ntok.  Column n reads activation row (tok ? tok[n] :
 // n) and writes output row (slot ? slot[n] : n).  The pair form (k_gemm_q6_swiglu)
@@ -1085,6 +1110,232 @@ extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_pe
 k_gemm_q6_swiglu_x(const GemmArgs a)
 {
     gemm_body<true, 2, true>(a);
+}
+
+// The large-call GEMM over the binary16 fragment copy (Q6Tiles::h16, made once at
+// finalize by k_q6_tile_h16): gemm_body's workgroup tiles, activation staging,
+// block-scale folding and epilogue, but each wave loads its A fragments ready-made,
+// one 16-byte load per lane, fragment and k-step (1 KB contiguous per wave), a
+// stage ahead, instead of loading Q6_K bytes and decoding them: the k-loop is
+// loads, LDS fragment reads and MFMAs.  The products are those of gemm_body (the
+// copy holds the fragments its decode forms).  Large calls only: one K slice.
+template <bool PAIR, int NJ>
+__device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
+{
+    constexpr uint32_t TNW = 32 * NJ;
+    constexpr uint32_t TMW = PAIR ? TM / 2 : TM;
+    uint32_t z, mx, ny;
+    {
+        const uint32_t gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+        const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+        const uint32_t q = total / 8, r = total % 8, xcd = L % 8, idx = L / 8;
+        const uint32_t V = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+        // Within a weight slice, groups of 8 token tiles with the row tiles next: the
+        // workgroups resident on one XCD (a run of consecutive V) then cover about 8
+        // row tiles x 8 token tiles, whose weights and activations its L2 shares.
+        // (Row tiles fastest over all token tiles, as gemm_body orders them, reads
+        // the whole weight once per token tile: 2.4 times the Q6_K bytes here.)
+        const uint32_t per = gx * gy, Vz = V % per, g = Vz / (gx * 8), w = Vz - g * gx * 8;
+        const uint32_t ng = min(8u, gy - g * 8);
+        mx = gx > 8 ? w / ng : Vz % gx;
+        ny = gx > 8 ? g * 8 + w % ng : Vz / gx;
+        z = V / per;
+    }
+    const uint32_t nb = a.w.nb, K = nb * 256;
+    const uint32_t m0 = mx * TMW, n0 = ny * TNW;
+    const uint32_t ntok = a.counts ? a.counts[z] : a.ntok;
+    if (m0 >= a.zrows || n0 >= ntok)
+        return;
+    const uint32_t *tokl = a.tok ? a.tok + (size_t)z * a.list_stride : nullptr;
+    const uint32_t *slotl = a.slot ? a.slot + (size_t)z * a.list_stride : nullptr;
+    const __amdgpu_buffer_rsrc_t xh = act_rsrc(a.x_hi), xl = act_rsrc(a.x_lo);
+    __shared__ __attribute__((aligned(16))) _Float16 Bh0[TNW * TK], Bh1[TNW * TK];
+    __shared__ __attribute__((aligned(16))) _Float16 Bl0[TNW * TK], Bl1[TNW * TK];
+    __shared__ float dsh[2][TM], rsh[2][TM];
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const uint32_t p = lane >> 5, lr = lane & 31;
+    const size_t ntb = (size_t)a.w.tiles * nb;
+    uint32_t vb[2], lb[2];
+    const uint8_t *hw[2]; // row tile i's fragments: tile-blocks wt * nb .. are consecutive
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        vb[i] = PAIR ? i * 128 + wave * 32 : wave * 64 + i * 32;
+        lb[i] = PAIR ? wave * 32 : vb[i];
+        const uint32_t wt = z * a.w.gtiles + min((m0 + lb[i]) >> 5, a.w.gtiles - 1);
+        hw[i] = (PAIR && i ? a.w2.h16 : a.w.h16) + (size_t)wt * nb * TILE_H16 + lane * 16;
+    }
+    uint32_t boff[NJ];
+#pragma unroll
+    for (int v = 0; v < NJ; ++v) {
+        const uint32_t t = (tid + GEMM_NTH * v) >> 3, col = min(n0 + t, ntok - 1);
+        boff[v] = ((tokl ? tokl[col] : col) * K + ((tid & 7) ^ ((t >> 1) & 7)) * 8) * 2;
+    }
+    // stage st's fragments of k-step ks (block st / 4, k-step 4 (st % 4) + ks of it)
+    auto loadF = [&](uint32_t st, int ks, half8 (&F)[2][4]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            F[i][ks] = *reinterpret_cast<const half8 *>(hw[i] + (size_t)st * 4096 + ks * 1024);
+    };
+    auto loadD = [=](uint32_t kb) -> uint32_t {
+        const uint8_t *wb = PAIR && tid >= 128 ? a.w2.base : a.w.base;
+        const uint32_t v = PAIR ? tid & 127 : tid;
+        const uint32_t t = z * a.w.gtiles + min((m0 + v) >> 5, a.w.gtiles - 1);
+        return tile_d(wb, ntb, (size_t)t * nb + kb, v & 31);
+    };
+    floatx16 acc[2][NJ];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][j][e] = 0.f;
+    auto rescale = [&](uint32_t rb) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float r = rsh[rb][vb[i] + 8 * (e / 4) + 4 * p + (e % 4)];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    acc[i][j][e] *= r;
+            }
+    };
+    float u = 1.0f;
+    auto set_d = [&](uint32_t slot, float d) {
+        dsh[slot][tid] = d;
+        const bool nz = d != 0.f;
+        rsh[slot][tid] = nz ? u / d : 1.0f;
+        u = nz ? d : u;
+    };
+    const uint32_t nst = nb * 4;
+    uint32_t dnext = 0;
+    float dnextf = 0.f;
+
+    // Stage st = 4 kb + sb over tile buffer sb % 2 and fragment set F (st % 2):
+    // issue stage st + 1's tile into the other buffer (and at sb = 0 block kb + 1's
+    // scale), then the k-steps, each followed by the load of stage st + 2's fragments
+    // of that k-step into the registers it just used (so fragments are requested
+    // about two stages ahead with two sets of registers), then wait for stage st +
+    // 1's tile (the 8 fragment loads issued after it stay in flight: loads retire in
+    // issue order) and meet at the barrier.
+    auto stage = [&](uint32_t st, const _Float16 *__restrict__ bh, const _Float16 *__restrict__ bl,
+                     _Float16 *__restrict__ nh, _Float16 *__restrict__ nl, half8 (&F)[2][4]) {
+        const uint32_t kb = st >> 2, sb = st & 3;
+        // Every load is issued without a branch around it (past the last stage and
+        // block, the last ones again, unused): a load under a branch leaves the
+        // compiler's wait counts unknown at the join, after which the first use of
+        // a fragment would wait for every load issued after it.
+        const uint32_t sn = min(st + 1, nst - 1), s2 = min(st + 2, nst - 1);
+        if (sb == 0 && kb > 0)
+            rescale(kb & 1);
+        issue_fence();
+        lds_dma_stage<NJ>(xh, xl, boff, sn * TK * 2, wave, nh, nl);
+        issue_fence();
+        if (sb == 0)
+            dnext = loadD(min(kb + 1, nb - 1));
+        issue_fence();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t kp = ks * 2 + p;
+            half8 bfh[2], bfl[2];
+            bfh[0] = lds_frag(bh, swz(lr, kp));
+            bfl[0] = lds_frag(bl, swz(lr, kp));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if (j + 1 < NJ) {
+                    bfh[(j + 1) & 1] = lds_frag(bh, swz((j + 1) * 32 + lr, kp));
+                    bfl[(j + 1) & 1] = lds_frag(bl, swz((j + 1) * 32 + lr, kp));
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[i][ks], bfh[j & 1], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[i][ks], bfl[j & 1], acc[i][j], 0, 0, 0);
+            }
+            issue_fence();
+            loadF(s2, ks, F);
+            issue_fence();
+        }
+        if (sb == 2 && kb + 1 < nb) // publish block kb + 1's scale (landed by stage 4 kb + 1's wait)
+            set_d((kb + 1) & 1, dnextf);
+        // stage st + 1's tile has landed (this wave's pieces; the wait also retires
+        // its LDS reads and writes, the scale issued after the tile, and stage st +
+        // 1's fragments, issued before it); stage st + 2's fragments stay in flight,
+        // and the barrier publishes the tile
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(8));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (sb == 1)
+            dnextf = half_bits_to_float(dnext);
+    };
+    half8 F0[2][4], F1[2][4];
+    lds_dma_stage<NJ>(xh, xl, boff, 0, wave, Bh0, Bl0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        loadF(0, ks, F0);
+        loadF(1, ks, F1); // nst >= 4
+    }
+    set_d(0, half_bits_to_float(loadD(0)));
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (uint32_t kb = 0; kb < nb; ++kb) {
+        stage(4 * kb + 0, Bh0, Bl0, Bh1, Bl1, F0);
+        stage(4 * kb + 1, Bh1, Bl1, Bh0, Bl0, F1);
+        stage(4 * kb + 2, Bh0, Bl0, Bh1, Bl1, F0);
+        stage(4 * kb + 3, Bh1, Bl1, Bh0, Bl0, F1);
+    }
+    __syncthreads();
+    rsh[0][tid] = u;
+    __syncthreads();
+    rescale(0);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const uint32_t n = n0 + j * 32 + lr;
+        if (n >= ntok)
+            continue;
+        const uint32_t orow = slotl ? slotl[n] : n;
+        const float xs = a.xscale[tokl ? tokl[n] : n];
+        float *out = a.c + (size_t)orow * a.ldc + a.col0;
+        if (PAIR) {
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float g = acc[0][j][e] * xs, uu = acc[1][j][e] * xs;
+                v[e] = g / (1.0f + expf(-g)) * uu;
+            }
+            store_rows16(out, m0 + lb[0] + 4 * p, a.zrows, v, false);
+            continue;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                v[e] = acc[i][j][e] * xs;
+            store_rows16(out, m0 + lb[i] + 4 * p, a.zrows, v, a.mode != 0);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_h16(const GemmArgs a)
+{
+    gemm_body_h<false, 4>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_h16_n64(const GemmArgs a)
+{
+    gemm_body_h<false, 2>(a);
+}
+
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+k_gemm_swiglu_h16(const GemmArgs a)
+{
+    gemm_body_h<true, 4>(a);
 }
 
 // The same products for calls of up to 128 tokens (chunked prefill: about 8

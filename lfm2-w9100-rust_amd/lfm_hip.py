@@ -148,7 +148,7 @@ def lib():
         "lfm_restore_session": (i32, [P, u32, pu8, sz]),
         "lfm_snapshot_logits": (i32, [P, pf32, sz]),
         "lfm_dispatch_count": (u64, [P]), "lfm_device_name": (i32, [P, C.c_char_p, sz]),
-        "lfm_engine_set_prefill_mode": (i32, [P, i32]),
+        "lfm_engine_set_prefill_mode": (i32, [P, i32]), "lfm_engine_h16_bytes": (i32, [P, C.POINTER(u64)]),
         "lfm_copy_time": (i32, [u64, u32, pf32]),
         "lfm_engine_run_mixer": (i32, [P, u32, pf32, u32]),
         "lfm_engine_run_ffn": (i32, [P, u32, pf32]),
@@ -796,6 +796,12 @@ class GpuEngine:
 
     def dispatch_count(self) -> int:
         return int(lib().lfm_dispatch_count(self._e))
+
+    def h16_bytes(self) -> int:
+        """lfm_engine_h16_bytes: device bytes of the binary16 GEMM weight copies."""
+        n = C.c_uint64()
+        _check(lib().lfm_engine_h16_bytes(self._e, C.byref(n)))
+        return int(n.value)
 
     @property
     def device_name(self) -> str:

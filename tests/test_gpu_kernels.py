@@ -130,6 +130,26 @@ def test_gemm_prefill_matches_f64(gpu, oracle, rows, in_dim, T):
         assert err <= 1e-5, (t, err)
 
 
+@pytest.mark.parametrize("rows,in_dim,T", [(6144, 2048, 200), (1792, 2048, 129), (8192, 256, 2048),
+                                           (1000, 512, 150), (2048, 7168, 300)])
+def test_gemm_prefill_h16_copy_bit_identical(gpu, oracle, monkeypatch, rows, in_dim, T):
+    """Large calls read the weights from a binary16 fragment copy made once
+    (k_q6_tile_h16: the A fragments the Q6_K kernels decode in registers, k-step
+    by k-step); with LFM_PREFILL_H16=0 they decode Q6_K in registers instead.  The
+    two paths run the same products in the same order, so their outputs agree
+    bit for bit; both stay within 1e-5 of the f64 oracle."""
+    raw = blocks(rows * in_dim // 256, rows * 5 + T).reshape(-1)
+    x = np.random.default_rng(T + 1).standard_normal((T, in_dim)).astype(np.float32)
+    x[1] *= 1000.0
+    w = gpu.Q6Weight(raw, rows, in_dim)
+    y_h16 = gpu.q6k_gemm(w, x)
+    monkeypatch.setenv("LFM_PREFILL_H16", "0")
+    y_q6 = gpu.q6k_gemm(w, x)
+    assert np.array_equal(y_h16.view(np.uint32), y_q6.view(np.uint32))
+    for t in sorted({0, 1, T // 2, T - 1}):
+        assert rel_l2(y_h16[t], oracle.q6k_matvec(raw, in_dim, rows, x[t])) <= 1e-5
+
+
 @pytest.mark.parametrize("T", [130, 64, 5])
 def test_gemm_prefill_block_scale_edges(gpu, oracle, T):
     """Super-block scales d that are zero (first, last, every other or every

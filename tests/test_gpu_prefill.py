@@ -236,3 +236,25 @@ def test_prefill_full_int8_scales_model(gpu, oracle):
         assert e[k][0] <= 2e-5 and e[k][1] <= 2e-5, (k, e[k])
     for k in ("whole vs oracle", "stepwise vs oracle"):
         assert e[k][0] <= 1e-3 and e[k][1] <= 1e-3, (k, e[k])
+
+
+def test_prefill_h16_copy_matches_q6_decode(gpu, real_width, monkeypatch):
+    """The whole prompt with the large-call GEMMs on the binary16 fragment copies
+    (the default) and with LFM_PREFILL_H16=0 (Q6_K decoded in registers, no copies
+    made at finalize): logits and resident state bit-identical, at real widths
+    (in_proj, out/o projections, q/k/v, dense and expert gate/up/down)."""
+    hp, tensors = real_width
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, hp.vocab, 300)]
+    g = gpu_engine(hp, tensors, ctx=512)
+    assert g.h16_bytes() > 0
+    lg = g.forward(prompt, 0)
+    sg = g.snapshot_resident_cache(len(prompt))
+    g.close()
+    monkeypatch.setenv("LFM_PREFILL_H16", "0")
+    q = gpu_engine(hp, tensors, ctx=512)
+    assert q.h16_bytes() == 0
+    lq = q.forward(prompt, 0)
+    sq = q.snapshot_resident_cache(len(prompt))
+    q.close()
+    assert np.array_equal(lg.view(np.uint32), lq.view(np.uint32))
+    assert sg == sq
