@@ -710,6 +710,8 @@ static int launch_gemm(Kernels *K, hipStream_t s, GemmArgs g, bool pair, uint32_
         // adding them costs more than the wider grid gains (the 6144-row in_proj at
         // four slices, the dense gate/up pair unsplit, the dense down at twelve)
         S = (uint32_t)std::max<size_t>(1, std::min<size_t>(S, std::min<size_t>(part_cap, GEMM_PART_SOFT) / per));
+        if (g.y_hi) // the split output is formed in the epilogue from whole sums
+            S = 1;
     }
     hipFunction_t f = small ? (pair ? (exact ? K->gemm_swiglu_t32x : K->gemm_swiglu_t32)
                                     : one_tile ? (exact ? K->gemm_q6_t32x : K->gemm_q6_t32n1) : K->gemm_q6_t32)
@@ -784,12 +786,20 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     HIPCHK(hipMalloc(&hi, hrows * in_dim * 2));
     HIPCHK(hipMalloc(&lo, hrows * in_dim * 2));
     HIPCHK(hipMalloc(&scale, (size_t)T * 4));
+    float *bscale = nullptr; // small calls: the half-block scales of the blocked rows
+    if (T <= GEMM_TOKENS && hipMalloc(&bscale, hrows * (in_dim / 128) * 4) != hipSuccess) {
+        (void)hipFree(hi);
+        (void)hipFree(lo);
+        (void)hipFree(scale);
+        return fail(LFM_EDEVICE, "lfm_q6k_gemm: scale allocation failed");
+    }
     SplitArgs sa;
     memset(&sa, 0, sizeof(sa));
     sa.x = x;
     sa.hi = hi;
     sa.lo = lo;
     sa.scale = scale;
+    sa.bscale = bscale;
     sa.T = T;
     sa.K = (uint32_t)in_dim;
     sa.mode = T <= GEMM_TOKENS ? SPLIT_BLOCKED : SPLIT_ROWMAJOR;
@@ -804,6 +814,7 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     ga.x_hi = hi;
     ga.x_lo = lo;
     ga.xscale = scale;
+    ga.bscale = bscale;
     ga.ntok = T;
     ga.zrows = (uint32_t)rows;
     ga.c = y;
@@ -823,6 +834,8 @@ extern "C" int lfm_q6k_gemm(const void *packed, uint64_t rows, uint64_t in_dim, 
     (void)hipFree(hi);
     (void)hipFree(lo);
     (void)hipFree(scale);
+    if (bscale)
+        (void)hipFree(bscale);
     if (part)
         (void)hipFree(part);
     if (tiles)
@@ -939,6 +952,11 @@ struct lfm_engine {
         float *cstate = nullptr; // the short conv's new state, until the next split copies it
         float *scale = nullptr, *logits = nullptr, *wsel = nullptr;
         uint16_t *hi = nullptr, *lo = nullptr;
+        // small calls: the blocked activations' half-block scales (bscale, written by
+        // the splits), and the SwiGLU output the gate/up GEMM stores split (hi2 / lo2
+        // / bscale2, read by the down projection)
+        float *bscale = nullptr, *bscale2 = nullptr;
+        uint16_t *hi2 = nullptr, *lo2 = nullptr;
         uint32_t *sel = nullptr, *counts = nullptr, *tok = nullptr, *slot = nullptr, *pos = nullptr;
         // router partial sums left by the out projection's reduce (small calls), and
         // whether the current layer's were written
@@ -1695,6 +1713,15 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
         HIPCHK(hipMalloc(&e->pf.hi, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.lo, hmax * 2));
         HIPCHK(hipMalloc(&e->pf.scale, TC * 4 * 4));
+        {
+            // small calls' logical rows: a padded list per expert (grouped) or the call's
+            const size_t lrows = std::max<size_t>(ts, E * ts), fmax = std::max<size_t>(hp.n_ff, hp.expert_ff);
+            const size_t h2 = std::max<size_t>(E * ts * hp.expert_ff, ts * hp.n_ff);
+            HIPCHK(hipMalloc(&e->pf.bscale, lrows * (kmax / 128) * 4));
+            HIPCHK(hipMalloc(&e->pf.bscale2, lrows * (fmax / 128) * 4));
+            HIPCHK(hipMalloc(&e->pf.hi2, h2 * 2));
+            HIPCHK(hipMalloc(&e->pf.lo2, h2 * 2));
+        }
         HIPCHK(hipMalloc(&e->pf.cstate, (size_t)dim * 2 * 4));
         const size_t tsmall = std::min<size_t>(TC, GEMM_TOKENS);
         HIPCHK(hipMalloc(&e->pf.rpart, tsmall * (dim / 256) * E * 4));
@@ -1750,6 +1777,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
     void *bufs[] = {e->st, e->ids, e->out_tokens, e->sel, e->log_ids, e->log_w, e->log_logits, e->flow, e->x, e->y, e->qkv, e->sw,
                     e->rlogits, e->rpart, e->rss, e->xw, e->logits, e->hpart, e->apart, e->rope,
                     e->pf.x, e->pf.bcx, e->pf.y, e->pf.g, e->pf.d, e->pf.part, e->pf.hi, e->pf.lo,
+                    e->pf.bscale, e->pf.bscale2, e->pf.hi2, e->pf.lo2,
                     e->pf.scale, e->pf.logits, e->pf.wsel, e->pf.sel, e->pf.counts, e->pf.tok,
                     e->pf.slot, e->pf.pos, e->pf.cstate, e->pf.rpart, e->pf.rss};
     for (void *p : bufs)
@@ -1798,6 +1826,7 @@ static SplitArgs split_args(lfm_engine *e, const float *x, const float *norm, ui
     a.hi = e->pf.hi;
     a.lo = e->pf.lo;
     a.scale = e->pf.scale;
+    a.bscale = e->pf.bscale;
     a.T = rows;
     a.K = K;
     a.mode = T > GEMM_TOKENS ? SPLIT_ROWMAJOR : grouped ? SPLIT_GROUPED : SPLIT_BLOCKED;
@@ -1857,16 +1886,19 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
     return LFM_OK;
 }
 
+// act2 (small calls): the activations are the SwiGLU output that the pair GEMM
+// stored split (pf.hi2 / lo2 / bscale2) instead of a split's.
 static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32_t ldc, uint32_t col0,
                    uint32_t mode, uint32_t *deferred = nullptr, const RouterPart *router = nullptr,
-                   bool *router_done = nullptr)
+                   bool *router_done = nullptr, bool act2 = false)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     g.w = w;
-    g.x_hi = e->pf.hi;
-    g.x_lo = e->pf.lo;
+    g.x_hi = act2 ? e->pf.hi2 : e->pf.hi;
+    g.x_lo = act2 ? e->pf.lo2 : e->pf.lo;
     g.xscale = e->pf.scale;
+    g.bscale = act2 ? e->pf.bscale2 : e->pf.bscale;
     g.ntok = T;
     g.zrows = w.rows;
     g.c = c;
@@ -1880,7 +1912,8 @@ static int pf_gemm(lfm_engine *e, const Q6Tiles &w, uint32_t T, float *c, uint32
 // Gate and up projections of a SwiGLU FFN in one launch: c = silu(Wg x) * (Wu x)
 // for `zrows` rows per weight (128 of each per workgroup).  Dense (tok null): the
 // T tokens of the call; grouped: z = expert over the per-expert token lists, as
-// pf_gemm_grouped.
+// pf_gemm_grouped.  Small calls store the output split for the down projection
+// (pf.hi2 / lo2 / bscale2, its act2 input) instead of fp32 in c.
 static int pf_gemm_swiglu(lfm_engine *e, const Q6Tiles &wg, const Q6Tiles &wu, uint32_t zrows, uint32_t T,
                           const uint32_t *tok, float *c, uint32_t ldc)
 {
@@ -1891,10 +1924,18 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6Tiles &wg, const Q6Tiles &wu, u
     g.x_hi = e->pf.hi;
     g.x_lo = e->pf.lo;
     g.xscale = e->pf.scale;
+    g.bscale = e->pf.bscale;
     g.ntok = T;
     g.zrows = zrows;
     g.c = c;
     g.ldc = ldc;
+    if (T <= GEMM_TOKENS) {
+        if (zrows % 128)
+            return fail(LFM_EINTERNAL, "prefill: split SwiGLU output needs rows in 128s, not %u", zrows);
+        g.y_hi = e->pf.hi2;
+        g.y_lo = e->pf.lo2;
+        g.y_bscale = e->pf.bscale2;
+    }
     if (!tok)
         return launch_gemm(e->K, e->stream, g, true, T, 1, T, 0, e->pf.part, GEMM_PART_BYTES / 4, &e->dispatches);
     g.tok = tok;
@@ -1911,14 +1952,15 @@ static int pf_gemm_swiglu(lfm_engine *e, const Q6Tiles &wg, const Q6Tiles &wu, u
 static int pf_gemm_grouped(lfm_engine *e, const Q6Tiles &w, uint32_t zrows, uint32_t T,
                            const uint32_t *tok, float *c, uint32_t ldc,
                            const CombinePrefillArgs *combine = nullptr, bool *combined = nullptr,
-                           ReduceCombineArgs *defer_combine = nullptr)
+                           ReduceCombineArgs *defer_combine = nullptr, bool act2 = false)
 {
     GemmArgs g;
     memset(&g, 0, sizeof(g));
     g.w = w;
-    g.x_hi = e->pf.hi;
-    g.x_lo = e->pf.lo;
+    g.x_hi = act2 ? e->pf.hi2 : e->pf.hi;
+    g.x_lo = act2 ? e->pf.lo2 : e->pf.lo;
     g.xscale = e->pf.scale;
+    g.bscale = act2 ? e->pf.bscale2 : e->pf.bscale;
     g.tok = tok;
     g.slot = e->pf.slot;
     g.counts = e->pf.counts;
@@ -2031,8 +2073,10 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         RC(pf_split(e, x, norm, T, dim, T));
         RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate.weight", l), q6tiles(e, "blk.%u.ffn_up.weight", l), ff, T,
                           nullptr, e->pf.g, ff));
-        RC(pf_split(e, e->pf.g, nullptr, T, ff, T));
-        RC(pf_gemm(e, q6tiles(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1));
+        const bool act2 = T <= GEMM_TOKENS; // small calls: the pair stored its output split
+        if (!act2)
+            RC(pf_split(e, e->pf.g, nullptr, T, ff, T));
+        RC(pf_gemm(e, q6tiles(e, "blk.%u.ffn_down.weight", l), T, x, dim, 0, 1, nullptr, nullptr, nullptr, act2));
         return LFM_OK;
     }
     const uint32_t eff = hp.expert_ff, E = hp.n_expert;
@@ -2082,14 +2126,15 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
         RC(log_routes(e, l, (uint32_t)((x - e->pf.x) / dim), T, true));
     RC(pf_gemm_swiglu(e, q6tiles(e, "blk.%u.ffn_gate_exps.weight", l), q6tiles(e, "blk.%u.ffn_up_exps.weight", l), eff,
                       T, e->pf.tok, e->pf.g, eff));
-    RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
+    if (!small) // (small calls: the pair stored its output split, per expert list)
+        RC(pf_split(e, e->pf.g, nullptr, 4 * T, eff, T, true, 1)); // slots are token * 4 + rank
     CombinePrefillArgs cb{e->pf.d, e->pf.wsel, x, T, dim, hp.n_used};
     // small calls before another layer: the combine is left to the next layer's
     // first split (its rows are this call's, x = e->pf.x)
     const bool defer = small && defer_ok && x == e->pf.x;
     bool combined = false;
     RC(pf_gemm_grouped(e, q6tiles(e, "blk.%u.ffn_down_exps.weight", l), dim, T, e->pf.slot, e->pf.d, dim, &cb,
-                       &combined, defer ? &e->pf.comb : nullptr));
+                       &combined, defer ? &e->pf.comb : nullptr, small));
     if (defer) {
         if (!combined) // one K slice: the down projection wrote d itself
             e->pf.comb = ReduceCombineArgs{e->pf.d, e->pf.wsel, x, 1, T, dim, hp.n_used};

@@ -229,6 +229,10 @@ struct SplitArgs {
     float eps;
     uint16_t *hi, *lo;   // binary16, layout by `mode`
     float *scale;        // [T], per source row
+    // blocked modes: the scale of logical row L's half-block h (k = 128 h .. + 127)
+    // at bscale[L * (K / 128) + h], which the small-call GEMMs read (a split row has
+    // one scale: it is written to each of the row's half-blocks)
+    float *bscale;
     uint32_t T, K;
     uint32_t mode;       // SPLIT_*
     // SPLIT_GROUPED: source row t feeds slots s = t * spr .. t * spr + spr - 1 (spr 4:
@@ -334,7 +338,18 @@ struct GemmArgs {
     Q6Tiles w;
     Q6Tiles w2;             // pair kernel: the up weight (gate in w), same shape
     const uint16_t *x_hi, *x_lo;
-    const float *xscale;
+    const float *xscale;    // large calls: per activation row
+    // small calls: per logical (blocked) row L and 128-wide half-block h of K, at
+    // bscale[L * (K / 128) + h]: row L's activations of half-block h were stored
+    // divided by it (a power of two)
+    const float *bscale;
+    // small-call pair form, unsplit (ksplit 1), y_hi set: the SwiGLU output is stored
+    // binary16 hi + lo in the blocked layout of width zrows instead of fp32 in c: token
+    // column n of group z is logical row (tok ? z * rpz : 0) + n, each 128 rows of a
+    // workgroup with the power-of-two scale of their largest magnitude (y_bscale, as
+    // bscale above), so that it feeds the next small-call GEMM with no split launch
+    uint16_t *y_hi, *y_lo;
+    float *y_bscale;
     const uint32_t *tok;    // [z][list_stride] activation rows, nullable
     const uint32_t *slot;   // [z][list_stride] output rows, nullable
     const uint32_t *counts; // [z] token counts, nullable (then ntok)

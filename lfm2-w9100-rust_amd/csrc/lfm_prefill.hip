@@ -20,6 +20,7 @@
 #include "wave_ops.h"
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define WG_THREADS 256
@@ -128,6 +129,12 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
     const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
     if (tid == 0)
         a.scale[t] = scale;
+    if (a.bscale && a.mode != SPLIT_ROWMAJOR) { // uniform
+        const uint32_t nh = a.K >> 7;
+        for (uint32_t q = 0; q < nl; ++q) // uniform
+            for (uint32_t h = tid; h < nh; h += WG_THREADS)
+                a.bscale[(size_t)L[q] * nh + h] = scale;
+    }
     half8 *hi = reinterpret_cast<half8 *>(a.hi), *lo = reinterpret_cast<half8 *>(a.lo);
 #pragma unroll
     for (int i = 0; i < SPLIT_NP; ++i) {
@@ -1398,6 +1405,8 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // below 2^31 (the host bounds the activation copies).
     const uint32_t lt = (tokl ? z * (a.rpz >> 5) : 0u) + ny;
     const uint32_t bsrc = 2 * (lt * (K >> 3) * 256 + (2 * wave + p) * 256 + min(lr, ntok - 1 - n0) * 8);
+    // this lane's token column's activation scales: logical row lrow, half-blocks of K
+    const float *bsc = a.bscale + (size_t)(lt * 32 + min(lr, ntok - 1 - n0)) * (K >> 7);
     // G + 4 stage buffers of 8 KB, hi then lo (stage s in buffer s % (G + 4));
     // every LDS read of them is in assembly, so the compiler adds no waits for the
     // tiles in flight and the buffer can be picked at run time
@@ -1420,10 +1429,13 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     };
     // this lane's A rows' block scales d, block kb of the slice, as binary16 bits
     // (converted where used, so the load does not wait for the weights issued before it)
-    auto loadD = [=](uint32_t kb, uint32_t (&d)[NI]) {
+    // and the activation scales of its half-blocks (two loads more)
+    auto loadD = [=](uint32_t kb, uint32_t (&d)[NI], float (&ts)[2]) {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             d[i] = tile_d(PAIR && i ? a.w2.base : a.w.base, ntb, (size_t)wt[i] * nb + kb0 + kb, lr);
+        ts[0] = bsc[2 * (kb0 + kb)];
+        ts[1] = bsc[2 * (kb0 + kb) + 1];
     };
     floatx16 acc[NI];
 #pragma unroll
@@ -1438,29 +1450,46 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     // (in assembly: the compiler would wait for the activation tiles in flight
     // before reading an LDS array it cannot tell apart from their buffers)
     __shared__ __attribute__((aligned(16))) float rowf[4][NI][32];
-    auto by_row = [&](int i, float v) {
+    // (times c, this lane's own factor: its token column's activation-scale ratio)
+    auto by_row = [&](int i, float v, float c) {
         floatx4 f[4]; // lanes lr and lr + 32 store the same value
         lds_rowf(lds_addr(&rowf[wave][i][lr]), v, lds_addr(&rowf[wave][i][4 * p]), f);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc[i][4 * k + j] *= f[k][j];
+                acc[i][4 * k + j] *= f[k][j] * c;
     };
     float u[NI], dcur[NI];
     uint32_t dnext[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
         u[i] = 1.0f, dnext[i] = 0;
+    // The activations of half-block h of this lane's column were stored divided by
+    // s_h: the accumulators hold sum_h s_h P_h / ut, multiplied by ut / s_h when
+    // half-block h starts (powers of two: exact) and by the final ut at the end.
+    float ut = 1.0f, tnext[2] = {1.0f, 1.0f}, tcur1 = 1.0f;
     auto enter_block = [&](bool first) { // accumulators: sum_b d_b P_b / u
+        const float c = ut / tnext[0];
+        ut = tnext[0];
+        tcur1 = tnext[1];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const bool nz = dcur[i] != 0.f;
             const float r = nz ? u[i] / dcur[i] : 1.0f;
             u[i] = nz ? dcur[i] : u[i];
             if (!first)
-                by_row(i, r);
+                by_row(i, r, c);
         }
+    };
+    auto enter_half = [&]() { // the block's second half-block
+        const float c = ut / tcur1;
+        ut = tcur1;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][e] *= c;
     };
     const uint32_t nst = nbl * 4;
 
@@ -1480,6 +1509,8 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
                 dcur[i] = half_bits_to_float(dnext[i]);
             enter_block(kb == 0);
         }
+        if (j == 2)
+            enter_half();
         issue_fence();
         if (j % G == 0) {
 #pragma unroll
@@ -1495,7 +1526,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         if ((j == JA || j == JB) && more) {
             loadA(2 * (kb + 1) + (j == JB), N[j == JB]);
             if (j == JA)
-                loadD(kb + 1, dnext);
+                loadD(kb + 1, dnext, tnext);
         }
         issue_fence();
         const int q = j & 1;
@@ -1591,7 +1622,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             asm volatile("" ::: "memory");
             if (j == 1) {
                 if (more)
-                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 6 * NI));
+                    __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(4 + 6 * NI + 2));
                 else
                     __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
             } else {
@@ -1607,7 +1638,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
             // scales of this stage (6 NI)
             asm volatile("" ::: "memory");
             if (more)
-                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(8 + 6 * NI));
+                __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(8 + 6 * NI + 2));
             else
                 __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(0));
             asm volatile("" ::: "memory");
@@ -1641,7 +1672,7 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
     }
     issue_fence();
     loadA(0, S0[0]);
-    loadD(0, dnext);
+    loadD(0, dnext, tnext);
     issue_fence();
     if (G == 2) {
         loadB(2);
@@ -1662,12 +1693,59 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
         block(kb, S0, S1);
 #pragma unroll
     for (int i = 0; i < NI; ++i)
-        by_row(i, u[i]);
+        by_row(i, u[i], 1.0f);
+    const float xs = ut;
+    if (PAIR && a.y_hi) { // uniform (ksplit 1): the SwiGLU output goes out split
+        float v[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float g = acc[0][e] * xs, uu = acc[NI - 1][e] * xs;
+            v[e] = g / (1.0f + expf(-g)) * uu;
+        }
+        // the largest magnitude of this column's 128 rows: 16 per lane, both lane
+        // halves, the four waves (lanes past the last column hold its copies)
+        float m = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            m = fmaxf(m, fabsf(v[e]));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        __shared__ float cmax[4][32];
+        if (p == 0)
+            cmax[wave][lr] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(cmax[0][lr], cmax[1][lr]), fmaxf(cmax[2][lr], cmax[3][lr]));
+        int ex = 0;
+        if (m > 0.f && m <= 3.0e38f)
+            frexpf(m, &ex);
+        const float sc = m > 0.f ? ldexpf(1.0f, ex - 14) : 1.0f, rs = 1.0f / sc;
+        const uint32_t n = n0 + lr;
+        if (n >= ntok)
+            return;
+        const uint32_t L = (tokl ? z * a.rpz : 0u) + n, Ko = a.zrows;
+        if (wave == 0 && p == 0)
+            a.y_bscale[(size_t)L * (Ko >> 7) + (m0 >> 7)] = sc;
+        // element e is row m0 + 32 wave + 8 (e / 4) + 4 p + e % 4: per e / 4, four
+        // consecutive k of one 8-wide piece, the lane half p's four halves of it
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            half4v h, l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                _Float16 hh, ll;
+                split_f16(v[4 * q + e] * rs, hh, ll);
+                h[e] = hh;
+                l[e] = ll;
+            }
+            const size_t o = blocked_index(L, m0 + lb[0] + 8 * q + 4 * p, Ko);
+            *reinterpret_cast<half4v *>(a.y_hi + o) = h;
+            *reinterpret_cast<half4v *>(a.y_lo + o) = l;
+        }
+        return;
+    }
     const uint32_t n = n0 + lr;
     if (n >= ntok)
         return;
     const uint32_t orow = slotl ? slotl[n] : n;
-    const float xs = a.xscale[tokl ? tokl[n] : n];
     if (a.ksplit > 1) {
         constexpr uint32_t NW = PAIR ? 2 : 1;
 #pragma unroll
