@@ -966,6 +966,8 @@ struct lfm_engine {
         // split to apply (comb_pending)
         ReduceCombineArgs comb{};
         bool comb_pending = false;
+        // small calls: the conv state the next split moves from cstate into place
+        float *state_pending = nullptr;
     } pf;
     uint32_t *host_ids = nullptr;   // pinned staging for prompt ids (ctx entries)
 
@@ -1854,6 +1856,12 @@ static int pf_split(lfm_engine *e, const float *x, const float *norm, uint32_t r
     a.copy_src = copy_src;
     a.copy_dst = copy_dst;
     a.copy_n = copy_n;
+    if (e->pf.state_pending && !copy_src) { // a short conv's new state (small calls)
+        a.copy_src = e->pf.cstate;
+        a.copy_dst = e->pf.state_pending;
+        a.copy_n = 2 * e->hp.dim;
+        e->pf.state_pending = nullptr;
+    }
     if (lists) {
         a.tok = e->pf.tok;
         a.slot = e->pf.slot;
@@ -1998,10 +2006,19 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         uint32_t S = 1;
         RC(pf_gemm(e, q6tiles(e, "blk.%u.shortconv.in_proj.weight", l), T, e->pf.bcx, 3 * dim, 0, 0, &S));
         ConvPrefillArgs c{S > 1 ? e->pf.part : e->pf.bcx, f32(e, "blk.%u.shortconv.conv.weight", l), e->conv[l],
-                          e->pf.cstate, e->pf.y, T, dim, S};
+                          e->pf.cstate, e->pf.y, T, dim, S, nullptr, nullptr, nullptr};
+        if (T <= GEMM_TOKENS) { // small calls: the conv stores y split for the out projection
+            if (dim % 256)
+                return fail(LFM_EINTERNAL, "prefill conv: width %u not a multiple of 256", dim);
+            c.y_hi = e->pf.hi;
+            c.y_lo = e->pf.lo;
+            c.y_bscale = e->pf.bscale;
+        }
         RC(launch(e->K->conv_prefill, dim3((dim + 255) / 256, T), 0, e->stream, c));
-        // the split of y also moves the new conv state into place
-        RC(pf_split(e, e->pf.y, nullptr, T, dim, T, false, 1, e->pf.cstate, e->conv[l], 2 * dim));
+        if (T <= GEMM_TOKENS) // the FFN's split moves the new conv state into place
+            e->pf.state_pending = e->conv[l];
+        else // the split of y also moves the new conv state into place
+            RC(pf_split(e, e->pf.y, nullptr, T, dim, T, false, 1, e->pf.cstate, e->conv[l], 2 * dim));
         RC(pf_out_proj(e, l, q6tiles(e, "blk.%u.shortconv.out_proj.weight", l), T));
         e->dispatches += 1;
         return LFM_OK;
@@ -2155,6 +2172,7 @@ static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
     if (e->route_log)
         std::fill(e->log_n.begin(), e->log_n.end(), 0u);
     e->pf.comb_pending = false;
+    e->pf.state_pending = nullptr;
     EmbedRowsArgs em{q6(e, "token_embd.weight"), e->ids, e->pf.x, T};
     RC(launch(e->K->embed_rows, dim3((T + 3) / 4), 0, e->stream, em));
     e->dispatches += 1;
@@ -2167,6 +2185,8 @@ static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
     }
     if (e->pf.comb_pending) // cannot happen: the last layer combines itself
         return fail(LFM_ESTATE, "prefill: a combine was left pending");
+    if (e->pf.state_pending) // cannot happen: every mixer is followed by its FFN's split
+        return fail(LFM_ESTATE, "prefill: a conv state was left unmoved");
     HIPCHK(hipMemcpyAsync(e->x, e->pf.x + (size_t)(T - 1) * hp.dim, hp.dim * 4,
                           hipMemcpyDeviceToDevice, e->stream));
     return LFM_OK;

@@ -395,6 +395,12 @@ struct ConvPrefillArgs {  // gated short conv over T tokens, parallel in t
     float *state_next;    // [dim][2] after it (copied over `state` by the next split)
     float *y;             // [T][dim]
     uint32_t T, dim, ksplit;
+    // nullable (small calls): y stored binary16 hi + lo in the blocked layout (logical
+    // row t, width dim) with the power-of-two scale of each 128 channels' largest
+    // magnitude at y_bscale[t * (dim / 128) + ch / 128], instead of fp32 in y, so
+    // that the output projection reads it with no split launch
+    uint16_t *y_hi, *y_lo;
+    float *y_bscale;
 };
 
 struct RopeKvArgs {       // per token: q/k head norm + RoPE, K/V to the binary16 cache

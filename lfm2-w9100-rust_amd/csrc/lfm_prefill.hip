@@ -1934,7 +1934,30 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_conv_prefill(const Co
     co = co + s0 * w3[0];
     co = co + s1 * w3[1];
     co = co + bx * w3[2];
-    a.y[(size_t)t * a.dim + ch] = v[6] * co;
+    const float yv = v[6] * co;
+    if (a.y_hi) { // uniform
+        // the largest magnitude of this half-block's 128 channels (waves 2h, 2h + 1)
+        __shared__ float hmax[4];
+        const float m = wave_max(fabsf(yv));
+        if ((threadIdx.x & 63) == 0)
+            hmax[threadIdx.x >> 6] = m;
+        __syncthreads();
+        const uint32_t w2 = (threadIdx.x >> 7) * 2;
+        const float mh = fmaxf(hmax[w2], hmax[w2 + 1]);
+        int ex = 0;
+        if (mh > 0.f && mh <= 3.0e38f)
+            frexpf(mh, &ex);
+        const float sc = mh > 0.f ? ldexpf(1.0f, ex - 14) : 1.0f;
+        if ((threadIdx.x & 127) == 0)
+            a.y_bscale[(size_t)t * (a.dim >> 7) + (ch >> 7)] = sc;
+        _Float16 hh, ll;
+        split_f16(yv * (1.0f / sc), hh, ll);
+        const size_t o = blocked_index(t, ch, a.dim);
+        reinterpret_cast<_Float16 *>(a.y_hi)[o] = hh;
+        reinterpret_cast<_Float16 *>(a.y_lo)[o] = ll;
+    } else {
+        a.y[(size_t)t * a.dim + ch] = yv;
+    }
     if (t + 1 == a.T) {
         a.state_next[ch * 2] = s1;
         a.state_next[ch * 2 + 1] = bx;
