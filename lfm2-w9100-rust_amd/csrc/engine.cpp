@@ -2048,13 +2048,22 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         at.part = e->pf.part;
         at.kb_per = kb_per;
         RC(launch(e->K->attn_prefill, dim3(qtiles, kv, nsplit), 0, e->stream, at));
-        AttnMergeSplitArgs mg{e->pf.part, e->pf.y, T, hp.heads, nsplit};
+        AttnMergeSplitArgs mg{e->pf.part, e->pf.y, T, hp.heads, nsplit, nullptr, nullptr, nullptr};
+        // small calls: the merge stores the output split for the output projection
+        const bool direct = T <= GEMM_TOKENS && hp.heads % 4 == 0 && hp.heads * 64 == dim;
+        if (direct) {
+            mg.y_hi = e->pf.hi;
+            mg.y_lo = e->pf.lo;
+            mg.y_bscale = e->pf.bscale;
+        }
         RC(launch(e->K->attn_merge_split, dim3(T, (hp.heads + 3) / 4), 0, e->stream, mg));
         e->dispatches += 1;
+        if (!direct)
+            RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     } else {
         RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
+        RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     }
-    RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     RC(pf_out_proj(e, l, q6tiles(e, "blk.%u.attn_output.weight", l), T));
     e->dispatches += 2;
     return LFM_OK;

@@ -429,6 +429,12 @@ struct AttnMergeSplitArgs { // out[t][h] = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s 
     const float *part;
     float *out;
     uint32_t T, heads, nsplit;
+    // nullable (small calls): out stored binary16 hi + lo in the blocked layout
+    // (logical row t, width heads * 64) with the power-of-two scale of each 128
+    // values' largest magnitude at y_bscale[t * (heads * 64 / 128) + k / 128], as the
+    // short conv's, for the output projection with no split launch
+    uint16_t *y_hi, *y_lo;
+    float *y_bscale;
 };
 
 struct RouterPrefillArgs {  // logits[t][e] = W_r rmsnorm(x_t)

@@ -2254,7 +2254,29 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_merge_split(cons
                 num += f * o[j];
             }
     }
-    a.out[(size_t)t * a.heads * 64 + h * 64 + d] = num / den;
+    const float yv = num / den;
+    if (a.y_hi) { // uniform (heads a multiple of 4): waves 2i, 2i + 1 hold half-block i
+        __shared__ float hmax[4];
+        const float m = wave_max(fabsf(yv));
+        if (d == 0)
+            hmax[threadIdx.x >> 6] = m;
+        __syncthreads();
+        const uint32_t w2 = (threadIdx.x >> 7) * 2, K = a.heads * 64, k = h * 64 + d;
+        const float mh = fmaxf(hmax[w2], hmax[w2 + 1]);
+        int ex = 0;
+        if (mh > 0.f && mh <= 3.0e38f)
+            frexpf(mh, &ex);
+        const float sc = mh > 0.f ? ldexpf(1.0f, ex - 14) : 1.0f;
+        if ((threadIdx.x & 127) == 0)
+            a.y_bscale[(size_t)t * (K >> 7) + (k >> 7)] = sc;
+        _Float16 hh, ll;
+        split_f16(yv * (1.0f / sc), hh, ll);
+        const size_t o = blocked_index(t, k, K);
+        reinterpret_cast<_Float16 *>(a.y_hi)[o] = hh;
+        reinterpret_cast<_Float16 *>(a.y_lo)[o] = ll;
+        return;
+    }
+    a.out[(size_t)t * a.heads * 64 + h * 64 + d] = yv;
 }
 
 // ------------------------------------------------------------------ FFN pieces
