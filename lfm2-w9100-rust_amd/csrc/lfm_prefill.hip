@@ -1122,9 +1122,9 @@ k_gemm_q6_swiglu_x(const GemmArgs a)
 // The large-call GEMM over the binary16 fragment copy (Q6Tiles::h16, made once at
 // finalize by k_q6_tile_h16): gemm_body's workgroup tiles, activation staging,
 // block-scale folding and epilogue, but each wave loads its A fragments ready-made,
-// one 16-byte load per lane, fragment and k-step (1 KB contiguous per wave), a
-// stage ahead, instead of loading Q6_K bytes and decoding them: the k-loop is
-// loads, LDS fragment reads and MFMAs.  The products are those of gemm_body (the
+// one 16-byte load per lane, fragment and k-step (1 KB contiguous per wave),
+// instead of loading Q6_K bytes and decoding them: the k-loop is loads, LDS
+// fragment reads and MFMAs.  The products are those of gemm_body (the
 // copy holds the fragments its decode forms).  Large calls only: one K slice.
 template <bool PAIR, int NJ>
 __device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
@@ -1219,13 +1219,15 @@ __device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
     uint32_t dnext = 0;
     float dnextf = 0.f;
 
-    // Stage st = 4 kb + sb over tile buffer sb % 2 and fragment set F (st % 2):
-    // issue stage st + 1's tile into the other buffer (and at sb = 0 block kb + 1's
-    // scale), then the k-steps, each followed by the load of stage st + 2's fragments
-    // of that k-step into the registers it just used (so fragments are requested
-    // about two stages ahead with two sets of registers), then wait for stage st +
-    // 1's tile (the 8 fragment loads issued after it stay in flight: loads retire in
-    // issue order) and meet at the barrier.
+    // Stage st = 4 kb + sb over tile buffer sb % 2 and the fragments F: issue stage
+    // st + 1's tile into the other buffer (and at sb = 0 block kb + 1's scale), then
+    // the k-steps, each followed by the load of stage st + 1's fragments of that
+    // k-step into the registers it just used (one register set: in isolated runs 5-9 %
+    // faster than a second set for two stages ahead, the same in the whole prompt,
+    // with 24 fewer VGPRs; loads issued together at the stage start were slower
+    // still), then wait for stage st + 1's tile (the 8 fragment loads
+    // issued after it stay in flight: loads retire in issue order) and meet at the
+    // barrier.
     auto stage = [&](uint32_t st, const _Float16 *__restrict__ bh, const _Float16 *__restrict__ bl,
                      _Float16 *__restrict__ nh, _Float16 *__restrict__ nl, half8 (&F)[2][4]) {
         const uint32_t kb = st >> 2, sb = st & 3;
@@ -1233,7 +1235,7 @@ __device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
         // block, the last ones again, unused): a load under a branch leaves the
         // compiler's wait counts unknown at the join, after which the first use of
         // a fragment would wait for every load issued after it.
-        const uint32_t sn = min(st + 1, nst - 1), s2 = min(st + 2, nst - 1);
+        const uint32_t sn = min(st + 1, nst - 1);
         if (sb == 0 && kb > 0)
             rescale(kb & 1);
         issue_fence();
@@ -1262,15 +1264,14 @@ __device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(F[i][ks], bfl[j & 1], acc[i][j], 0, 0, 0);
             }
             issue_fence();
-            loadF(s2, ks, F);
+            loadF(sn, ks, F);
             issue_fence();
         }
         if (sb == 2 && kb + 1 < nb) // publish block kb + 1's scale (landed by stage 4 kb + 1's wait)
             set_d((kb + 1) & 1, dnextf);
         // stage st + 1's tile has landed (this wave's pieces; the wait also retires
-        // its LDS reads and writes, the scale issued after the tile, and stage st +
-        // 1's fragments, issued before it); stage st + 2's fragments stay in flight,
-        // and the barrier publishes the tile
+        // its LDS reads and writes and the scale issued after the tile); stage st +
+        // 1's fragments stay in flight, and the barrier publishes the tile
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(WAITCNT_VM_LGKM0(8));
         __builtin_amdgcn_s_barrier();
@@ -1278,21 +1279,19 @@ __device__ __forceinline__ void gemm_body_h(const GemmArgs &a)
         if (sb == 1)
             dnextf = half_bits_to_float(dnext);
     };
-    half8 F0[2][4], F1[2][4];
+    half8 F[2][4];
     lds_dma_stage<NJ>(xh, xl, boff, 0, wave, Bh0, Bl0);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        loadF(0, ks, F0);
-        loadF(1, ks, F1); // nst >= 4
-    }
+    for (int ks = 0; ks < 4; ++ks)
+        loadF(0, ks, F);
     set_d(0, half_bits_to_float(loadD(0)));
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (uint32_t kb = 0; kb < nb; ++kb) {
-        stage(4 * kb + 0, Bh0, Bl0, Bh1, Bl1, F0);
-        stage(4 * kb + 1, Bh1, Bl1, Bh0, Bl0, F1);
-        stage(4 * kb + 2, Bh0, Bl0, Bh1, Bl1, F0);
-        stage(4 * kb + 3, Bh1, Bl1, Bh0, Bl0, F1);
+        stage(4 * kb + 0, Bh0, Bl0, Bh1, Bl1, F);
+        stage(4 * kb + 1, Bh1, Bl1, Bh0, Bl0, F);
+        stage(4 * kb + 2, Bh0, Bl0, Bh1, Bl1, F);
+        stage(4 * kb + 3, Bh1, Bl1, Bh0, Bl0, F);
     }
     __syncthreads();
     rsh[0][tid] = u;
@@ -1333,7 +1332,8 @@ k_gemm_h16(const GemmArgs a)
     gemm_body_h<false, 4>(a);
 }
 
-extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+// (152 VGPRs: three waves per SIMD)
+extern "C" __global__ __launch_bounds__(GEMM_NTH) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 k_gemm_h16_n64(const GemmArgs a)
 {
     gemm_body_h<false, 2>(a);
