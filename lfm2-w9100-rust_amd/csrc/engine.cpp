@@ -2032,7 +2032,7 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
                  start, hp.heads, kv, e->ctx, S};
     RC(launch(e->K->rope_kv_prefill, dim3(T), 0, e->stream, r));
     AttnPrefillArgs at{e->pf.bcx, e->kc[l], e->vc[l], e->pf.y, 1.0f / sqrtf((float)hp.head_dim), T,
-                       start, hp.heads, kv, e->ctx, nullptr, 0};
+                       start, hp.heads, kv, e->ctx, nullptr, 0, 0};
     // Few query tiles (small calls, e.g. 64-token chunks late in the context): the
     // keys are split into ranges (about 256 workgroups, at least 4 blocks of 32
     // keys each) whose softmax states k_attn_merge_split combines.
@@ -2061,7 +2061,8 @@ static int pf_mixer(lfm_engine *e, uint32_t l, uint32_t T, uint32_t start)
         if (!direct)
             RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     } else {
-        RC(launch(e->K->attn_prefill, dim3(qtiles, kv), 0, e->stream, at));
+        at.paired = 1; // a long and a short query tile per workgroup
+        RC(launch(e->K->attn_prefill, dim3((qtiles + 1) / 2, kv), 0, e->stream, at));
         RC(pf_split(e, e->pf.y, nullptr, T, dim, T));
     }
     RC(pf_out_proj(e, l, q6tiles(e, "blk.%u.attn_output.weight", l), T));

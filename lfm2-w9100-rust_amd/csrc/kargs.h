@@ -423,6 +423,9 @@ struct AttnPrefillArgs {  // causal GQA attention of T queries at positions star
     // writes (max, sum, o[64]) of each (query, head) to part[((s T + t) heads + h) 66]
     float *part;
     uint32_t kb_per;
+    // nonzero (no key split): grid x = ceil(query tiles / 2), workgroup b takes
+    // query tiles n - 1 - b and b
+    uint32_t paired;
 };
 
 struct AttnMergeSplitArgs { // out[t][h] = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s

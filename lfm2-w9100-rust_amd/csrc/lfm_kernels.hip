@@ -842,7 +842,8 @@ __device__ __forceinline__ float head_norm_rope(float v, const HeadIn in, float 
     const float ss = wave_sum(v * v);
     const float inv = 1.0f / sqrtf(ss / 64.0f + eps);
     v *= inv * in.w;
-    const float other = __shfl_xor(v, 32, 64);
+    const float2v vh = wave_halves(v);
+    const float other = d < 32 ? vh[1] : vh[0];
     const float cs = in.cs, sn = in.sn;
     // lane d < 32 holds x0 (partner x1); lane d >= 32 holds x1 (partner x0)
     return d < 32 ? v * cs - other * sn : other * sn + v * cs;

@@ -2001,7 +2001,8 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_rope_kv_prefill(const
         const float ss = wave_sum(x * x);
         const float inv = 1.0f / sqrtf(ss / 64.0f + a.eps);
         x *= inv * w;
-        const float other = __shfl_xor(x, 32, 64);
+        const float2v xh = wave_halves(x);
+        const float other = lane < 32 ? xh[1] : xh[0];
         return lane < 32 ? x * c - other * s : other * s + x * c;
     };
 #pragma unroll
@@ -2044,11 +2045,9 @@ typedef float floatx16a __attribute__((ext_vector_type(16)));
 #define FA_VROW 36 // halves per transposed-V row in LDS (32 + 4)
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const AttnPrefillArgs a)
 {
-    // the longest (latest) query tiles are dispatched first
-    const uint32_t kh = blockIdx.y, t0 = (gridDim.x - 1 - blockIdx.x) * FA_Q;
-    if (t0 >= a.T)
-        return;
-    const uint32_t G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64, stride = dim + 2 * hdkv;
+    const uint32_t ntile = (a.T + FA_Q - 1) / FA_Q;
+    const uint32_t kh = blockIdx.y, G = a.heads / a.kv, dim = a.heads * 64, hdkv = a.kv * 64,
+                   stride = dim + 2 * hdkv;
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31,
                    lh = lane >> 5;
     __shared__ __attribute__((aligned(16))) _Float16 Ks[2][FA_K * FA_KROW];
@@ -2059,156 +2058,176 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_attn_prefill(const At
     // Scores are kept in log2 units (q scaled by scale * log2 e), so the softmax
     // exponentials are single v_exp_f32 (2^x): 2^(s2 - m2) = e^(s - m).
     const float qscale = a.scale * 1.4426950408889634f;
-    const uint32_t tq = t0 + lq;
-    half8 qh[4], ql[4];
-    {
-        const float *qrow = a.qkv + (size_t)(tq < a.T ? tq : a.T - 1) * stride + h * 64;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const float4 v0 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh);
-            const float4 v1 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh + 4);
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float x = v[i] * qscale;
-                qh[ks][i] = (_Float16)x;
-                ql[ks][i] = (_Float16)(x - (float)qh[ks][i]);
-            }
-        }
-    }
-    const uint32_t qpos = a.start + tq; // causal limit of this lane's query
-    const uint32_t tmax = min(t0 + FA_Q, a.T) - 1;
-    // key blocks [kb_lo, kb_hi) of this workgroup: all the causal ones, or one range
-    const uint32_t nblk_all = (a.start + tmax) / FA_K + 1;
-    const uint32_t kb_lo = a.kb_per ? blockIdx.z * a.kb_per : 0;
-    const uint32_t kb_hi = a.kb_per ? min(nblk_all, kb_lo + a.kb_per) : nblk_all;
-    const uint32_t nblk = kb_hi > kb_lo ? kb_hi - kb_lo : 0;
-    // staging: thread -> key row tid / 8, dims (tid % 8) * 8 .. +7
-    const uint32_t sr = tid >> 3, sp = (tid & 7) * 8;
-    const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
-    const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
-    auto load_kv = [&](uint32_t blk, uint4 &kr, uint4 &vr) { // blk counts from kb_lo
-        const uint32_t pos = min((kb_lo + blk) * FA_K + sr, a.ctx - 1);
-        kr = *reinterpret_cast<const uint4 *>(kg + (size_t)pos * 64 + sp);
-        vr = *reinterpret_cast<const uint4 *>(vg + (size_t)pos * 64 + sp);
-    };
-    auto store_kv = [&](uint32_t buf, uint4 kr, uint4 vr) {
-        *reinterpret_cast<uint4 *>(&Ks[buf][sr * FA_KROW + sp]) = kr;
-        const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vr);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            reinterpret_cast<uint16_t *>(Vt[buf])[(sp + i) * FA_VROW + sr] = v16[i];
-    };
-    floatx16a o0, o1;
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-        o0[e] = 0.f, o1[e] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    uint4 kr, vr;
-    if (nblk > 0) {
-        load_kv(0, kr, vr);
-        store_kv(0, kr, vr);
-    }
-    if (nblk > 1)
-        load_kv(1, kr, vr);
-    __syncthreads();
-    for (uint32_t blk = 0; blk < nblk; ++blk) {
-        const uint32_t buf = blk & 1;
-        if (active) {
-            // S^T[key][query] for the block's 32 keys
-            floatx16a sacc;
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                sacc[e] = 0.f;
+    // The longest (latest) query tiles are dispatched first.  Paired: workgroup b
+    // runs tile ntile - 1 - b and then tile b (every workgroup near ntile + 1 key
+    // blocks, so the causal triangle does not leave the long tiles sharing their
+    // SIMDs with short ones); the middle tile of an odd count runs once.
+    for (uint32_t pass = 0; pass < (a.paired ? 2u : 1u); ++pass) {
+        const uint32_t tile = pass ? blockIdx.x : a.paired ? ntile - 1 - blockIdx.x : gridDim.x - 1 - blockIdx.x;
+        if (tile >= ntile || (pass && tile >= ntile - 1 - blockIdx.x)) // uniform
+            break;
+        const uint32_t t0 = tile * FA_Q;
+        const uint32_t tq = t0 + lq;
+        half8 qh[4], ql[4];
+        {
+            const float *qrow = a.qkv + (size_t)(tq < a.T ? tq : a.T - 1) * stride + h * 64;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const half8 kf = *reinterpret_cast<const half8 *>(&Ks[buf][lq * FA_KROW + ks * 16 + 8 * lh]);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], sacc, 0, 0, 0);
-            }
-            // lane's items: keys 8*(e/4) + 4*lh + e%4 of the block, query lq.  A block
-            // that ends before the tile's first query position needs no mask; its
-            // scores are finite, and so is the new maximum.
-            const bool diag = (kb_lo + blk + 1) * FA_K > a.start + t0;
-            float bm = -INFINITY;
-            if (diag) {
+                const float4 v0 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh);
+                const float4 v1 = *reinterpret_cast<const float4 *>(qrow + ks * 16 + 8 * lh + 4);
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t kpos = (kb_lo + blk) * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
-                    if (kpos > qpos)
-                        sacc[e] = -INFINITY;
+                for (int i = 0; i < 8; ++i) {
+                    const float x = v[i] * qscale;
+                    qh[ks][i] = (_Float16)x;
+                    ql[ks][i] = (_Float16)(x - (float)qh[ks][i]);
                 }
             }
+        }
+        const uint32_t qpos = a.start + tq; // causal limit of this lane's query
+        const uint32_t tmax = min(t0 + FA_Q, a.T) - 1;
+        // key blocks [kb_lo, kb_hi) of this workgroup: all the causal ones, or one range
+        const uint32_t nblk_all = (a.start + tmax) / FA_K + 1;
+        const uint32_t kb_lo = a.kb_per ? blockIdx.z * a.kb_per : 0;
+        const uint32_t kb_hi = a.kb_per ? min(nblk_all, kb_lo + a.kb_per) : nblk_all;
+        const uint32_t nblk = kb_hi > kb_lo ? kb_hi - kb_lo : 0;
+        // staging: thread -> key row tid / 8, dims (tid % 8) * 8 .. +7
+        const uint32_t sr = tid >> 3, sp = (tid & 7) * 8;
+        const uint16_t *kg = a.kcache + (size_t)kh * a.ctx * 64;
+        const uint16_t *vg = a.vcache + (size_t)kh * a.ctx * 64;
+        auto load_kv = [&](uint32_t blk, uint4 &kr, uint4 &vr) { // blk counts from kb_lo
+            const uint32_t pos = min((kb_lo + blk) * FA_K + sr, a.ctx - 1);
+            kr = *reinterpret_cast<const uint4 *>(kg + (size_t)pos * 64 + sp);
+            vr = *reinterpret_cast<const uint4 *>(vg + (size_t)pos * 64 + sp);
+        };
+        auto store_kv = [&](uint32_t buf, uint4 kr, uint4 vr) {
+            *reinterpret_cast<uint4 *>(&Ks[buf][sr * FA_KROW + sp]) = kr;
+            const uint16_t *v16 = reinterpret_cast<const uint16_t *>(&vr);
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                bm = fmaxf(bm, sacc[e]);
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-            const float mn = fmaxf(m, bm);
-            const float r = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.f;
-            float ps = 0.f;
-            half8 phi[2], plo[2];
+            for (int i = 0; i < 8; ++i)
+                reinterpret_cast<uint16_t *>(Vt[buf])[(sp + i) * FA_VROW + sr] = v16[i];
+        };
+        floatx16a o0, o1;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float p = !diag || sacc[e] > -INFINITY ? __builtin_amdgcn_exp2f(sacc[e] - mn) : 0.f;
-                ps += p;
-                const _Float16 hi = (_Float16)p;
-                phi[e / 8][e % 8] = hi;
-                plo[e / 8][e % 8] = (_Float16)(p - (float)hi);
-            }
-            ps += __shfl_xor(ps, 32, 64);
-            l = l * r + ps;
-            m = mn;
-            if (__ballot(r != 1.0f) != 0) {
+        for (int e = 0; e < 16; ++e)
+            o0[e] = 0.f, o1[e] = 0.f;
+        float m = -INFINITY, l = 0.f;
+        uint4 kr, vr;
+        if (nblk > 0) {
+            load_kv(0, kr, vr);
+            store_kv(0, kr, vr);
+        }
+        if (nblk > 1)
+            load_kv(1, kr, vr);
+        __syncthreads();
+        for (uint32_t blk = 0; blk < nblk; ++blk) {
+            const uint32_t buf = blk & 1;
+            if (active) {
+                // S^T[key][query] for the block's 32 keys
+                floatx16a sacc;
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
-                    o0[e] *= r, o1[e] *= r;
+                    sacc[e] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const half8 kf = *reinterpret_cast<const half8 *>(&Ks[buf][lq * FA_KROW + ks * 16 + 8 * lh]);
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[ks], sacc, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, ql[ks], sacc, 0, 0, 0);
+                }
+                // lane's items: keys 8*(e/4) + 4*lh + e%4 of the block, query lq.  A block
+                // that ends before the tile's first query position needs no mask; its
+                // scores are finite, and so is the new maximum.
+                const bool diag = (kb_lo + blk + 1) * FA_K > a.start + t0;
+                float bm = -INFINITY;
+                if (diag) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const uint32_t kpos = (kb_lo + blk) * FA_K + 8 * (e / 4) + 4 * lh + (e % 4);
+                        if (kpos > qpos)
+                            sacc[e] = -INFINITY;
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    bm = fmaxf(bm, sacc[e]);
+                const float2v bh = wave_halves(bm);
+                bm = fmaxf(bh[0], bh[1]);
+                const float mn = fmaxf(m, bm);
+                const float r = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.f;
+                // masked scores are -inf and 2^-inf = 0; a query with no unmasked key
+                // yet (a key range wholly past it) has mn = -inf and subtracts 0
+                const float mz = mn > -INFINITY ? mn : 0.f;
+                float ps = 0.f;
+                half8 phi[2], plo[2];
+#pragma unroll
+                for (int e = 0; e < 16; e += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(sacc[e] - mz), p1 = __builtin_amdgcn_exp2f(sacc[e + 1] - mz);
+                    ps += p0;
+                    ps += p1;
+                    const half2v hp = __builtin_convertvector((float2v){p0, p1}, half2v);
+                    const float2v hb = __builtin_convertvector(hp, float2v);
+                    const half2v lp = __builtin_convertvector((float2v){p0 - hb[0], p1 - hb[1]}, half2v);
+                    phi[e / 8][e % 8] = hp[0];
+                    phi[e / 8][e % 8 + 1] = hp[1];
+                    plo[e / 8][e % 8] = lp[0];
+                    plo[e / 8][e % 8 + 1] = lp[1];
+                }
+                const float2v sh = wave_halves(ps);
+                ps = sh[0] + sh[1];
+                l = l * r + ps;
+                m = mn;
+                if (__ballot(r != 1.0f) != 0) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        o0[e] *= r, o1[e] *= r;
+                }
+                // O^T[dim][query] += V^T[dim][key] P^T[key][query], keys in groups of 16
+#pragma unroll
+                for (int G = 0; G < 2; ++G) {
+                    const half4v a0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 4 * lh]);
+                    const half4v b0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 8 + 4 * lh]);
+                    const half4v a1 = *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 4 * lh]);
+                    const half4v b1 =
+                        *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 8 + 4 * lh]);
+                    const half8 v0 = {a0[0], a0[1], a0[2], a0[3], b0[0], b0[1], b0[2], b0[3]};
+                    const half8 v1 = {a1[0], a1[1], a1[2], a1[3], b1[0], b1[1], b1[2], b1[3]};
+                    o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, phi[G], o0, 0, 0, 0);
+                    o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, plo[G], o0, 0, 0, 0);
+                    o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, phi[G], o1, 0, 0, 0);
+                    o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, plo[G], o1, 0, 0, 0);
+                }
             }
-            // O^T[dim][query] += V^T[dim][key] P^T[key][query], keys in groups of 16
+            if (blk + 1 < nblk)
+                store_kv(buf ^ 1, kr, vr);
+            if (blk + 2 < nblk)
+                load_kv(blk + 2, kr, vr);
+            __syncthreads();
+        }
+        if (active && tq < a.T) {
+            if (a.kb_per) { // this key range's softmax state, merged by k_attn_merge_split
+                float *pp = a.part + (((size_t)blockIdx.z * a.T + tq) * a.heads + h) * 66;
+                if (lh == 0) {
+                    pp[0] = m;
+                    pp[1] = l;
+                }
 #pragma unroll
-            for (int G = 0; G < 2; ++G) {
-                const half4v a0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 4 * lh]);
-                const half4v b0 = *reinterpret_cast<const half4v *>(&Vt[buf][lq * FA_VROW + 16 * G + 8 + 4 * lh]);
-                const half4v a1 = *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 4 * lh]);
-                const half4v b1 =
-                    *reinterpret_cast<const half4v *>(&Vt[buf][(32 + lq) * FA_VROW + 16 * G + 8 + 4 * lh]);
-                const half8 v0 = {a0[0], a0[1], a0[2], a0[3], b0[0], b0[1], b0[2], b0[3]};
-                const half8 v1 = {a1[0], a1[1], a1[2], a1[3], b1[0], b1[1], b1[2], b1[3]};
-                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, phi[G], o0, 0, 0, 0);
-                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, plo[G], o0, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, phi[G], o1, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, plo[G], o1, 0, 0, 0);
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
+                    pp[2 + d] = o0[e];
+                    pp[2 + 32 + d] = o1[e];
+                }
+            } else {
+                const float rl = 1.0f / l;
+                float *orow = a.out + (size_t)tq * dim + h * 64;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
+                    orow[d] = o0[e] * rl;
+                    orow[32 + d] = o1[e] * rl;
+                }
             }
         }
-        if (blk + 1 < nblk)
-            store_kv(buf ^ 1, kr, vr);
-        if (blk + 2 < nblk)
-            load_kv(blk + 2, kr, vr);
-        __syncthreads();
-    }
-    if (!active || tq >= a.T)
-        return;
-    if (a.kb_per) { // this key range's softmax state, merged by k_attn_merge_split
-        float *pp = a.part + (((size_t)blockIdx.z * a.T + tq) * a.heads + h) * 66;
-        if (lh == 0) {
-            pp[0] = m;
-            pp[1] = l;
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
-            pp[2 + d] = o0[e];
-            pp[2 + 32 + d] = o1[e];
-        }
-        return;
-    }
-    const float rl = 1.0f / l;
-    float *orow = a.out + (size_t)tq * dim + h * 64;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const uint32_t d = 8 * (e / 4) + 4 * lh + (e % 4);
-        orow[d] = o0[e] * rl;
-        orow[32 + d] = o1[e] * rl;
-    }
+    } // pass
 }
 
 // Combines the key ranges of a split prefill attention: for (query t, head h),

@@ -99,6 +99,20 @@ template <int N> __device__ __forceinline__ void half_wave_sums(float *v)
         v[i] += dpp_mov<0x142>(v[i], 0.f);
 }
 
+typedef float float2v __attribute__((ext_vector_type(2)));
+// v of lanes 0..31 and of lanes 32..63, each in both wave halves (lane l sees its
+// own value and lane l ^ 32's): one v_permlane32_swap, a VALU lane move (a
+// ds_bpermute shuffle goes through the LDS).  The results are copied out of the
+// returned pair before the bit casts: __builtin_bit_cast of an element of it
+// read element 0 for both.
+__device__ __forceinline__ float2v wave_halves(float v)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const uint32_t lo = r[0], hi = r[1];
+    return {__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi)};
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
     v = fmaxf(v, dpp_mov<0xb1>(v, -INFINITY));
