@@ -856,7 +856,7 @@ int lfm_argmax_enqueue(const float *v, uint32_t n, DevState *st, float *partial,
     RC(get_kernels(&K));
     const uint32_t grid = lfm_argmax_grid(n);
     ArgmaxArgs a{v, partial, n, st};
-    FinalArgs f{partial, grid, nullptr, 0, st};
+    FinalArgs f{partial, grid, nullptr, 0, st, nullptr};
     RC(launch(K->argmax, dim3(grid), 0, s, a));
     return launch(K->argmax_final, dim3(1), 0, s, f);
 }
@@ -946,6 +946,8 @@ struct lfm_engine {
     uint32_t head_grid = 1, nchunk = 1;
     float *rope = nullptr; // [ctx][32] (cos, sin)
     DevState *host_st = nullptr;    // pinned staging for state copies
+    HostResult *host_res = nullptr; // pinned, device-mapped: forward calls' results
+    HostResult *host_res_dev = nullptr; // its device address
     // batched prefill buffers (capacity: ctx tokens per call)
     struct {
         float *x = nullptr, *bcx = nullptr, *y = nullptr, *g = nullptr, *d = nullptr, *part = nullptr;
@@ -1436,17 +1438,19 @@ static int enq_ffn(lfm_engine *e, uint32_t l, bool fuse)
     return LFM_OK;
 }
 
-static int enq_head(lfm_engine *e, uint32_t advance)
+// x: the residual to finish (the decode state's e->x, or a prefill's last row);
+// host: nullable device address of pinned memory that also receives the result.
+static int enq_head(lfm_engine *e, uint32_t advance, const float *x = nullptr, HostResult *host = nullptr)
 {
     HeadArgs h;
     h.emb = q6(e, "token_embd.weight");
-    h.src = xsrc(e->x, f32(e, "token_embd_norm.weight"), e->hp.eps);
+    h.src = xsrc(x ? x : e->x, f32(e, "token_embd_norm.weight"), e->hp.eps);
     h.logits = e->logits;
     h.partial = e->hpart;
     h.vocab = e->hp.vocab;
     h.st = e->st;
     RC(launch_t(e->K->head.fn(), dim3(e->head_grid), e->K->head.threads(), 0, e->stream, h));
-    FinalArgs f{e->hpart, e->head_grid, e->out_tokens, advance, e->st};
+    FinalArgs f{e->hpart, e->head_grid, e->out_tokens, advance, e->st, host};
     RC(launch(e->K->argmax_final, dim3(1), 0, e->stream, f));
     e->dispatches += 2;
     return LFM_OK;
@@ -1576,6 +1580,9 @@ extern "C" int lfm_engine_finalize(lfm_engine *e)
     }
     const size_t swn = std::max<size_t>((size_t)hp.n_ff, (size_t)hp.n_used * hp.expert_ff);
     HIPCHK(hipHostMalloc((void **)&e->host_st, sizeof(DevState), hipHostMallocDefault));
+    // forward calls' results, stored by the last kernel into host memory
+    HIPCHK(hipHostMalloc((void **)&e->host_res, sizeof(HostResult), hipHostMallocCoherent | hipHostMallocMapped));
+    HIPCHK(hipHostGetDevicePointer((void **)&e->host_res_dev, e->host_res, 0));
     HIPCHK(hipHostMalloc((void **)&e->host_ids, (size_t)e->ctx * 4, hipHostMallocDefault));
     HIPCHK(hipMalloc(&e->st, sizeof(DevState)));
     HIPCHK(hipMemset(e->st, 0, sizeof(DevState)));
@@ -1787,6 +1794,8 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
             (void)hipFree(p);
     if (e->host_st)
         (void)hipHostFree(e->host_st);
+    if (e->host_res)
+        (void)hipHostFree(e->host_res);
     if (e->host_ids)
         (void)hipHostFree(e->host_ids);
     for (auto p : e->qkvdev)
@@ -1810,7 +1819,7 @@ extern "C" void lfm_engine_destroy(lfm_engine *e)
 // The multi-token forward (lfm.rs:290-694 with n > 1): every projection is a
 // matrix-core GEMM over the T tokens of the call, the conv is parallel in t,
 // attention is causal over the binary16 cache.  Leaves the last token's
-// residual in e->x (the decode path's residual) for the head.
+// residual in row T - 1 of pf.x, which the head reads.
 // RMSNorm (optional) + binary16 hi / lo split of `rows` activation rows for a
 // GEMM of a T-token call: row-major for large calls, token-blocked for the
 // small-call kernels (T <= GEMM_TOKENS), whose B reads expect that layout.
@@ -2175,15 +2184,30 @@ static int pf_ffn(lfm_engine *e, uint32_t l, float *x, uint32_t T, bool defer_ok
 }
 
 // Runs the layer stack for e->ids[0..T) at positions start.. and leaves the
-// last token's residual in e->x.
-static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
+// last token's residual in row T - 1 of pf.x.
+// ids (nullable, T <= EMBED_INLINE_IDS): the call's ids, passed in the embedding
+// launch's arguments, which also starts the decode state (no copies before it).
+static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start, const uint32_t *ids = nullptr)
 {
     const lfm_hparams &hp = e->hp;
     if (e->route_log)
         std::fill(e->log_n.begin(), e->log_n.end(), 0u);
     e->pf.comb_pending = false;
     e->pf.state_pending = nullptr;
-    EmbedRowsArgs em{q6(e, "token_embd.weight"), e->ids, e->pf.x, T};
+    EmbedRowsArgs em;
+    memset(&em, 0, sizeof(em));
+    em.emb = q6(e, "token_embd.weight");
+    em.ids = e->ids;
+    em.x = e->pf.x;
+    em.T = T;
+    if (ids) {
+        if (T > EMBED_INLINE_IDS)
+            return fail(LFM_EINTERNAL, "prefill: %u inline ids > %u", T, EMBED_INLINE_IDS);
+        em.ids = nullptr;
+        memcpy(em.ids_inline, ids, (size_t)T * 4);
+        em.st = e->st;
+        em.start = start;
+    }
     RC(launch(e->K->embed_rows, dim3((T + 3) / 4), 0, e->stream, em));
     e->dispatches += 1;
     for (uint32_t l = 0; l < hp.n_layers; ++l) {
@@ -2197,9 +2221,7 @@ static int enq_prefill(lfm_engine *e, uint32_t T, uint32_t start)
         return fail(LFM_ESTATE, "prefill: a combine was left pending");
     if (e->pf.state_pending) // cannot happen: every mixer is followed by its FFN's split
         return fail(LFM_ESTATE, "prefill: a conv state was left unmoved");
-    HIPCHK(hipMemcpyAsync(e->x, e->pf.x + (size_t)(T - 1) * hp.dim, hp.dim * 4,
-                          hipMemcpyDeviceToDevice, e->stream));
-    return LFM_OK;
+    return LFM_OK; // the last token's residual is row T - 1 of pf.x
 }
 
 // ------------------------------------------------------------------ forward
@@ -2254,22 +2276,33 @@ static int check_ids(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t st
     return LFM_OK;
 }
 
-// Layers for every id (graph replays), then the head without feedback.
+static_assert(LFM_MAX_TOKEN_BATCH <= EMBED_INLINE_IDS, "forward_token batches fit the embedding launch's ids");
+
+// Layers for every id (graph replays), then the head without feedback; the
+// result also goes to the pinned e->host_res.
 static int run_prompt(lfm_engine *e, const uint32_t *ids, uint32_t n, uint32_t start)
 {
     RC(check_ids(e, ids, n, start));
-    RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu)); // also waits for prior use of host_ids
-    memcpy(e->host_ids, ids, (size_t)n * 4);
-    HIPCHK(hipMemcpyAsync(e->ids, e->host_ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
-    if (n >= 2 && !e->stepwise_prefill) {
-        RC(enq_prefill(e, n, start)); // matrix-core path
+    e->host_res->token = ~0u; // every earlier call has synchronized: no kernel writes it now
+    const bool prefill = n >= 2 && !e->stepwise_prefill;
+    if (prefill && n <= EMBED_INLINE_IDS) {
+        // forward_token batches: the ids travel in the embedding launch's arguments,
+        // which also starts the decode state (no copies ahead of the first kernel)
+        RC(enq_prefill(e, n, start, ids));
     } else {
-        for (uint32_t j = 0; j < n; ++j) { // one captured decode step per token
-            HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
-            e->dispatches += e->nodes_layers;
+        RC(set_state(e, ids[0], start, n, 0xFFFFFFFFu)); // also waits for prior use of host_ids
+        memcpy(e->host_ids, ids, (size_t)n * 4);
+        HIPCHK(hipMemcpyAsync(e->ids, e->host_ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+        if (prefill) {
+            RC(enq_prefill(e, n, start)); // matrix-core path
+        } else {
+            for (uint32_t j = 0; j < n; ++j) { // one captured decode step per token
+                HIPCHK(hipGraphLaunch(e->g_layers, e->stream));
+                e->dispatches += e->nodes_layers;
+            }
         }
     }
-    RC(enq_head(e, 0));
+    RC(enq_head(e, 0, prefill ? e->pf.x + (size_t)(n - 1) * e->hp.dim : e->x, e->host_res_dev));
     return LFM_OK;
 }
 
@@ -2295,11 +2328,22 @@ extern "C" int lfm_forward_token(lfm_engine *e, const uint32_t *ids, uint32_t n,
     if (!next)
         return fail(LFM_EINVAL, "next is null");
     RC(run_prompt(e, ids, n, start));
-    DevState h;
-    RC(read_state(e, &h));
-    *next = h.last_token;
+    HIPCHK(hipStreamSynchronize(e->stream));
+    const HostResult r = *e->host_res; // written by k_argmax_final (no copy back)
+    if (r.token == ~0u) // not stored (a halted state): the state copy has the result
+    {
+        DevState h;
+        RC(read_state(e, &h));
+        *next = h.last_token;
+        if (max_logit)
+            *max_logit = h.last_value;
+        return LFM_OK;
+    }
+    if (r.fault)
+        return fail(LFM_EDEVICE, "a fused decode kernel's handoff wait timed out (workgroups not co-resident)");
+    *next = r.token;
     if (max_logit)
-        *max_logit = h.last_value;
+        *max_logit = r.value;
     return LFM_OK;
 }
 

@@ -182,12 +182,23 @@ struct ArgmaxArgs {      // per-workgroup argmax partials of a plain vector
     DevState *st;
 };
 
+// A forward call's result, stored by k_argmax_final straight into pinned host
+// memory (read once the stream has synchronized: no copy back).  token is
+// ~0u until the kernel has written it.
+struct HostResult {
+    uint32_t token;
+    float value;
+    uint32_t fault; // DevState::fault when the result was stored
+    uint32_t pad;
+};
+
 struct FinalArgs {       // reduce partials; decode step: store, feed back, advance
     const float *partial;
     uint32_t n_partial;
     uint32_t *out_tokens;
     uint32_t advance;
     DevState *st;
+    HostResult *host;    // nullable: also store the result here (device address of pinned memory)
 };
 
 struct AdvanceArgs {
@@ -487,11 +498,18 @@ struct CombinePrefillArgs {  // x[t] += sum_r w[t][r] * D[t*4 + r] (rank order)
     uint32_t T, dim, n_used;
 };
 
+#define EMBED_INLINE_IDS 64 // forward_token's batch limit
 struct EmbedRowsArgs {
     Q6T emb;
-    const uint32_t *ids;  // [T]
+    const uint32_t *ids;  // [T]; null: ids_inline (T <= EMBED_INLINE_IDS)
     float *x;             // [T][dim]
     uint32_t T;
+    // nullable: workgroup 0 also starts the call's decode state (the host's
+    // set_state without a copy): tok = the first id, pos = start, eos = ~0u,
+    // n_ids = T, the other fields but gen zero
+    DevState *st;
+    uint32_t start;
+    uint32_t ids_inline[EMBED_INLINE_IDS];
 };
 
 // The short-conv mixer of one layer in one launch (k_conv_mixer, k_conv_mixer_r):

@@ -1481,6 +1481,11 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_argmax_final(const Fi
         st->last_token = bi;
         st->last_value = bv;
         st->gen = st->gen + 1;
+        if (a.host) {
+            a.host->value = bv;
+            a.host->fault = st->fault;
+            a.host->token = bi;
+        }
         if (a.advance) {
             if (bi == st->eos) {
                 st->halt = 1;

@@ -2542,9 +2542,25 @@ extern "C" __global__ __launch_bounds__(WG_THREADS) void k_reduce_combine(const 
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_embed_rows(const EmbedRowsArgs a)
 {
     const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (a.st && blockIdx.x == 0 && threadIdx.x == 0) { // uniform per workgroup
+        DevState *st = a.st;
+        st->tok = a.ids ? a.ids[0] : a.ids_inline[0];
+        st->pos = a.start;
+        st->halt = 0;
+        st->step = 0;
+        st->eos = ~0u;
+        st->cursor = 0;
+        st->n_ids = a.T;
+        st->last_token = 0;
+        st->last_value = 0.f;
+        st->fault = 0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i)
+            st->pad[i] = 0;
+    }
     if (t >= a.T)
         return;
-    const uint32_t tok = a.ids[t];
+    const uint32_t tok = a.ids ? a.ids[t] : a.ids_inline[t];
     for (uint32_t u = lane; u < a.emb.nb * 8; u += 64) {
         const uint32_t b = u >> 3, c = u & 7;
         float v[32];
