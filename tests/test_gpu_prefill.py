@@ -258,3 +258,37 @@ def test_prefill_h16_copy_matches_q6_decode(gpu, real_width, monkeypatch):
     q.close()
     assert np.array_equal(lg.view(np.uint32), lq.view(np.uint32))
     assert sg == sq
+
+
+def test_forward_token_after_halted_decode(gpu, real_width):
+    """A multi-token forward_token starts the decode state in its embedding launch
+    (the ids travel in the launch's arguments, no state copy) and returns its
+    result from pinned host memory: after a decode run that halted at its EOS
+    token, the same call gives the same token and maximum logit, bit for bit, as
+    on a fresh state, and so do the one-token call (decode graph) and the logits
+    path."""
+    hp, tensors = real_width
+    g = gpu_engine(hp, tensors, ctx=512)
+    prompt = [int(t) for t in np.random.default_rng(64).integers(0, hp.vocab, 64)]
+    tok = g.forward_token(prompt, 0)
+    val = g.last_max_logit
+    first = g.decode_run(tok, 64, 2)
+    assert len(first) == 2
+    g.reset_session()
+    one = g.forward_token(prompt[:1], 0)
+    one_val = g.last_max_logit
+    for _ in range(2):
+        # halt: EOS is the token this continuation generates first
+        g.reset_session()
+        assert g.forward_token(prompt, 0) == tok
+        assert g.decode_run(tok, 64, 4, eos=first[0]) == []
+        g.reset_session()
+        assert g.forward_token(prompt, 0) == tok
+        assert np.float32(g.last_max_logit).tobytes() == np.float32(val).tobytes()
+        assert g.decode_run(tok, 64, 4, eos=first[0]) == []
+        g.reset_session()
+        assert g.forward_token(prompt[:1], 0) == one
+        assert np.float32(g.last_max_logit).tobytes() == np.float32(one_val).tobytes()
+    g.reset_session()
+    lg = g.forward(prompt, 0)
+    assert int(np.argmax(lg)) == tok and np.float32(lg.max()).tobytes() == np.float32(val).tobytes()
