@@ -38,8 +38,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense binary16 matrix-core peak
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 KiB per dispatch; the scales are what the two
 # counters read for a plain 512 MiB copy), and the SHA-256 of the decode code object
 # those passes ran: the figure is reported only for that same code object.
-GATEUP_TRAFFIC_BYTES = 24579566
-GATEUP_TRAFFIC_CODE_OBJECT = "8811cb1f1cca27291a5f24a1697419fe636acd2f16ea651118f6e10bf9b570ce"
+GATEUP_TRAFFIC_BYTES = 24579564
+GATEUP_TRAFFIC_CODE_OBJECT = "03d8e3b9b411c98add4de5827727c985eec1ff7da8579b7fe648957e4cd8471c"
 SEED = 0x9E3779B97F4A7C15
 CTX = 4096          # context of the workload (positions 0..4095)
 N_PROMPT = 3840     # prompt tokens prefilled before decode
