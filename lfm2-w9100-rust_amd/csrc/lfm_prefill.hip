@@ -1708,7 +1708,8 @@ __device__ __forceinline__ void gemm_small_body(const GemmArgs &a)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
             m = fmaxf(m, fabsf(v[e]));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        const float2v mh = wave_halves(m);
+        m = fmaxf(mh[0], mh[1]);
         __shared__ float cmax[4][32];
         if (p == 0)
             cmax[wave][lr] = m;
