@@ -84,9 +84,22 @@ __device__ __forceinline__ void slice_sums(const float *p, size_t step, uint32_t
 // matching pieces nw of the norm weight when a.norm_w is set, split into hi / lo of
 // v / scale (scale[t] written): into row t (SPLIT_ROWMAJOR) or into the nl logical
 // rows L[j] of the token-blocked layout.
-__device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8],
-                                             const float (&nw)[SPLIT_NP][8], const uint32_t *L, uint32_t nl)
+// The workgroup barriers of the split wait only for LDS: a routing wave's list
+// atomics (route_self) stay in flight across them.
+__device__ __forceinline__ void split_barrier()
 {
+    __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// first() runs before the reductions; rows(L) fills the logical rows L[0..n) and
+// returns n, after them, just before the stores.
+template <typename Mid, typename Rows>
+__device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, float (&v)[SPLIT_NP][8],
+                                             const float (&nw)[SPLIT_NP][8], Mid &&first, Rows &&rows)
+{
+    first();
     const uint32_t tid = threadIdx.x, npc = a.K >> 3;
     __shared__ float red[4], redm[4];
     if (a.norm_w) { // uniform
@@ -99,7 +112,7 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
         ss = wave_sum(ss);
         if ((tid & 63) == 0)
             red[tid >> 6] = ss;
-        __syncthreads();
+        split_barrier();
         const float tot = ((red[0] + red[1]) + red[2]) + red[3];
         const float inv = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
@@ -121,7 +134,7 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
     amax = wave_max(amax);
     if ((tid & 63) == 0)
         redm[tid >> 6] = amax;
-    __syncthreads();
+    split_barrier();
     amax = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
     int e = 0;
     if (amax > 0.f && amax <= 3.0e38f)
@@ -129,6 +142,8 @@ __device__ __forceinline__ void split_pieces(const SplitArgs &a, uint32_t t, flo
     const float scale = amax > 0.f ? ldexpf(1.0f, e - 14) : 1.0f, rs = 1.0f / scale;
     if (tid == 0)
         a.scale[t] = scale;
+    uint32_t L[4];
+    const uint32_t nl = rows(L);
     if (a.bscale && a.mode != SPLIT_ROWMAJOR) { // uniform
         const uint32_t nh = a.K >> 7;
         for (uint32_t q = 0; q < nl; ++q) // uniform
@@ -276,12 +291,29 @@ __device__ __forceinline__ uint32_t route_rows(const SplitArgs &a, uint32_t t, u
 // EXT: the small calls' extra duties (a pending combine, the expert lists), in a
 // kernel of their own so that the plain split keeps its registers.
 // Routes token t in wave 0 (as k_route_topk does from the router partials) and
-// takes list indexes for its slots by atomic adds on counts; returns the logical
-// rows of its slots as route_rows does.
-__device__ __forceinline__ uint32_t route_self(const SplitArgs &a, uint32_t t, uint32_t (&L)[4])
+// takes list indexes for its slots by atomic adds on counts: the picks go to
+// ids[] at once, the atomics' results (pr, lanes < n_used of wave 0) are used
+// only by route_self_rows, after the split's reductions, so that their round trip
+// overlaps them.
+// (wave 0: the loads of its router partial sums, issued with the row's)
+__device__ __forceinline__ void route_self_load(const SplitArgs &a, uint32_t t, float (&dp)[8], float (&sp)[8])
 {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
-    __shared__ uint32_t ids[4], pos[4];
+    if (tid < 64) { // wave 0
+        const uint32_t e = min(lane, a.n_expert - 1);
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint32_t bb = min((uint32_t)b, a.nparts - 1);
+            dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
+            sp[b] = a.rss[(size_t)t * a.nparts + bb];
+        }
+    }
+}
+__device__ __forceinline__ uint32_t route_self_issue(const SplitArgs &a, uint32_t t, const float (&dp)[8],
+                                                     const float (&sp)[8], uint32_t *ids)
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    uint32_t pr = 0;
     if (tid < 64) { // wave 0
         Route r;
         r.logits = nullptr;
@@ -290,13 +322,6 @@ __device__ __forceinline__ uint32_t route_self(const SplitArgs &a, uint32_t t, u
         r.n_used = a.n_used;
         r.sel_out = nullptr;
         const uint32_t e = min(lane, a.n_expert - 1);
-        float dp[8], sp[8];
-#pragma unroll
-        for (int b = 0; b < 8; ++b) {
-            const uint32_t bb = min((uint32_t)b, a.nparts - 1);
-            dp[b] = a.rpart[((size_t)t * a.nparts + bb) * a.n_expert + e];
-            sp[b] = a.rss[(size_t)t * a.nparts + bb];
-        }
         float dot = 0.f, ss = 0.f;
 #pragma unroll
         for (int b = 0; b < 8; ++b)
@@ -313,14 +338,24 @@ __device__ __forceinline__ uint32_t route_self(const SplitArgs &a, uint32_t t, u
             a.sel_out[(size_t)t * 4 + lane] = id;
             a.wsel_out[(size_t)t * 4 + lane] = lane < a.n_used ? rt.w(lane) : 0.f;
             ids[lane] = id;
-            if (lane < a.n_used) {
-                const uint32_t pr = atomicAdd(&a.counts[id], 1u);
-                pos[lane] = pr;
-                a.tok[(size_t)id * a.list_stride + pr] = t;
-                a.slot[(size_t)id * a.list_stride + pr] = t * 4 + lane;
-                a.pos[(size_t)t * 4 + lane] = pr;
-            }
+            if (lane < a.n_used)
+                pr = atomicAdd(&a.counts[id], 1u);
         }
+    }
+    return pr;
+}
+
+// The list entries of the routed slots and their logical rows L (route_self_issue).
+__device__ __forceinline__ uint32_t route_self_rows(const SplitArgs &a, uint32_t t, const uint32_t *ids,
+                                                    uint32_t *pos, uint32_t pr, uint32_t (&L)[4])
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64 && lane < a.n_used) {
+        const uint32_t id = ids[lane];
+        pos[lane] = pr;
+        a.tok[(size_t)id * a.list_stride + pr] = t;
+        a.slot[(size_t)id * a.list_stride + pr] = t * 4 + lane;
+        a.pos[(size_t)t * 4 + lane] = pr;
     }
     __syncthreads();
 #pragma unroll
@@ -359,10 +394,27 @@ __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
             reinterpret_cast<float4 *>(a.copy_dst)[u] = reinterpret_cast<const float4 *>(a.copy_src)[u];
     if (EXT && a.cpart) // uniform
         combine_pieces(a, t, v);
-    uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
     if (EXT && a.mode == SPLIT_GROUPED && a.tok && a.rpart) { // uniform
-        nl = route_self(a, t, L);
-    } else if (EXT && a.mode == SPLIT_GROUPED && a.tok) { // uniform
+        // the partial sums' loads go out with the row's, the picks and the list
+        // atomics before the split's reductions, the list entries after them: the
+        // atomics' round trip overlaps the reductions
+        __shared__ uint32_t rids[4], rpos[4];
+        float dp[8], sp[8];
+        route_self_load(a, t, dp, sp);
+        uint32_t pr = 0;
+        split_pieces(
+            a, t, v, nw,
+            [&]() {
+                // the row's loads (and the partial sums) complete here, so that the
+                // reductions' uses of the row wait for nothing issued later
+                __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+                pr = route_self_issue(a, t, dp, sp, rids);
+            },
+            [&](uint32_t (&L)[4]) { return route_self_rows(a, t, rids, rpos, pr, L); });
+        return;
+    }
+    uint32_t L[4] = {t, 0, 0, 0}, nl = 1;
+    if (EXT && a.mode == SPLIT_GROUPED && a.tok) { // uniform
         nl = route_rows(a, t, L);
     } else if (a.mode == SPLIT_GROUPED) { // uniform
         nl = 0;
@@ -372,7 +424,12 @@ __device__ __forceinline__ void split_rows_body(const SplitArgs &a, uint32_t t)
                 L[nl++] = a.sel[s] * a.rpe + a.pos[s];
         }
     }
-    split_pieces(a, t, v, nw, L, nl);
+    split_pieces(a, t, v, nw, []() {}, [&](uint32_t (&Lo)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            Lo[i] = L[i];
+        return nl;
+    });
 }
 
 extern "C" __global__ __launch_bounds__(WG_THREADS) void k_split_rows(const SplitArgs a)
